@@ -1,0 +1,230 @@
+"""Benchmark of the W8A8 INT8 linear path on one MI355X.
+
+Default workload (one step): the DiT FFN block of the FP16-fix flow at
+M=16384 tokens, hidden 3072, FFN 8192:
+  1. FC1 input: ConvRot256 + per-row INT8 quantization of h [16384, 3072]
+  2. FC1: INT8 GEMM 3072 -> 2x8192 (gate|up), column-order epilogue, FP16 out
+  3. FC2 prologue: FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8 [16384, 8192]
+  4. FC2: INT8 GEMM 8192 -> 3072, row-order epilogue with the /512-folded
+     weight scale and the FP16 residual add
+Inputs and weights are seeded synthetic tensors already resident in HBM.
+
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+
+Prints one JSON line: INT8 TOPS of the whole block, ms per step, the
+roofline of the dominant kernel (the FC1 GEMM, timed with HIP events on the
+launch stream), per-kernel times, and the CPU oracle timed on a bounded row
+sample of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / 'minimax-h3-2xt4_amd')):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = 'INT8 GEMM TOPS & % of MI355X i8 MFMA peak; DiT FFN block µs at M=16384'
+PEAK_INT8_TOPS = 5000.0
+PEAK_HBM_GBS = 8000.0
+
+
+def cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def blas_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        n = [i['num_threads'] for i in threadpool_info() if i.get('user_api') == 'blas']
+        if n:
+            return max(n)
+    except Exception:
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+class KernelTimer:
+    """Per-launch HIP events on the current (launch) stream."""
+
+    def __init__(self, torch, names, steps):
+        self.torch = torch
+        self.names = names
+        self.events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(steps)]
+
+    def mark(self, step, i):
+        self.events[step][i].record()
+
+    def averages_ms(self):
+        sums = [0.0] * len(self.names)
+        for ev in self.events:
+            for i in range(len(self.names)):
+                sums[i] += ev[i].elapsed_time(ev[i + 1])
+        return {n: s / len(self.events) for n, s in zip(self.names, sums)}
+
+
+def run_dit_ffn(args, torch, dev):
+    from w8a8 import kernels, workloads
+    from w8a8.h3_tensor_flow import TensorFlowPolicy, prepare_tp
+    from w8a8.tp_dit import DiTFeedForwardINT8
+
+    m, hidden, ffn = 16384, 3072, 8192
+    data = workloads.dit_ffn(m=m, hidden=hidden, ffn=ffn)
+    block = DiTFeedForwardINT8(hidden, ffn, device=dev)
+    q1, s1 = workloads.quantize_weight(data['w1'], dev)
+    q2, s2 = workloads.quantize_weight(data['w2'], dev)
+    block.fc1.weight.data.copy_(q1)
+    block.fc1.weight_scale.data.copy_(s1)
+    block.fc2.weight.data.copy_(q2)
+    block.fc2.weight_scale.data.copy_(s2)
+    prepare_tp(block, 'dit', TensorFlowPolicy(mode='fp16'))
+    w1, ws1 = block.fc1.weight, block.fc1.weight_scale
+    w2, ws2 = block.fc2.weight, block.fc2.weight_scale
+    h = data['h'].to(dev)
+    res = data['residual'].to(dev)
+
+    names = ('fc1_quantize', 'fc1_gemm', 'fc2_prologue', 'fc2_gemm')
+
+    def step(timer=None, i=0):
+        # The same library calls DiTFeedForwardINT8.forward makes.
+        mark = (lambda j: timer.mark(i, j)) if timer else (lambda j: None)
+        mark(0)
+        qa, a = kernels.quantize_rows(h, convrot=True, round_rotated=True)
+        mark(1)
+        y1 = kernels.gemm(qa, w1, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=ws1, out_dtype=torch.float16)
+        mark(2)
+        p = kernels.swiglu_quantize(y1)
+        mark(3)
+        out = kernels.gemm(p['q'], w2, epilogue=kernels.EPI_ROW, row_scale=p['scale'], col_scale=ws2,
+                           out_dtype=torch.float16, residual=res)
+        mark(4)
+        return out
+
+    # The timed sequence is the module's forward, bit for bit.
+    ref = block(h, res)
+    if not torch.equal(step(), ref):
+        raise RuntimeError('bench step differs from DiTFeedForwardINT8.forward')
+    del ref
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = KernelTimer(torch, names, args.steps)
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        step(timer, i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = start.elapsed_time(stop) / args.steps
+    kms = timer.averages_ms()
+
+    ops_fc1 = 2.0 * m * (2 * ffn) * hidden
+    ops_fc2 = 2.0 * m * hidden * ffn
+    bytes_q1 = m * hidden * 2 + m * hidden + 4 * m
+    bytes_pro = m * 2 * ffn * 2 + m * ffn + 4 * m
+    kernels_out = {
+        'fc1_quantize': dict(us=kms['fc1_quantize'] * 1e3, gbs=bytes_q1 / (kms['fc1_quantize'] * 1e-3) / 1e9),
+        'fc1_gemm': dict(us=kms['fc1_gemm'] * 1e3, tops=ops_fc1 / (kms['fc1_gemm'] * 1e-3) / 1e12),
+        'fc2_prologue': dict(us=kms['fc2_prologue'] * 1e3, gbs=bytes_pro / (kms['fc2_prologue'] * 1e-3) / 1e9),
+        'fc2_gemm': dict(us=kms['fc2_gemm'] * 1e3, tops=ops_fc2 / (kms['fc2_gemm'] * 1e-3) / 1e12),
+    }
+    for v in kernels_out.values():
+        if 'tops' in v:
+            v['frac'] = v['tops'] / PEAK_INT8_TOPS
+        else:
+            v['frac'] = v['gbs'] / PEAK_HBM_GBS
+    fc1 = kernels_out['fc1_gemm']
+    roofline = dict(bound='mfma', achieved=round(fc1['tops'], 1), peak=PEAK_INT8_TOPS, unit='TOPS',
+                    frac=round(fc1['frac'], 4), traffic=None, kernel='gemm_i8_256x256 (FC1 16384x16384x3072)',
+                    algorithmic=f'{ops_fc1:.4g} int8 ops per launch (2*M*N*K)')
+    tops = (ops_fc1 + ops_fc2) / (ms * 1e-3) / 1e12
+    result = dict(metric=METRIC, value=round(tops, 1), unit='TOPS', n_gpus=1, steps=args.steps,
+                  warmup=args.warmup, ms_per_step=round(ms, 4), higher_is_better=True, scaling='weak',
+                  vs_baseline=None, dtype='int8', data='synthetic (seeded N(0,1) activations with x20 outlier '
+                  'channels, N(0,0.02) weights quantized per channel)',
+                  config=dict(workload='dit_ffn_block', m=m, hidden=hidden, ffn=ffn,
+                              fc1='3072->2x8192 column, ConvRot256 input, fp16 out',
+                              fc2='8192->3072 row, fused SwiGLU+ConvRot256 prologue, /512 scale, fp16 residual'),
+                  block_us=round(ms * 1e3, 1), wall_ms_per_step=round(wall_ms, 4),
+                  mfma_peak_frac=round(tops / PEAK_INT8_TOPS, 4),
+                  kernels={k: {kk: round(vv, 4 if kk == 'frac' else 1) for kk, vv in v.items()}
+                           for k, v in kernels_out.items()},
+                  roofline=roofline)
+    if not args.no_cpu_baseline:
+        result['cpu_baseline'] = cpu_baseline_ffn(args, data, block, m, ops_fc1 + ops_fc2)
+    return result
+
+
+def cpu_baseline_ffn(args, data, block, m, ops_block):
+    """The CPU oracle (numpy, float64 BLAS for the exact INT32 GEMM) on a row
+    sample of the same block, extrapolated linearly in rows (rows are
+    independent under per-row scales)."""
+    import numpy as np
+
+    import oracle as o
+    rows = args.cpu_rows
+    w1 = block.fc1.weight.detach().cpu().numpy()
+    w2 = block.fc2.weight.detach().cpu().numpy()
+    s1 = block.fc1.weight_scale.detach().cpu().numpy().reshape(-1)
+    s2 = block.fc2.weight_scale.detach().cpu().numpy().reshape(-1)
+    w1f = w1.astype(np.float64)
+    w2f = w2.astype(np.float64)
+    h = data['h'][:rows].numpy()
+    r = data['residual'][:rows].numpy()
+    times = []
+    for rep in range(4):     # one warm-up, three timed
+        t0 = time.perf_counter()
+        o.ffn_block(h, w1, s1, w2, s2, r, w1_f64=w1f, w2_f64=w2f)
+        if rep:
+            times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    full_s = t * m / rows
+    return dict(value=round(ops_block / full_s / 1e12, 4), unit='TOPS', cores=blas_threads(), kind='port',
+                sample=f'oracle DiT FFN block on {rows} of {m} rows (median of 3 after 1 warm-up, '
+                       f'{t:.2f} s), extrapolated x{m // rows} to {full_s * 1e6:.0f} us per block; '
+                       f'numpy float64 BLAS for the exact int32 GEMM; CPU: {cpu_model()}')
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=10)
+    ap.add_argument('--workload', default='dit_ffn', choices=sorted(WORKLOADS))
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--cpu-rows', type=int, default=256)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py: this W8A8 path runs on one GPU; --gpus {args.gpus} is not supported '
+              '(multi-GPU sharding is a design note, not part of this build)', file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print('bench.py: no GPU visible', file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device('cuda', 0)
+    from w8a8 import _abi
+    _abi.load()
+    result = WORKLOADS[args.workload](args, torch, dev)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,219 @@
+/*
+ * w8a8.h - C ABI of the MI355X (gfx950) W8A8 INT8 linear path.
+ *
+ * Plain C: fixed-width integers, raw device pointers, an opaque stream
+ * handle (a hipStream_t passed as void*). No torch types. Every entry point
+ * takes a pointer to an argument struct whose first field is the struct size
+ * (checked against sizeof, like the reference's AttentionArgs static_assert,
+ * patches/kitchen_attention_native/attention.cu:5-18,79), validates shapes,
+ * strides and alignment before launching, enqueues work on the caller's
+ * stream without synchronising, and returns a w8a8_status code
+ * (the reference's native entry returns a cudaError_t, attention.cu:79-101).
+ *
+ * The caller owns and allocates every input, output and workspace buffer;
+ * the library allocates no device memory and keeps no state beyond a
+ * per-thread error message. Calls on different streams may run concurrently.
+ *
+ * Numerics (all float ops are IEEE binary32 round-to-nearest-even, no FMA
+ * contraction):
+ *   quantize:  s = max(amax * fp32(1/127), fp32(1e-30)),
+ *              q = clamp(rne(x / s), -128, 127)         (IEEE division)
+ *   ConvRot256: per 256-column group, four radix-4 stages (strides 1,4,16,64)
+ *              of the regular H4 butterfly ((p+q)+r)+s, then * fp32(1/16)
+ *   GEMM:      C[m][n] = sum_k A[m][k] * B[n][k]  (int32, exact)
+ *   ROW epilogue:    y = (f32(C) * a[m]) * w[n]   [+ f32(bias[n])]
+ *   COLUMN epilogue: y = f32(C) * (a[m] * w[n])   [+ f32(bias[n])]
+ *   residual:  out = f16(f32(res[m][n]) + f32(f16(y)))
+ */
+#ifndef W8A8_H
+#define W8A8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W8A8_ABI_VERSION 1
+
+typedef enum w8a8_status {
+  W8A8_OK = 0,
+  W8A8_ERR_INVALID = 1,     /* bad pointer, shape, stride, alignment or size */
+  W8A8_ERR_UNSUPPORTED = 2, /* valid request outside what the kernels cover */
+  W8A8_ERR_LAUNCH = 3       /* the HIP runtime refused a launch */
+} w8a8_status;
+
+typedef enum w8a8_dtype {
+  W8A8_F16 = 1,
+  W8A8_BF16 = 2,
+  W8A8_F32 = 3,
+  W8A8_I32 = 4,
+  W8A8_I8 = 5
+} w8a8_dtype;
+
+typedef enum w8a8_epilogue {
+  W8A8_EPI_INT32 = 0,  /* raw int32 accumulators */
+  W8A8_EPI_ROW = 1,    /* (C * a) * w, parallel_int8.dequantize order */
+  W8A8_EPI_COLUMN = 2  /* C * (a * w), column epilogue order */
+} w8a8_epilogue;
+
+/*
+ * Dynamic per-row absmax quantization, optionally after ConvRot256.
+ * Replaces: patches/parallel_int8.py:26-43 (quantize),
+ *           patches/dit_column_linear.py:13-21 (_prepare_activation),
+ *           patches/tilelang_row_quant.py:26-46,81-86 (quantizer with an
+ *           external row maximum).
+ * x: [rows, cols] of x_dtype (F16, BF16, F32), row stride ldx elements.
+ * convrot: 0 (none) or 256 (ConvRot256 before the absmax).
+ * round_rotated: with convrot, 1 rounds the rotated values to x_dtype before
+ *   the absmax (the column path's rotation returns a tensor of x's dtype,
+ *   patches/dit_column_linear.py:18-19); 0 keeps them in FP32 (the fused
+ *   rotate-and-quantize route of patches/parallel_int8.py:32-36).
+ * row_max: optional [rows] external absmax (e.g. a global maximum over
+ *   tensor-parallel owners); NULL computes the row's own absmax.
+ * q: [rows, cols] int8, row stride ldq. scale: [rows] fp32.
+ * Requirements: cols % 16 == 0 (cols % 256 == 0 with convrot), x, q 16-byte
+ *   aligned, ldx * elem and ldq multiples of 16 bytes.
+ */
+typedef struct W8A8QuantArgs {
+  uint32_t struct_size;
+  int32_t x_dtype;
+  const void* x;
+  int64_t ldx;
+  int64_t rows;
+  int64_t cols;
+  int32_t convrot;
+  int32_t round_rotated;
+  const float* row_max;
+  int8_t* q;
+  int64_t ldq;
+  float* scale;
+  void* stream;
+} W8A8QuantArgs;
+
+int w8a8_quantize_rows(const W8A8QuantArgs* args);
+
+/*
+ * FC2 prologue: FP32 SwiGLU -> ConvRot256 -> row absmax -> quantize, fused,
+ * with no FP32 round trip through memory.
+ * Replaces: patches/tilelang_swiglu_quant.py:11-64 (fused_kernel, phases
+ *           stored / maximum / recompute), :67-92 (prepare, fused_stored),
+ *           patches/tilelang_row_quant.py:26-46 (external-max quantizer).
+ * x: [rows, 2*width] of x_dtype (F16 or F32): gate in columns [0, width),
+ *   up in [width, 2*width); row stride ldx elements. width % 256 == 0.
+ * Per element: a = (g / (1 + exp(-g))) * u in FP32 (exp is this library's
+ *   own correctly-rounded-to-about-1-ulp Cody-Waite/Cephes evaluation).
+ * row_max: optional [rows] external (global) absmax of the rotated values.
+ * row_max_out: optional [rows] output of the local absmax.
+ * group_max: optional [rows, width/256] output of per-group absmax.
+ * q: [rows, width] int8 (row stride ldq) or NULL (maximum phase only).
+ * scale: [rows] fp32 (required when q is non-NULL).
+ */
+typedef struct W8A8SwigluArgs {
+  uint32_t struct_size;
+  int32_t x_dtype;
+  const void* x;
+  int64_t ldx;
+  int64_t rows;
+  int64_t width;
+  const float* row_max;
+  float* row_max_out;
+  float* group_max;
+  int8_t* q;
+  int64_t ldq;
+  float* scale;
+  void* stream;
+} W8A8SwigluArgs;
+
+int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
+
+/*
+ * INT8 GEMM on gfx950 i8 MFMA with a fused epilogue.
+ * Replaces: patches/parallel_int8.py:46-50 (int_mm),
+ *           patches/optimized_tp.py:34-43 (native_int_mm),
+ *           patches/dit_column_linear.py:51-57 (_column_accumulate)
+ *   fused with patches/parallel_int8.py:53-69 (dequantize, ROW order),
+ *   patches/tilelang_column_epilogue.py:10-40 (COLUMN order) and
+ *   patches/h3_tensor_flow.py:130-131 (residual_add).
+ * a: [m, k] int8 activations (row stride lda); b: [n, k] int8 weights
+ *   (row stride ldb) - both K-contiguous ("TN").
+ * row_scale: [m] fp32; col_scale: [n] fp32 with col_scale_stride 1, or a
+ *   scalar with stride 0. Unused for W8A8_EPI_INT32.
+ * bias: optional [n] of bias_dtype (F16 or F32), added after the products.
+ * residual: optional [m, n] F16 (row stride ldr); requires out_dtype F16.
+ *   May alias out (in-place residual update).
+ * out: [m, n] of out_dtype (I32 for EPI_INT32; F16, BF16 or F32 otherwise),
+ *   row stride ldc.
+ * Requirements: k % 16 == 0; a, b 16-byte aligned; lda, ldb % 16 == 0;
+ *   out 16-byte aligned; ldc % 4 == 0.
+ */
+typedef struct W8A8GemmArgs {
+  uint32_t struct_size;
+  int32_t epilogue;
+  const int8_t* a;
+  int64_t lda;
+  const int8_t* b;
+  int64_t ldb;
+  int64_t m;
+  int64_t n;
+  int64_t k;
+  const float* row_scale;
+  const float* col_scale;
+  int64_t col_scale_stride;
+  const void* bias;
+  int32_t bias_dtype;
+  int32_t out_dtype;
+  const void* residual;
+  int64_t ldr;
+  void* out;
+  int64_t ldc;
+  void* stream;
+} W8A8GemmArgs;
+
+int w8a8_gemm(const W8A8GemmArgs* args);
+
+/*
+ * Standalone dequantization of an int32 accumulator (the epilogue of
+ * w8a8_gemm without the GEMM).
+ * Replaces: patches/parallel_int8.py:53-69 (dequantize),
+ *           patches/tilelang_column_epilogue.py:10-40 (dequantize),
+ *           patches/dit_column_linear.py:24-37 (_dequantize_eager).
+ * acc: [m, n] int32, row stride ldacc. Other fields as in W8A8GemmArgs.
+ */
+typedef struct W8A8DequantArgs {
+  uint32_t struct_size;
+  int32_t epilogue;   /* W8A8_EPI_ROW or W8A8_EPI_COLUMN */
+  const int32_t* acc;
+  int64_t ldacc;
+  int64_t m;
+  int64_t n;
+  const float* row_scale;
+  const float* col_scale;
+  int64_t col_scale_stride;
+  const void* bias;
+  int32_t bias_dtype;
+  int32_t out_dtype;
+  const void* residual;
+  int64_t ldr;
+  void* out;
+  int64_t ldc;
+  void* stream;
+} W8A8DequantArgs;
+
+int w8a8_dequantize(const W8A8DequantArgs* args);
+
+/* ABI version (W8A8_ABI_VERSION). */
+int w8a8_abi_version(void);
+
+/* sizeof of each argument struct, by index: 0 Quant, 1 Swiglu, 2 Gemm,
+ * 3 Dequant; -1 for an unknown index. Lets bindings verify their layout. */
+int64_t w8a8_struct_size(int32_t which);
+
+/* Message describing the last error returned on the calling thread. */
+const char* w8a8_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W8A8_H */

@@ -1,0 +1,77 @@
+"""Compile the gfx950 HIP sources into the in-tree C-ABI library libw8a8.so.
+
+    python minimax-h3-2xt4_amd/build_lib.py [--jobs N] [--verbose]
+
+Each csrc/*.hip compiles to an object under _build/ (in parallel), then one
+hipcc link produces w8a8/libw8a8.so next to the Python bindings.
+"""
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / 'csrc'
+BUILD = PKG / '_build'
+OUT = PKG / 'w8a8' / 'libw8a8.so'
+ARCH = 'gfx950'
+
+HIPCC_FLAGS = [
+    f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC',
+    # Every float expression is evaluated as written: no FMA contraction and
+    # no fast-math reassociation or reciprocal division.
+    '-ffp-contract=off', '-fno-fast-math',
+    # Packed FP32 instructions stay off.
+    '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+    '-Wno-unused-command-line-argument',
+    f'-I{ROOT / "include"}', f'-I{CSRC}',
+]
+
+
+def hipcc():
+    path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
+    if not Path(path).exists():
+        raise RuntimeError('hipcc not found')
+    return path
+
+
+def _compile(src, verbose):
+    obj = BUILD / (src.stem + '.o')
+    cmd = [hipcc(), *HIPCC_FLAGS, '-c', str(src), '-o', str(obj)]
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f'hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}')
+    if verbose and res.stderr.strip():
+        print(res.stderr, file=sys.stderr)
+    return obj
+
+
+def build(jobs=None, verbose=False):
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob('*.hip'))
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4) // 2))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), sources))
+    tmp = OUT.with_suffix('.so.tmp')
+    cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, objs), '-o', str(tmp)]
+    if verbose:
+        print(' '.join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f'link failed:\n{res.stdout}\n{res.stderr}')
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == '__main__':
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--jobs', type=int, default=None)
+    ap.add_argument('--verbose', action='store_true')
+    args = ap.parse_args()
+    print(build(args.jobs, args.verbose))

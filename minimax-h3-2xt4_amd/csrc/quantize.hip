@@ -1,0 +1,166 @@
+// Dynamic per-row absmax INT8 quantization, optionally after ConvRot256.
+//
+// One wavefront per row. Lane l owns the 16-element units u = l + 64 j
+// (elements [16u, 16u + 16)), loaded with 128-bit loads and stored as one
+// 128-bit int8 store, so each wave instruction touches a contiguous span.
+// With ConvRot256 a 256-column group is owned by 16 consecutive lanes and
+// rotated through a wave-private LDS transpose (w8a8_device.h).
+#include "w8a8_device.h"
+#include "w8a8_host.h"
+
+namespace w8a8 {
+
+constexpr int kQuantWaves = 4;
+constexpr int kQuantMaxJ = 8;  // units per lane kept in registers
+
+template <int DT>
+constexpr int dt_bytes() { return DT == kF32 ? 4 : 2; }
+
+// ROT: 0 no rotation, 1 ConvRot256 kept in FP32, 2 ConvRot256 rounded to
+// the input dtype. J > 0: the row (at most J units per lane) stays in
+// registers between the absmax and the quantization. J == 0: streaming, the
+// row is read twice.
+template <int DT, int ROT, int J>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(
+    const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t cols,
+    const float* __restrict__ row_max, int8_t* __restrict__ q, int64_t ldq,
+    float* __restrict__ scale) {
+  __shared__ float lds[ROT ? kQuantWaves * 1024 : 1];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kQuantWaves + wave;
+  if (row >= rows) return;
+  const int units = (int)(cols >> 4);
+  const int jcount = (units + 63) >> 6;
+  const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * dt_bytes<DT>();
+  float* buf = ROT ? lds + wave * 1024 + (lane >> 4) * 256 : nullptr;
+  const int t = lane & 15;
+
+  auto load_unit = [&](int u, float (&v)[16]) {
+    load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v);
+    if constexpr (ROT != 0) {
+      convrot256_lanes<true>(v, buf, t);
+      if constexpr (ROT == 2) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = round_to<DT>(v[i]);
+      }
+    }
+  };
+  auto store_unit = [&](int u, const float (&v)[16], float s, float rcp) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = pack4(quant1(v[4 * i], s, rcp), quant1(v[4 * i + 1], s, rcp),
+                   quant1(v[4 * i + 2], s, rcp), quant1(v[4 * i + 3], s, rcp));
+    *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  };
+
+  if constexpr (J > 0) {
+    float v[J][16];
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int u = lane + 64 * j;
+      if (u < units) {
+        load_unit(u, v[j]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+      }
+    }
+    amax = row_max ? row_max[row] : wave_max(amax);
+    const float s = row_scale_of(amax);
+    const float rcp = 1.0f / s;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int u = lane + 64 * j;
+      if (u < units) store_unit(u, v[j], s, rcp);
+    }
+    if (lane == 0) scale[row] = s;
+  } else {
+    float amax = 0.0f;
+    if (row_max) {
+      amax = row_max[row];
+    } else {
+      for (int j = 0; j < jcount; ++j) {
+        const int u = lane + 64 * j;
+        if (u < units) {
+          float v[16];
+          load_unit(u, v);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        }
+      }
+      amax = wave_max(amax);
+    }
+    const float s = row_scale_of(amax);
+    const float rcp = 1.0f / s;
+    for (int j = 0; j < jcount; ++j) {
+      const int u = lane + 64 * j;
+      if (u < units) {
+        float v[16];
+        load_unit(u, v);
+        store_unit(u, v, s, rcp);
+      }
+    }
+    if (lane == 0) scale[row] = s;
+  }
+}
+
+template <int DT, int ROT>
+static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
+  const int units = (int)(a->cols >> 4);
+  const int jneed = (units + 63) / 64;
+  const dim3 grid((unsigned)((a->rows + kQuantWaves - 1) / kQuantWaves));
+  const dim3 block(64 * kQuantWaves);
+#define W8A8_QLAUNCH(JJ)                                                                      \
+  hipLaunchKernelGGL((quantize_rows_kernel<DT, ROT, JJ>), grid, block, 0, stream, a->x, a->ldx, \
+                     a->rows, a->cols, a->row_max, a->q, a->ldq, a->scale)
+  switch (jneed) {
+    case 1: W8A8_QLAUNCH(1); break;
+    case 2: W8A8_QLAUNCH(2); break;
+    case 3: W8A8_QLAUNCH(3); break;
+    case 4: W8A8_QLAUNCH(4); break;
+    case 5: case 6: W8A8_QLAUNCH(6); break;
+    case 7: case 8: W8A8_QLAUNCH(8); break;
+    default: W8A8_QLAUNCH(0); break;
+  }
+#undef W8A8_QLAUNCH
+  static_assert(kQuantMaxJ == 8, "dispatch covers J = 1..8");
+  return launch_status("w8a8_quantize_rows");
+}
+
+}  // namespace w8a8
+
+extern "C" int w8a8_quantize_rows(const W8A8QuantArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_quantize_rows: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8QuantArgs),
+               "w8a8_quantize_rows: struct_size %u != %zu", a->struct_size, sizeof(W8A8QuantArgs));
+  const int es = (a->x_dtype == W8A8_F16 || a->x_dtype == W8A8_BF16) ? 2 : a->x_dtype == W8A8_F32 ? 4 : 0;
+  W8A8_REQUIRE(es != 0, "w8a8_quantize_rows: x_dtype %d not F16/BF16/F32", a->x_dtype);
+  W8A8_REQUIRE(a->rows >= 0 && a->cols >= 0, "w8a8_quantize_rows: negative shape");
+  W8A8_REQUIRE(a->convrot == 0 || a->convrot == 256, "w8a8_quantize_rows: convrot must be 0 or 256");
+  W8A8_REQUIRE(a->cols % (a->convrot ? 256 : 16) == 0,
+               "w8a8_quantize_rows: cols %lld not a multiple of %d", (long long)a->cols, a->convrot ? 256 : 16);
+  W8A8_REQUIRE(a->cols <= ((int64_t)1 << 30), "w8a8_quantize_rows: cols too large");
+  if (a->rows == 0 || a->cols == 0) {
+    W8A8_REQUIRE(a->cols != 0 || a->rows == 0, "w8a8_quantize_rows: zero-width rows have no scale");
+    return W8A8_OK;
+  }
+  W8A8_REQUIRE(a->x && a->q && a->scale, "w8a8_quantize_rows: null buffer");
+  W8A8_REQUIRE(a->ldx >= a->cols && a->ldq >= a->cols, "w8a8_quantize_rows: leading dimension below cols");
+  W8A8_REQUIRE(aligned16(a->x) && aligned16(a->q) && (a->ldx * es) % 16 == 0 && a->ldq % 16 == 0,
+               "w8a8_quantize_rows: x/q must be 16-byte aligned with 16-byte row strides");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
+  W8A8_REQUIRE(a->round_rotated == 0 || a->round_rotated == 1, "w8a8_quantize_rows: round_rotated must be 0 or 1");
+  const int mode = a->convrot == 0 ? 0 : (a->round_rotated && a->x_dtype != W8A8_F32) ? 2 : 1;
+  switch (a->x_dtype * 4 + mode) {
+    case W8A8_F16 * 4 + 0: return launch_quantize<kF16, 0>(a, stream);
+    case W8A8_F16 * 4 + 1: return launch_quantize<kF16, 1>(a, stream);
+    case W8A8_F16 * 4 + 2: return launch_quantize<kF16, 2>(a, stream);
+    case W8A8_BF16 * 4 + 0: return launch_quantize<kBF16, 0>(a, stream);
+    case W8A8_BF16 * 4 + 1: return launch_quantize<kBF16, 1>(a, stream);
+    case W8A8_BF16 * 4 + 2: return launch_quantize<kBF16, 2>(a, stream);
+    case W8A8_F32 * 4 + 0: return launch_quantize<kF32, 0>(a, stream);
+    default: return launch_quantize<kF32, 1>(a, stream);
+  }
+}

@@ -1,0 +1,165 @@
+// FC2 prologue: FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8, fused.
+//
+// One 256-thread workgroup per row. Sixteen 16-lane slots each own one
+// 256-column group per pass (lane t of a slot loads gate/up elements
+// [16t, 16t + 16) of the group with 128-bit loads). The rotated FP32 values
+// stay in registers until the row maximum is known, so the only HBM traffic
+// is the FP16 gate|up row in and the int8 row out (plus the fp32 scale).
+#include "w8a8_device.h"
+#include "w8a8_host.h"
+
+namespace w8a8 {
+
+constexpr int kSwigluMaxPasses = 4;  // register-resident up to width 16384
+
+template <int DT>
+constexpr int sw_bytes() { return DT == kF32 ? 4 : 2; }
+
+// P > 0: the row's rotated values stay in registers (P passes of 16 groups).
+// P == 0: streaming, the row is transformed twice (maximum, then quantize).
+template <int DT, int P>
+__global__ __launch_bounds__(256) void swiglu_quant_kernel(
+    const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t width,
+    const float* __restrict__ row_max_in, float* __restrict__ row_max_out,
+    float* __restrict__ group_max, int8_t* __restrict__ q, int64_t ldq,
+    float* __restrict__ scale) {
+  __shared__ float lds[4 * 1024];
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t row = blockIdx.x;
+  const int groups = (int)(width >> 8);
+  const int slot = tid >> 4;
+  const int t = tid & 15;
+  float* buf = lds + wave * 1024 + (lane >> 4) * 256;
+  const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * sw_bytes<DT>();
+
+  // v[j] <- rotated element 16 j + t of group g.
+  auto transform = [&](int g, float (&v)[16]) {
+    float gv[16], uv[16];
+    load16<DT>(xrow + ((int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), gv);
+    load16<DT>(xrow + (width + (int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), uv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = swiglu(gv[i], uv[i]);
+    convrot256_lanes<false>(v, buf, t);
+  };
+  auto group_absmax = [&](int g, const float (&v)[16]) {
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[j]));
+    m = seg16_max(m);
+    if (group_max && t == 0) group_max[row * groups + g] = m;
+    return m;
+  };
+  auto store_group = [&](int g, const float (&v)[16], float s, float rcp) {
+    uint8_t* bytes = reinterpret_cast<uint8_t*>(buf);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) bytes[16 * j + t] = (uint8_t)quant1(v[j], s, rcp);
+    wave_lds_sync();
+    const uint4 packed = reinterpret_cast<const uint4*>(bytes)[t];
+    *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)g * 256 + 16 * t) = packed;
+    wave_lds_sync();
+  };
+  auto row_reduce = [&](float m) {
+    m = wave_max(m);
+    if (lane == 0) wmax[wave] = m;
+    __syncthreads();
+    return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  };
+
+  if constexpr (P > 0) {
+    float v[P][16];
+    float local = 0.0f;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int g = slot + 16 * p;
+      if (g < groups) {
+        transform(g, v[p]);
+        local = fmaxf(local, group_absmax(g, v[p]));
+      }
+    }
+    const float rmax = row_reduce(local);
+    if (row_max_out && tid == 0) row_max_out[row] = rmax;
+    if (q) {
+      const float s = row_scale_of(row_max_in ? row_max_in[row] : rmax);
+      const float rcp = 1.0f / s;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        const int g = slot + 16 * p;
+        if (g < groups) store_group(g, v[p], s, rcp);
+      }
+      if (tid == 0) scale[row] = s;
+    }
+  } else {
+    float local = 0.0f;
+    const bool need_max = !row_max_in || row_max_out || group_max;
+    if (need_max) {
+      for (int g = slot; g < groups; g += 16) {
+        float v[16];
+        transform(g, v);
+        local = fmaxf(local, group_absmax(g, v));
+      }
+    }
+    const float rmax = row_reduce(local);
+    if (row_max_out && tid == 0) row_max_out[row] = rmax;
+    if (q) {
+      const float s = row_scale_of(row_max_in ? row_max_in[row] : rmax);
+      const float rcp = 1.0f / s;
+      for (int g = slot; g < groups; g += 16) {
+        float v[16];
+        transform(g, v);
+        store_group(g, v, s, rcp);
+      }
+      if (tid == 0) scale[row] = s;
+    }
+  }
+}
+
+template <int DT>
+static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
+  const int groups = (int)(a->width >> 8);
+  const int passes = (groups + 15) / 16;
+  const dim3 grid((unsigned)a->rows), block(256);
+#define W8A8_SLAUNCH(PP)                                                                     \
+  hipLaunchKernelGGL((swiglu_quant_kernel<DT, PP>), grid, block, 0, stream, a->x, a->ldx,     \
+                     a->rows, a->width, a->row_max, a->row_max_out, a->group_max, a->q, a->ldq, \
+                     a->scale)
+  switch (passes) {
+    case 1: W8A8_SLAUNCH(1); break;
+    case 2: W8A8_SLAUNCH(2); break;
+    case 3: W8A8_SLAUNCH(3); break;
+    case 4: W8A8_SLAUNCH(4); break;
+    default: W8A8_SLAUNCH(0); break;
+  }
+#undef W8A8_SLAUNCH
+  static_assert(kSwigluMaxPasses == 4, "dispatch covers P = 1..4");
+  return launch_status("w8a8_swiglu_quantize");
+}
+
+}  // namespace w8a8
+
+extern "C" int w8a8_swiglu_quantize(const W8A8SwigluArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_swiglu_quantize: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8SwigluArgs),
+               "w8a8_swiglu_quantize: struct_size %u != %zu", a->struct_size, sizeof(W8A8SwigluArgs));
+  W8A8_REQUIRE(a->x_dtype == W8A8_F16 || a->x_dtype == W8A8_F32,
+               "w8a8_swiglu_quantize: x_dtype %d not F16/F32", a->x_dtype);
+  const int es = a->x_dtype == W8A8_F16 ? 2 : 4;
+  W8A8_REQUIRE(a->rows >= 0 && a->width >= 0, "w8a8_swiglu_quantize: negative shape");
+  W8A8_REQUIRE(a->width % 256 == 0, "w8a8_swiglu_quantize: width %lld not a multiple of 256",
+               (long long)a->width);
+  W8A8_REQUIRE(a->rows <= 0x7fffffffLL && a->width <= ((int64_t)1 << 28), "w8a8_swiglu_quantize: shape too large");
+  if (a->rows == 0) return W8A8_OK;
+  W8A8_REQUIRE(a->width > 0, "w8a8_swiglu_quantize: zero width");
+  W8A8_REQUIRE(a->x != nullptr, "w8a8_swiglu_quantize: null x");
+  W8A8_REQUIRE(a->q || a->row_max_out || a->group_max, "w8a8_swiglu_quantize: no output requested");
+  W8A8_REQUIRE(!a->q || a->scale, "w8a8_swiglu_quantize: q requires scale");
+  W8A8_REQUIRE(a->ldx >= 2 * a->width, "w8a8_swiglu_quantize: ldx below 2*width");
+  W8A8_REQUIRE(aligned16(a->x) && (a->ldx * es) % 16 == 0, "w8a8_swiglu_quantize: x must be 16-byte aligned");
+  if (a->q) {
+    W8A8_REQUIRE(a->ldq >= a->width && a->ldq % 16 == 0 && aligned16(a->q),
+                 "w8a8_swiglu_quantize: q must be 16-byte aligned with ldq >= width, ldq %% 16 == 0");
+  }
+  hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
+  return a->x_dtype == W8A8_F16 ? launch_swiglu<kF16>(a, stream) : launch_swiglu<kF32>(a, stream);
+}

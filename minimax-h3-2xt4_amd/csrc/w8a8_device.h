@@ -1,0 +1,229 @@
+// Device-side helpers shared by the gfx950 kernels of the W8A8 path.
+//
+// Every floating-point expression here is meant to compile to separate IEEE
+// binary32 operations (the library is built with -ffp-contract=off and
+// without fast-math), in the order written: the CPU oracle evaluates the
+// same sequence.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w8a8 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- constants
+// fp32(1/127) = 0x3C010204 and the 1e-30 scale floor of the row quantizer.
+__device__ constexpr float kR127 = 1.0f / 127.0f;
+__device__ constexpr float kScaleFloor = 1e-30f;
+__device__ constexpr float kInv16 = 1.0f / 16.0f;
+// Fast-path bound of quant1: |y - rint(y)| below this means the reciprocal
+// product and the IEEE quotient round to the same integer (their distance is
+// below 2^-15 for |y| < 128, the margin here is 2^-12).
+__device__ constexpr float kTieGuard = 0.5f - 1.0f / 4096.0f;
+
+// ---------------------------------------------------------- conversions
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ float bf2f(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+enum DType { kF16 = 1, kBF16 = 2, kF32 = 3, kI32 = 4, kI8 = 5 };
+
+// Load 16 consecutive elements of type DT starting at p (16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load16(const void* p, float (&v)[16]) {
+  if constexpr (DT == kF32) {
+    const float4* q = reinterpret_cast<const float4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float4 t = q[i];
+      v[4 * i + 0] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+  } else {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint4 t = q[i];
+      uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint16_t lo = (uint16_t)(w[j] & 0xffffu), hi = (uint16_t)(w[j] >> 16);
+        v[8 * i + 2 * j + 0] = DT == kF16 ? h2f(lo) : bf2f(lo);
+        v[8 * i + 2 * j + 1] = DT == kF16 ? h2f(hi) : bf2f(hi);
+      }
+    }
+  }
+}
+
+// Round an fp32 value to the storage dtype DT and back (the rotation of a
+// 16-bit input returns a 16-bit tensor).
+template <int DT>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (DT == kF16) return h2f(f2h(x));
+  else if constexpr (DT == kBF16) return bf2f(f2bf(x));
+  else return x;
+}
+
+// ------------------------------------------------------------- exponential
+// Cephes single-precision exp (Moshier, Cephes Math Library expf.c):
+// Cody-Waite reduction with ln2 = C1 + C2, degree-5 minimax polynomial,
+// separate fp32 multiplies/adds, n rounded half to even, inputs clamped to
+// [-104, 89] (beyond which fp32 exp is 0 / inf), scaled by ldexp.
+__device__ __forceinline__ float exp_f32(float x) {
+  x = fminf(fmaxf(x, -104.0f), 89.0f);
+  const float n = rintf(x * 1.44269504088896341f);
+  float r = x - n * 0.693359375f;
+  r = r - n * -2.12194440e-4f;
+  const float z = r * r;
+  float p = 1.9875691500e-4f;
+  p = p * r + 1.3981999507e-3f;
+  p = p * r + 8.3334519073e-3f;
+  p = p * r + 4.1665795894e-2f;
+  p = p * r + 1.6666665459e-1f;
+  p = p * r + 5.0000001201e-1f;
+  const float y = (p * z + r) + 1.0f;
+  return ldexpf(y, (int)n);
+}
+
+// SwiGLU in FP32: (g / (1 + exp(-g))) * u with IEEE division.
+__device__ __forceinline__ float swiglu(float g, float u) {
+  const float den = 1.0f + exp_f32(-g);
+  const float act = g / den;
+  return act * u;
+}
+
+// ------------------------------------------------------------- quantizer
+// q = clamp(rne(x / s), -128, 127) with the IEEE quotient x / s.
+// rcp = 1/s (IEEE). The product x*rcp is within 2^-15 of the quotient for
+// |quotient| < 128, so away from half-integers both round to the same
+// integer; near a half-integer (or out of range, or NaN) the exact quotient
+// is computed.
+__device__ __forceinline__ int quant1(float x, float s, float rcp) {
+  const float y = x * rcp;
+  float n = rintf(y);
+  if (!(fabsf(y - n) < kTieGuard && fabsf(y) < 128.0f)) n = rintf(x / s);
+  n = fminf(fmaxf(n, -128.0f), 127.0f);
+  return (int)n;
+}
+
+__device__ __forceinline__ float row_scale_of(float amax) {
+  return fmaxf(amax * kR127, kScaleFloor);
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
+         ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+}
+
+// ------------------------------------------------------------- ConvRot256
+// One radix-4 stage of the regular H4 butterfly on four values e0..e3 that
+// differ only in the stage's digit: output digit d negates input 3-d, and
+// the sum runs ((p + q) + r) + s in input order.
+__device__ __forceinline__ void h4(float& e0, float& e1, float& e2, float& e3) {
+  const float o0 = ((e0 + e1) + e2) + (-e3);
+  const float o1 = ((e0 + e1) + (-e2)) + e3;
+  const float o2 = ((e0 + (-e1)) + e2) + e3;
+  const float o3 = (((-e0) + e1) + e2) + e3;
+  e0 = o0; e1 = o1; e2 = o2; e3 = o3;
+}
+
+// Stages over the two low digits of a 16-element register block v[i]
+// (i = 4*d1 + d0): digit d0 (stride 1), then digit d1 (stride 4).
+__device__ __forceinline__ void h4_low_digits(float (&v)[16]) {
+#pragma unroll
+  for (int b = 0; b < 4; ++b) h4(v[4 * b + 0], v[4 * b + 1], v[4 * b + 2], v[4 * b + 3]);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) h4(v[b + 0], v[b + 4], v[b + 8], v[b + 12]);
+}
+
+// Order LDS traffic between the lanes of one wavefront (lanes execute in
+// lockstep; this keeps the compiler from moving accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ConvRot256 of one 256-element group held by 16 consecutive lanes, lane t
+// holding elements 16t..16t+15 in v (natural order). buf is this group's
+// 256-float LDS slice. On return, if NATURAL, v again holds elements
+// 16t..16t+15; otherwise v[j] holds element 16j + t. The 1/16 factor is
+// applied last, as in the reference butterfly.
+template <bool NATURAL>
+__device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int t) {
+  h4_low_digits(v);
+  float4* row = reinterpret_cast<float4*>(buf + 16 * t);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) row[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  wave_lds_sync();
+  float w[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) w[j] = buf[16 * j + t];
+  // w[j] = element 16 j + t: j = 4*d3 + d2; digit d2 (stride 16), then d3.
+#pragma unroll
+  for (int b = 0; b < 4; ++b) h4(w[4 * b + 0], w[4 * b + 1], w[4 * b + 2], w[4 * b + 3]);
+#pragma unroll
+  for (int b = 0; b < 4; ++b) h4(w[b + 0], w[b + 4], w[b + 8], w[b + 12]);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) w[j] = w[j] * kInv16;
+  if constexpr (NATURAL) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) buf[16 * j + t] = w[j];
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float4 q = row[i];
+      v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+    }
+    wave_lds_sync();
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = w[j];
+    wave_lds_sync();
+  }
+}
+
+// ------------------------------------------------------------- reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Max over the 16 lanes of an aligned 16-lane segment.
+__device__ __forceinline__ float seg16_max(float v) {
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// -------------------------------------------------------------- epilogue
+enum Epilogue { kEpiInt32 = 0, kEpiRow = 1, kEpiColumn = 2 };
+
+template <int EPI>
+__device__ __forceinline__ float dequant1(int c, float a, float w) {
+  const float cf = (float)c;
+  if constexpr (EPI == kEpiRow) {
+    const float t = cf * a;
+    return t * w;
+  } else {
+    const float s = a * w;
+    return cf * s;
+  }
+}
+
+}  // namespace w8a8

@@ -1,0 +1,74 @@
+"""Operator selection for the INT8 projections (subset of the reference policy).
+
+Mirrors the linear-path fields and dispatch of patches/h3_operator_policy.py
+(H3OperatorPolicy :9-41, row_linear :213-237, row_linear_parts :240-255).
+Attention, RMS-RoPE and lifetime switches of the reference are not part of
+this path and are not represented.
+"""
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass(frozen=True)
+class H3OperatorPolicy:
+    row_linear_backend: str = 'tilelang_scaled_fp16'
+    fc2_quantizer: str = 'fused_stored'
+    column_linear_backend: str = 'cuda_int8_tilelang'
+
+    def __post_init__(self):
+        if self.row_linear_backend not in ('tilelang_packed', 'tilelang_scaled_fp16', 'native'):
+            raise ValueError('Unknown row-linear backend')
+        if self.fc2_quantizer not in ('native', 'owned_fp32', 'fused_stored', 'fused_recompute'):
+            raise ValueError('Unknown FC2 quantizer')
+        if self.column_linear_backend not in ('preallocated', 'cuda_int8_tilelang'):
+            raise ValueError('Unknown column linear backend')
+
+
+def configure_block(block, kind, policy):
+    """Attach the policy to a block's projections (h3_operator_policy.py:56-75, linear part)."""
+    block.operator_policy = policy
+    names = ('o_proj', 'down_proj', 'q_proj', 'k_proj', 'v_proj', 'gate_proj', 'up_proj') if kind == 'te' \
+        else ('out_proj', 'fc2', 'qkv_proj', 'fc1')
+    for name in names:
+        module = getattr(block, name, None)
+        if module is not None:
+            module.operator_policy = policy
+    return block
+
+
+def row_linear(module, x, fallback, comm, input_act=None, residual=None):
+    """Dispatch a row projection; the fused SwiGLU route when the policy selects it.
+
+    ``residual`` (FP16, optional) is fused into the GEMM epilogue on the fused
+    route; on the fallback it is added after the storage cast.
+    """
+    from . import swiglu_quant as quant
+    policy = getattr(module, 'operator_policy', None)
+    fused = (policy is not None and policy.fc2_quantizer in ('fused_stored', 'fused_recompute')
+             and input_act == 'swiglu' and policy.row_linear_backend != 'native')
+    if fused and quant.supported(x, module.weight, module.weight_scale, module.world_size,
+                                 module.convrot_groupsize):
+        return quant.row_linear(x, module.weight, module.weight_scale, comm, mode=policy.fc2_quantizer,
+                                scaled_transport=policy.row_linear_backend == 'tilelang_scaled_fp16',
+                                residual=residual)
+    if input_act == 'swiglu' or (policy is not None and policy.row_linear_backend == 'tilelang_scaled_fp16'):
+        # FP32 preparation island, as the reference keeps on fallback geometry.
+        x = x.float()
+    out = fallback(x, module.weight, module.weight_scale, comm, module.world_size, module.convrot_groupsize,
+                   input_act)
+    if residual is not None:
+        from .h3_tensor_flow import residual_add
+        out = residual_add(residual, out.to(residual.dtype))
+    return out
+
+
+def row_linear_parts(module, gate, up, fallback, comm):
+    """TE down projection from separate gate/up halves (h3_operator_policy.py:240-255)."""
+    policy = getattr(module, 'operator_policy', None)
+    if gate.shape != up.shape or gate.dtype != up.dtype or gate.device != up.device:
+        raise ValueError('Matching gate/up required')
+    if (policy is not None and policy.row_linear_backend != 'native'
+            and policy.fc2_quantizer in ('fused_stored', 'fused_recompute')):
+        return row_linear(module, torch.cat((gate, up), -1), fallback, comm, 'swiglu')
+    return row_linear(module, torch.cat((gate, up), -1).float(), fallback, comm, 'swiglu')

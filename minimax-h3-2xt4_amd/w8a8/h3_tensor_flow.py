@@ -1,0 +1,71 @@
+"""FP16-fix tensor flow: residual divisor folding and the residual add.
+
+Mirrors the linear-path parts of patches/h3_tensor_flow.py: TensorFlowPolicy
+(:16-37), fold_linear (:82-103; the divisor goes into the FP32 INT8 weight
+scales of the row projections), prepare_tp (:114-127, projection folds) and
+residual_add (:130-131).
+"""
+from dataclasses import dataclass
+
+import torch
+from torch import nn
+
+
+@dataclass(frozen=True)
+class TensorFlowPolicy:
+    mode: str = 'legacy'
+    residual_exponent: int = 9
+    vision_residual_exponent: int = 0
+    video_residual_exponent: int = 0
+
+    def __post_init__(self):
+        if self.mode not in ('legacy', 'fp16', 'bf16_reference'):
+            raise ValueError('Unknown H3 tensor flow')
+        for value in (self.residual_exponent, self.vision_residual_exponent, self.video_residual_exponent):
+            if type(value) is not int or not 0 <= value <= 12:
+                raise ValueError('Residual exponent must be an integer in [0,12]')
+
+    @property
+    def enabled(self):
+        return self.mode != 'legacy'
+
+    @property
+    def dtype(self):
+        return torch.bfloat16 if self.mode == 'bf16_reference' else torch.float16
+
+    @property
+    def divisor(self):
+        return float(2 ** self.residual_exponent)
+
+
+def fold_linear(module, divisor):
+    """Divide the FP32 INT8 weight scale (and any bias) by the divisor once.
+
+    The divisor is a power of two, so the fold is exact for normal values.
+    """
+    base = getattr(module, 'base', module)
+    if not hasattr(base, 'weight_scale'):
+        raise ValueError('Residual folding requires an INT8 projection with FP32 weight scales')
+    base.weight_scale = nn.Parameter(base.weight_scale.detach().float() / divisor, requires_grad=False)
+    bias = getattr(base, 'bias', None)
+    if bias is not None:
+        base.bias = nn.Parameter(bias.detach() / divisor, requires_grad=False)
+
+
+def prepare_tp(block, kind, policy):
+    """Fold the divisor into the row projections of a block (linear part of :114-127)."""
+    if not policy.enabled:
+        return block
+    if hasattr(block, 'tensor_flow'):
+        raise ValueError('Tensor flow already prepared')
+    block.tensor_flow = policy
+    for name in (('o_proj', 'down_proj') if kind == 'te' else ('out_proj', 'fc2')):
+        module = getattr(block, name, None)
+        if module is not None:
+            fold_linear(module, policy.divisor)
+    return block
+
+
+def residual_add(x, branch):
+    """x = cast(f32(x) + f32(branch)) to x's dtype."""
+    return (x.float() + branch.float()).to(x.dtype)

@@ -1,0 +1,216 @@
+"""Typed wrappers of the libw8a8 entry points over torch device tensors.
+
+Outputs are allocated here with torch (the library never allocates) and the
+work is queued on the current stream of the tensors' device. Every wrapper
+checks device, dtype, shape and layout first and raises ValueError on a
+contract violation; a failing library call raises W8A8Error.
+"""
+import torch
+
+from . import _abi
+from ._abi import EPI_COLUMN, EPI_INT32, EPI_ROW  # noqa: F401
+
+_OUT_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _device(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError('libw8a8 operates on HIP device tensors only (no CPU fallback)')
+    dev = tensors[0].device
+    for t in tensors:
+        if t is not None and t.device != dev:
+            raise ValueError('all tensors must be on the same device')
+    return dev
+
+
+def _rows_2d(x):
+    """[rows, cols] view with unit column stride (row stride may exceed cols)."""
+    if x.ndim != 2:
+        x = x.reshape(-1, x.shape[-1])
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x
+
+
+def _scale_vec(s, n, name):
+    s = s.to(dtype=torch.float32).reshape(-1)
+    if not s.is_contiguous():
+        s = s.contiguous()
+    if s.numel() not in (1, n):
+        raise ValueError(f'{name} must be scalar or have {n} entries')
+    return s, (0 if s.numel() == 1 else 1)
+
+
+def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=None, scale_out=None):
+    """Per-row absmax INT8 quantization of x [M, K] -> (q int8 [M,K], scale fp32 [M,1]).
+
+    convrot=True rotates each 256-column group first (regular-H4 ConvRot256);
+    round_rotated rounds the rotated values to x's dtype before the absmax.
+    row_max [M] (or [M,1]) fp32 replaces the row's own absmax.
+    """
+    x = _rows_2d(x)
+    _device(x, row_max)
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError('x must be float16, bfloat16 or float32')
+    rows, cols = x.shape
+    if convrot and cols % 256:
+        raise ValueError('ConvRot group size must divide input features')
+    if cols % 16:
+        raise ValueError('input features must be a multiple of 16')
+    q = out if out is not None else torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    scale = scale_out if scale_out is not None else torch.empty((rows, 1), dtype=torch.float32, device=x.device)
+    if row_max is not None:
+        row_max = row_max.to(torch.float32).reshape(-1).contiguous()
+        if row_max.numel() != rows:
+            raise ValueError('row_max must have one entry per row')
+    if rows == 0:
+        return q, scale
+    args = _abi.QuantArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows, cols=cols,
+                          convrot=256 if convrot else 0, round_rotated=1 if round_rotated else 0,
+                          row_max=_abi.ptr(row_max), q=q.data_ptr(), ldq=q.stride(0), scale=scale.data_ptr(),
+                          stream=_abi.stream_of(x))
+    _abi.call('w8a8_quantize_rows', args)
+    return q, scale
+
+
+def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_group_max=False):
+    """Fused FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8 of x [M, 2W].
+
+    Returns a dict with 'q' [M,W] int8 and 'scale' [M,1] fp32 (when
+    quantize), 'row_max' [M,1] and 'group_max' [M,W/256] when requested.
+    row_max (input) is an external absmax for the quantization.
+    """
+    x = _rows_2d(x)
+    _device(x, row_max)
+    if x.dtype not in (torch.float16, torch.float32):
+        raise ValueError('x must be float16 or float32')
+    rows, two_w = x.shape
+    width = two_w // 2
+    if two_w != 2 * width or width % 256 or width == 0:
+        raise ValueError('[M, 2W] input with W a positive multiple of 256 required')
+    if not (quantize or want_row_max or want_group_max):
+        raise ValueError('no output requested')
+    dev = x.device
+    res = {}
+    if quantize:
+        res['q'] = torch.empty((rows, width), dtype=torch.int8, device=dev)
+        res['scale'] = torch.empty((rows, 1), dtype=torch.float32, device=dev)
+    if want_row_max:
+        res['row_max'] = torch.empty((rows, 1), dtype=torch.float32, device=dev)
+    if want_group_max:
+        res['group_max'] = torch.empty((rows, width // 256), dtype=torch.float32, device=dev)
+    if row_max is not None:
+        row_max = row_max.to(torch.float32).reshape(-1).contiguous()
+        if row_max.numel() != rows:
+            raise ValueError('row_max must have one entry per row')
+    if rows == 0:
+        return res
+    args = _abi.SwigluArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows,
+                           width=width, row_max=_abi.ptr(row_max), row_max_out=_abi.ptr(res.get('row_max')),
+                           group_max=_abi.ptr(res.get('group_max')), q=_abi.ptr(res.get('q')),
+                           ldq=width, scale=_abi.ptr(res.get('scale')), stream=_abi.stream_of(x))
+    _abi.call('w8a8_swiglu_quantize', args)
+    return res
+
+
+def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out, device):
+    if epilogue == EPI_INT32:
+        if bias is not None or residual is not None:
+            raise ValueError('raw int32 output takes no bias or residual')
+        out = out if out is not None else torch.empty((m, n), dtype=torch.int32, device=device)
+        if out.dtype != torch.int32:
+            raise ValueError('int32 output required')
+        return dict(row_scale=None, col_scale=None, col_scale_stride=0, bias=None, bias_dtype=0,
+                    out_dtype=_abi.I32, residual=None, ldr=0), out, ()
+    if epilogue not in (EPI_ROW, EPI_COLUMN):
+        raise ValueError('unknown epilogue')
+    if out_dtype not in _OUT_DTYPES:
+        raise ValueError('out_dtype must be float16, bfloat16 or float32')
+    a = row_scale.to(torch.float32).reshape(-1).contiguous()
+    if a.numel() != m:
+        raise ValueError('row scale must have one entry per row')
+    w, wstride = _scale_vec(col_scale, n, 'weight_scale')
+    keep = [a, w]
+    bias_dtype = 0
+    if bias is not None:
+        bias = bias.reshape(-1)
+        if bias.dtype not in (torch.float16, torch.float32):
+            bias = bias.float()
+        bias = bias.contiguous()
+        if bias.numel() != n:
+            raise ValueError('bias must have one entry per output feature')
+        bias_dtype = _abi.DTYPE_CODE[bias.dtype]
+        keep.append(bias)
+    ldr = 0
+    if residual is not None:
+        if out_dtype != torch.float16 or residual.dtype != torch.float16:
+            raise ValueError('the fused residual add is FP16 only')
+        residual = _rows_2d(residual)
+        if residual.shape != (m, n) or residual.stride(0) % 4 or residual.data_ptr() % 8:
+            raise ValueError('residual must be [M, N] with an aligned row stride')
+        ldr = residual.stride(0)
+        keep.append(residual)
+    _device(a, w, bias, residual)
+    out = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=device)
+    if out.dtype != out_dtype or out.shape != (m, n) or out.stride(-1) != 1:
+        raise ValueError('out must be [M, N] of out_dtype with unit column stride')
+    return dict(row_scale=a.data_ptr(), col_scale=w.data_ptr(), col_scale_stride=wstride,
+                bias=_abi.ptr(bias), bias_dtype=bias_dtype, out_dtype=_abi.DTYPE_CODE[out_dtype],
+                residual=_abi.ptr(residual), ldr=ldr), out, keep
+
+
+def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=None, residual=None,
+         out_dtype=torch.float16, out=None):
+    """C = q @ weight.T on i8 MFMA with a fused epilogue.
+
+    q int8 [M, K], weight int8 [N, K]. epilogue EPI_INT32 -> int32 [M, N];
+    EPI_ROW -> out_dtype((C * a) * w [+ bias]); EPI_COLUMN ->
+    out_dtype(C * (a * w) [+ bias]); residual (FP16 [M, N]) -> FP16
+    residual + FP16 branch, and out may be the residual itself.
+    """
+    q = _rows_2d(q)
+    if weight.ndim != 2:
+        raise ValueError('weight must be 2-D [N, K]')
+    if weight.stride(-1) != 1:
+        weight = weight.contiguous()
+    _device(q, weight)
+    if q.dtype != torch.int8 or weight.dtype != torch.int8:
+        raise ValueError('int8 operands required')
+    m, k = q.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError('Input and weight inner dimensions must match')
+    if k % 16 or q.stride(0) % 16 or weight.stride(0) % 16:
+        raise ValueError('K and the operand row strides must be multiples of 16')
+    fields, out, keep = _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out,
+                                       q.device)
+    if m == 0 or n == 0:
+        return out
+    args = _abi.GemmArgs(epilogue=epilogue, a=q.data_ptr(), lda=q.stride(0), b=weight.data_ptr(),
+                         ldb=weight.stride(0), m=m, n=n, k=k, out=out.data_ptr(), ldc=out.stride(0),
+                         stream=_abi.stream_of(q), **fields)
+    _abi.call('w8a8_gemm', args)
+    del keep
+    return out
+
+
+def dequantize(acc, row_scale, col_scale, *, epilogue=EPI_ROW, out_dtype=torch.float16, bias=None, residual=None,
+               out=None):
+    """Standalone epilogue of an int32 accumulator [M, N]."""
+    acc = _rows_2d(acc)
+    _device(acc)
+    if acc.dtype != torch.int32:
+        raise ValueError('int32 accumulator required')
+    if epilogue not in (EPI_ROW, EPI_COLUMN):
+        raise ValueError('dequantize needs the ROW or COLUMN order')
+    m, n = acc.shape
+    fields, out, keep = _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out,
+                                       acc.device)
+    if m == 0 or n == 0:
+        return out
+    args = _abi.DequantArgs(epilogue=epilogue, acc=acc.data_ptr(), ldacc=acc.stride(0), m=m, n=n,
+                            out=out.data_ptr(), ldc=out.stride(0), stream=_abi.stream_of(acc), **fields)
+    _abi.call('w8a8_dequantize', args)
+    del keep
+    return out

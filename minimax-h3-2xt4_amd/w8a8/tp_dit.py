@@ -1,0 +1,128 @@
+"""INT8 projection modules (the reference's tp_dit API) at world_size 1.
+
+ColumnParallelLinearINT8 / RowParallelLinearINT8 keep the attribute names of
+patches/tp_dit.py:25-162 (weight int8 [N, K], weight_scale fp32 [N, 1],
+convrot, convrot_groupsize, world_size, in/out features) so shards load the
+same way; with world_size 1 there is no exchange. DiTFeedForwardINT8 is the
+FC1 -> SwiGLU/ConvRot256 -> FC2 (+ residual) part of TPDiTBlockINT8.forward
+(patches/tp_dit.py:350-360) and chunked_rows runs any of them over M in
+fixed row chunks with the weights resident.
+"""
+import torch
+from torch import nn
+
+from . import parallel_int8
+from .dit_column_linear import column_linear
+from .h3_operator_policy import H3OperatorPolicy, row_linear as dispatch_row
+
+
+class ColumnParallelLinearINT8(nn.Module):
+    """Output-feature split INT8 projection (patches/tp_dit.py:25-96)."""
+
+    def __init__(self, in_features, out_features, rank=0, world_size=1, convrot=True, convrot_groupsize=256,
+                 device=None, components=1):
+        super().__init__()
+        if out_features % world_size:
+            raise ValueError('out_features must divide across ranks')
+        self.components = components
+        self.in_features = in_features
+        self.out_features_per_rank = out_features // world_size
+        self.rank = rank
+        self.world_size = world_size
+        self.convrot = convrot
+        self.convrot_groupsize = convrot_groupsize
+        self.device = torch.device(device) if device is not None else torch.device('cuda', 0)
+        self.weight = nn.Parameter(torch.empty(self.out_features_per_rank, in_features, dtype=torch.int8,
+                                               device=self.device), requires_grad=False)
+        self.weight_scale = nn.Parameter(torch.empty(self.out_features_per_rank, 1, dtype=torch.float32,
+                                                     device=self.device), requires_grad=False)
+
+    def load_shard_from_full(self, full_weight, full_scale):
+        w, scale = parallel_int8.packed_rows(full_weight, full_scale, self.rank, self.world_size, self.components)
+        self.weight.data.copy_(w)
+        self.weight_scale.data.copy_(scale)
+
+    def forward(self, x):
+        policy = getattr(self, 'operator_policy', None)
+        backend = 'preallocated' if policy is None else policy.column_linear_backend
+        out = column_linear(x.reshape(-1, self.in_features), self.weight, self.weight_scale,
+                            convrot=self.convrot, convrot_groupsize=self.convrot_groupsize,
+                            out_dtype=x.dtype, backend=backend)
+        return out.view(*x.shape[:-1], self.out_features_per_rank)
+
+
+class RowParallelLinearINT8(nn.Module):
+    """Input-feature split INT8 projection (patches/tp_dit.py:98-162)."""
+
+    def __init__(self, in_features, out_features, rank=0, world_size=1, convrot=True, convrot_groupsize=256,
+                 device=None):
+        super().__init__()
+        if in_features % world_size:
+            raise ValueError('in_features must divide across ranks')
+        self.in_features_per_rank = in_features // world_size
+        self.out_features = out_features
+        self.rank = rank
+        self.world_size = world_size
+        self.convrot = convrot
+        self.convrot_groupsize = convrot_groupsize
+        self.device = torch.device(device) if device is not None else torch.device('cuda', 0)
+        self.weight = nn.Parameter(torch.empty(out_features, self.in_features_per_rank, dtype=torch.int8,
+                                               device=self.device), requires_grad=False)
+        self.weight_scale = nn.Parameter(torch.empty(out_features, 1, dtype=torch.float32, device=self.device),
+                                         requires_grad=False)
+
+    def load_shard_from_full(self, full_weight, full_scale):
+        start = self.rank * self.in_features_per_rank
+        self.weight.data.copy_(full_weight[:, start:start + self.in_features_per_rank])
+        self.weight_scale.data.copy_(full_scale)
+
+    def forward(self, x, reduce_sum=True, input_act=None, *, residual=None, out_dtype=None):
+        """Row projection. With ``residual`` (FP16) the result is the updated
+        residual fp16(residual + fp16(branch)); otherwise the branch in
+        ``out_dtype`` (default x's dtype).
+        """
+        if not reduce_sum and self.world_size > 1:
+            raise ValueError('Quantization-preserving projection requires reduction')
+        out = dispatch_row(self, x, parallel_int8.row_linear, None, input_act, residual=residual)
+        if residual is not None:
+            return out
+        return out.to(out_dtype or x.dtype)
+
+
+class DiTFeedForwardINT8(nn.Module):
+    """FC1 (column, gate|up) -> fused SwiGLU/ConvRot256 prologue -> FC2 (row) + residual.
+
+    hidden -> 2*ffn -> hidden on one GPU; fc2.weight_scale carries the
+    residual divisor once prepared (h3_tensor_flow.prepare_tp).
+    """
+
+    def __init__(self, hidden, ffn, device=None, policy=None):
+        super().__init__()
+        self.fc1 = ColumnParallelLinearINT8(hidden, 2 * ffn, device=device, components=2)
+        self.fc2 = RowParallelLinearINT8(ffn, hidden, device=device)
+        policy = policy or H3OperatorPolicy()
+        self.operator_policy = policy
+        self.fc1.operator_policy = policy
+        self.fc2.operator_policy = policy
+
+    def forward(self, h, residual):
+        y = self.fc1(h)
+        return self.fc2(y, input_act='swiglu', residual=residual)
+
+
+def chunked_rows(fn, x, *others, chunk_rows=16384, out=None):
+    """Apply fn(x_chunk, *other_chunks) over row chunks of 2-D x.
+
+    Exact for W8A8 projections because every scale is per row. ``out`` (if
+    given) receives the rows in place; otherwise the chunks are concatenated.
+    """
+    rows = x.shape[0]
+    parts = []
+    for start in range(0, rows, chunk_rows):
+        stop = min(start + chunk_rows, rows)
+        y = fn(x[start:stop], *[o[start:stop] for o in others])
+        if out is not None:
+            out[start:stop].copy_(y)
+        else:
+            parts.append(y)
+    return out if out is not None else torch.cat(parts, 0)

@@ -1,0 +1,103 @@
+"""Seeded synthetic inputs for the W8A8 path's benchmark shapes.
+
+All tensors are drawn on the CPU with torch.Generator(seed) so any consumer
+(GPU kernels, the CPU baseline) sees identical bytes. Activations are FP16
+N(0, sigma) with a few outlier channels scaled x20; weights are FP32
+N(0, 0.02) to be quantized per output channel; biases FP16 N(0, 0.01).
+
+Shapes:
+  w8a8_linear     M=4096 tokens, K=3072, N=3072, bias, 8 outlier channels
+  dit_ffn         M=16384, hidden 3072, FFN 8192 (FC1 3072 -> 2x8192 gate|up,
+                  FC2 8192 -> 3072), FP16 residual N(0,1)/512
+  dit_qkv         M=53504 (16 frames x 76x44 patches), 3072 -> 9216, bias,
+                  0.1% outlier channels
+  te_skinny       M in {1, 64, 512}, 4096 -> 14336 (up), 14336 -> 4096 (down),
+                  activations N(0, 0.5)
+  dit_half_shard  M=204336 in 16384-row chunks; QKV 3072 -> 4608, FC1
+                  3072 -> 2x4096, FC2 4096 -> 3072 with an FP32 output
+"""
+import torch
+
+RESIDUAL_DIVISOR = 512.0
+
+SHAPES = {
+    'w8a8_linear': dict(seed=0, m=4096, k=3072, n=3072, outliers=8),
+    'dit_ffn': dict(seed=1, m=16384, hidden=3072, ffn=8192, outliers=8),
+    'dit_qkv': dict(seed=2, m=53504, k=3072, n=9216, outliers=3),
+    'te_skinny': dict(seed=3, ms=(1, 64, 512), hidden=4096, ffn=14336),
+    'dit_half_shard': dict(seed=4, m=204336, hidden=3072, qkv=4608, ffn=4096, chunk=16384, outliers=8),
+}
+
+
+def activations(gen, m, k, outliers, sigma=1.0):
+    x = torch.randn((m, k), generator=gen, dtype=torch.float32) * sigma
+    if outliers:
+        cols = torch.randperm(k, generator=gen)[:outliers]
+        x[:, cols] *= 20.0
+    return x.half()
+
+
+def weights(gen, n, k, std=0.02):
+    return torch.randn((n, k), generator=gen, dtype=torch.float32) * std
+
+
+def bias(gen, n):
+    return (torch.randn((n,), generator=gen, dtype=torch.float32) * 0.01).half()
+
+
+def w8a8_linear(m=None, seed=None):
+    s = SHAPES['w8a8_linear']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m = m or s['m']
+    x = activations(g, m, s['k'], s['outliers'])
+    w = weights(g, s['n'], s['k'])
+    b = bias(g, s['n'])
+    return dict(x=x, w=w, bias=b)
+
+
+def dit_ffn(m=None, hidden=None, ffn=None, seed=None):
+    s = SHAPES['dit_ffn']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m, hidden, ffn = m or s['m'], hidden or s['hidden'], ffn or s['ffn']
+    h = activations(g, m, hidden, s['outliers'])
+    w1 = weights(g, 2 * ffn, hidden)        # rows [0, ffn) gate, [ffn, 2ffn) up
+    w2 = weights(g, hidden, ffn)
+    residual = (torch.randn((m, hidden), generator=g) / RESIDUAL_DIVISOR).half()
+    return dict(h=h, w1=w1, w2=w2, residual=residual)
+
+
+def dit_qkv(m=None, seed=None):
+    s = SHAPES['dit_qkv']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m = m or s['m']
+    x = activations(g, m, s['k'], s['outliers'])
+    w = weights(g, s['n'], s['k'])
+    b = bias(g, s['n'])
+    return dict(x=x, w=w, bias=b)
+
+
+def te_skinny(m, seed=None):
+    s = SHAPES['te_skinny']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    x = (torch.randn((m, s['hidden']), generator=g) * 0.5).half()
+    w_up = weights(g, s['ffn'], s['hidden'])
+    w_down = weights(g, s['hidden'], s['ffn'])
+    x_down = (torch.randn((m, s['ffn']), generator=g) * 0.5).half()
+    return dict(x=x, w_up=w_up, w_down=w_down, x_down=x_down)
+
+
+def dit_half_shard(m=None, seed=None):
+    s = SHAPES['dit_half_shard']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m = m or s['m']
+    h = activations(g, m, s['hidden'], s['outliers'])
+    w_qkv = weights(g, s['qkv'], s['hidden'])
+    w1 = weights(g, 2 * s['ffn'], s['hidden'])
+    w2 = weights(g, s['hidden'], s['ffn'])
+    return dict(h=h, w_qkv=w_qkv, w1=w1, w2=w2)
+
+
+def quantize_weight(w, device):
+    """Per-output-channel INT8 weights and FP32 scales [N, 1] on the GPU (libw8a8)."""
+    from . import kernels
+    return kernels.quantize_rows(w.to(device=device, dtype=torch.float32))

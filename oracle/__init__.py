@@ -1,0 +1,41 @@
+"""CPU oracle of the W8A8 INT8 linear path - TEST INFRASTRUCTURE ONLY.
+
+This package restates, in numpy, the arithmetic of the reference's torch
+quantize + ``_int_mm`` + dequantize path and of its fused FC2 prologue, so
+that the HIP kernels can be checked bit for bit. Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may
+import it, and only as the checker (or the timed CPU baseline): the product
+path (the ``w8a8`` package and ``libw8a8.so``) never calls it and has no CPU
+fallback.
+
+Pinning (what checks each function, beyond "the same formula retyped"):
+
+* ``quantize_rows``     - hand-computed known answers, exact ties (half to
+  even), zero rows (scale 1e-30), the absmax element mapping to +-127, and a
+  scale that distinguishes ``amax * fp32(1/127)`` from ``amax / 127``.
+* ``convrot256``        - the closed form H[i][j] = (-1)^#{digits with
+  i_d + j_d = 3} / 16 in float64 (exact on small integer inputs), H.H = I,
+  unit vectors mapping to columns, norm preservation.
+* ``exp_f32``           - against float64 ``exp`` over a dense sweep (<= 2
+  ulp), exact at 0, overflow/underflow thresholds.
+* ``swiglu_f32``        - against float64 ``g*u/(1+exp(-g))`` (few ulp) and
+  special values.
+* ``int_mm``            - brute-force int64 products on small inputs and the
+  all -128 known answer K*16384.
+* ``dequantize_*``      - the reference's hand example
+  (benchmarks/test_fp16_fc2_experiment.py:11-29), and order-sensitive cases
+  where (C*a)*w and C*(a*w) round differently.
+* ``fc2_prologue``      - composition of the pinned pieces, plus the
+  invariant that rotated row norms equal the SwiGLU row norms.
+
+Functions that only an import of the absent third-party comfy-kitchen 0.2.37
+could pin bit for bit (its GEMM-based rotation summation order) are noted
+"parity unpinned" in the function docstrings.
+"""
+from .w8a8_oracle import (  # noqa: F401
+    R127, SCALE_FLOOR, INV16,
+    quantize_rows, convrot256, hadamard256, exp_f32, swiglu_f32,
+    prepare_activation, fc2_prologue, int_mm, dequantize_row,
+    dequantize_column, residual_add, to_bf16_bits, from_bf16_bits,
+    cast_out, quantize_weight, column_linear, row_linear_fc2, ffn_block,
+)

@@ -1,0 +1,109 @@
+"""The C ABI library on the CPU: it loads, exports every symbol the header
+declares, agrees on struct layouts, and rejects invalid arguments before any
+launch (nothing here runs device code)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (loaded first: the library shares torch's HIP runtime)
+
+from w8a8 import _abi
+
+HEADER = Path(__file__).resolve().parents[1] / 'include' / 'w8a8.h'
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r'^\s*(?:int|int64_t|const char\*)\s+(w8a8_\w+)\s*\(', text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    assert declared_functions() == sorted(_abi.ENTRY_POINTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_abi.LIB_PATH))
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_struct_sizes():
+    lib = _abi.load()
+    assert lib.w8a8_abi_version() == _abi.ABI_VERSION
+    for i, st in enumerate(_abi.STRUCTS):
+        assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
+    assert lib.w8a8_struct_size(99) == -1
+    # header field order: sizes computed from the C declaration
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 144, 120]
+
+
+def _expect_invalid(name, args, fragment):
+    lib = _abi.load()
+    rc = getattr(lib, name)(ctypes.byref(args))
+    assert rc == _abi.ERR_INVALID
+    assert fragment in lib.w8a8_last_error().decode()
+
+
+def test_struct_size_mismatch_rejected():
+    a = _abi.QuantArgs(struct_size=12, x_dtype=_abi.F16)
+    _expect_invalid('w8a8_quantize_rows', a, 'struct_size')
+
+
+def test_quantize_argument_checks():
+    base = dict(struct_size=ctypes.sizeof(_abi.QuantArgs), x_dtype=_abi.F16, x=4096, ldx=256, rows=4, cols=256,
+                convrot=0, round_rotated=0, q=8192, ldq=256, scale=16384)
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'x_dtype': 9}), 'x_dtype')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'convrot': 128}), 'convrot')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'cols': 24, 'ldx': 24, 'ldq': 24}),
+                    'multiple of 16')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'x': 4097}), 'aligned')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'ldx': 100}), 'leading dimension')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'scale': None}), 'null buffer')
+
+
+def test_gemm_argument_checks():
+    base = dict(struct_size=ctypes.sizeof(_abi.GemmArgs), epilogue=_abi.EPI_INT32, a=4096, lda=64, b=8192,
+                ldb=64, m=16, n=16, k=64, out=16384, ldc=16, out_dtype=_abi.I32)
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'k': 72, 'lda': 80, 'ldb': 80}), 'multiple of 16')
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'bias': 4096, 'bias_dtype': _abi.F16}), 'no bias')
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'out_dtype': _abi.F16}), 'I32')
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'epilogue': _abi.EPI_ROW, 'out_dtype': _abi.F16}),
+                    'row_scale')
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'epilogue': _abi.EPI_ROW, 'out_dtype': _abi.BF16,
+                                                   'row_scale': 64, 'col_scale': 64, 'col_scale_stride': 1,
+                                                   'residual': 4096, 'ldr': 16}), 'residual')
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'k': 1 << 20, 'lda': 1 << 20, 'ldb': 1 << 20}),
+                    'overflow')
+    _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'a': 4100}), 'aligned')
+
+
+def test_swiglu_argument_checks():
+    base = dict(struct_size=ctypes.sizeof(_abi.SwigluArgs), x_dtype=_abi.F16, x=4096, ldx=512, rows=2,
+                width=256, q=8192, ldq=256, scale=16384)
+    _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'width': 320, 'ldx': 640}), 'multiple of 256')
+    _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'x_dtype': _abi.BF16}), 'x_dtype')
+    _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'q': None, 'scale': None}), 'no output')
+    _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'ldx': 256}), 'ldx')
+
+
+def test_dequantize_argument_checks():
+    base = dict(struct_size=ctypes.sizeof(_abi.DequantArgs), epilogue=_abi.EPI_INT32, acc=4096, ldacc=16, m=4,
+                n=16, row_scale=64, col_scale=128, col_scale_stride=1, out=8192, ldc=16, out_dtype=_abi.F16)
+    _expect_invalid('w8a8_dequantize', _abi.DequantArgs(**base), 'ROW or COLUMN')
+    _expect_invalid('w8a8_dequantize', _abi.DequantArgs(**{**base, 'epilogue': _abi.EPI_ROW,
+                                                            'col_scale_stride': 3}), 'stride')
+
+
+def test_empty_problems_return_ok_without_launch():
+    lib = _abi.load()
+    a = _abi.GemmArgs(struct_size=ctypes.sizeof(_abi.GemmArgs), epilogue=_abi.EPI_INT32, m=0, n=16, k=64,
+                      out_dtype=_abi.I32)
+    assert lib.w8a8_gemm(ctypes.byref(a)) == _abi.OK
+    q = _abi.QuantArgs(struct_size=ctypes.sizeof(_abi.QuantArgs), x_dtype=_abi.F32, rows=0, cols=64)
+    assert lib.w8a8_quantize_rows(ctypes.byref(q)) == _abi.OK
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match='no CPU fallback'):
+        _abi.load(tmp_path / 'libw8a8.so')

@@ -1,0 +1,224 @@
+"""GPU parity of each libw8a8 kernel against the CPU oracle (bit-exact).
+
+Inputs are drawn on the CPU (seeded), copied to the GPU, and the GPU result
+is compared with the oracle on the same bytes: int8 codes, int32
+accumulators, fp32 scales and the stored fp16/bf16/fp32 outputs must be
+bit-identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from helpers import assert_bits_equal, np_of, randi8, randn16, tname
+from w8a8 import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------ GEMM int32
+GEMM_SHAPES = [(1, 16, 16), (13, 48, 64), (64, 64, 128), (256, 256, 64), (300, 520, 192), (257, 260, 80),
+               (1000, 1100, 3072), (4096, 3072, 3072)]
+
+
+@pytest.mark.parametrize('m,n,k', GEMM_SHAPES)
+def test_gemm_int32_exact(gpu, m, n, k):
+    g = torch.Generator().manual_seed(m * 7 + n * 3 + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32)
+    assert_bits_equal(np_of(got), o.int_mm(np_of(a), np_of(b)), f'gemm {m}x{n}x{k}')
+
+
+def test_gemm_signed_extremes_and_layout(gpu):
+    k = 5120
+    a = torch.full((33, k), -128, dtype=torch.int8)
+    b = torch.full((40, k), -128, dtype=torch.int8)
+    b[7] = 127
+    a[5, ::2] = 127
+    got = np_of(kernels.gemm(a.to(gpu), b.to(gpu)))
+    assert_bits_equal(got, o.int_mm(np_of(a), np_of(b)), 'extremes')
+    assert got[0, 0] == k * 128 * 128
+    # one-hot operands pin the row/column placement of every accumulator
+    eye_a = torch.zeros((48, 64), dtype=torch.int8)
+    eye_b = torch.zeros((80, 64), dtype=torch.int8)
+    for i in range(48):
+        eye_a[i, i % 64] = 1 + (i % 5)
+    for j in range(80):
+        eye_b[j, j % 64] = 1 + (j % 3)
+    got = np_of(kernels.gemm(eye_a.to(gpu), eye_b.to(gpu)))
+    assert_bits_equal(got, o.int_mm(np_of(eye_a), np_of(eye_b)), 'one-hot')
+
+
+def test_gemm_strided_operands_and_empty(gpu):
+    g = torch.Generator().manual_seed(5)
+    big = randi8(g, (70, 160))
+    a = big[:, :96]              # row stride 160
+    b = randi8(g, (33, 96))
+    got = kernels.gemm(a.to(gpu), b.to(gpu))
+    assert_bits_equal(np_of(got), o.int_mm(np_of(a).copy(), np_of(b)), 'strided')
+    empty = kernels.gemm(torch.zeros((0, 64), dtype=torch.int8, device=gpu),
+                         torch.zeros((8, 64), dtype=torch.int8, device=gpu))
+    assert empty.shape == (0, 8)
+
+
+# ------------------------------------------------------------------ epilogues
+@pytest.mark.parametrize('epi', ['row', 'column'])
+@pytest.mark.parametrize('out_dtype', [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('bias_dtype', [None, torch.float16, torch.float32])
+def test_gemm_fused_epilogue(gpu, epi, out_dtype, bias_dtype):
+    g = torch.Generator().manual_seed(11)
+    m, n, k = 197, 300, 256
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
+    ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
+    bias = None if bias_dtype is None else (torch.randn((n,), generator=g) * 0.5).to(bias_dtype)
+    code = kernels.EPI_ROW if epi == 'row' else kernels.EPI_COLUMN
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=code, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       bias=None if bias is None else bias.to(gpu), out_dtype=out_dtype)
+    acc = o.int_mm(np_of(a), np_of(b))
+    fn = o.dequantize_row if epi == 'row' else o.dequantize_column
+    want = fn(acc, np_of(rs).reshape(-1), np_of(ws).reshape(-1), tname(out_dtype),
+              None if bias is None else np_of(bias))
+    assert_bits_equal(np_of(got), want, f'{epi} {out_dtype} {bias_dtype}')
+
+
+def test_gemm_scalar_weight_scale_and_residual(gpu):
+    g = torch.Generator().manual_seed(12)
+    m, n, k = 130, 96, 512
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.01
+    ws = torch.tensor([[3.0e-5]])
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_COLUMN, row_scale=rs.to(gpu),
+                       col_scale=ws.to(gpu), out_dtype=torch.float16)
+    acc = o.int_mm(np_of(a), np_of(b))
+    assert_bits_equal(np_of(got), o.dequantize_column(acc, np_of(rs), np_of(ws), 'f16'), 'scalar scale')
+    res = randn16(g, (m, n), 1 / 512)
+    ws2 = (torch.rand((n, 1), generator=g) * 1e-3) / 512
+    res_gpu = res.to(gpu)
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu),
+                       col_scale=ws2.to(gpu), out_dtype=torch.float16, residual=res_gpu, out=res_gpu)
+    want = o.residual_add(np_of(res), o.dequantize_row(acc, np_of(rs), np_of(ws2), 'f16'))
+    assert_bits_equal(np_of(got), want, 'in-place residual')
+
+
+ADVERSARIAL = ('random', 'zero', 'bounds', 'cancellation', 'ties_outliers')
+
+
+@pytest.mark.parametrize('pattern', ADVERSARIAL)
+@pytest.mark.parametrize('epi', ['row', 'column'])
+def test_dequantize_adversarial_int32(gpu, pattern, epi):
+    # Patterns of benchmarks/test_tp2_p2_epilogue.py:18-25 (INT32 values near
+    # and beyond 2^24, exact bounds, cancellations, ties).
+    g = torch.Generator().manual_seed(744)
+    rows, width, k = 17, 256, 7168
+    acc = torch.randint(-10000000, 10000000, (rows, width), generator=g, dtype=torch.int32)
+    if pattern == 'zero':
+        acc.zero_()
+    if pattern == 'bounds':
+        acc.fill_(k * 128 * 128)
+    if pattern == 'cancellation':
+        acc = -acc + 17
+    if pattern == 'ties_outliers':
+        acc.zero_()
+        acc[:, 0] = 16777217
+        acc[:, 1] = -8388609
+        acc[:, 2:10] = torch.tensor([1, -1, 3, -3, 127, -127, 65535, -65535], dtype=torch.int32)
+    a = torch.rand((rows, 1), generator=g) * 0.1
+    w = torch.rand((width,), generator=g) * 0.001
+    code = kernels.EPI_ROW if epi == 'row' else kernels.EPI_COLUMN
+    fn = o.dequantize_row if epi == 'row' else o.dequantize_column
+    for out_dtype in (torch.float32, torch.float16):
+        got = kernels.dequantize(acc.to(gpu), a.to(gpu), w.to(gpu), epilogue=code, out_dtype=out_dtype)
+        want = fn(np_of(acc), np_of(a), np_of(w), tname(out_dtype))
+        assert_bits_equal(np_of(got), want, f'{pattern} {epi} {out_dtype}')
+
+
+# ------------------------------------------------------------------ quantize
+QUANT_CASES = [
+    (1, 16, False), (7, 3072, False), (33, 4096, False), (5, 5120, False), (9, 8192, False),
+    (3, 16384, False), (2, 2064, False),
+    (1, 256, True), (7, 3072, True), (33, 4096, True), (4, 8192, True), (3, 12800, True), (2, 16384, True),
+]
+
+
+@pytest.mark.parametrize('rows,cols,rot', QUANT_CASES)
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16, torch.float32])
+def test_quantize_rows(gpu, rows, cols, rot, dtype):
+    g = torch.Generator().manual_seed(rows * 31 + cols)
+    x = randn16(g, (rows, cols), 3.0, dtype)
+    if cols >= 64:
+        x[:, 5] *= 20
+    x[0, -1] = 0
+    if rows > 2:
+        x[2] = 0          # zero row: scale floor
+    got_q, got_s = kernels.quantize_rows(x.to(gpu), convrot=rot, round_rotated=True)
+    want_q, want_s = o.prepare_activation(np_of(x), convrot=rot, x_dtype=tname(dtype))
+    assert_bits_equal(np_of(got_s).reshape(-1), want_s, f'scale {rows}x{cols} rot={rot} {dtype}')
+    assert_bits_equal(np_of(got_q), want_q, f'codes {rows}x{cols} rot={rot} {dtype}')
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.float32])
+def test_quantize_fp32_rotation_and_external_max(gpu, dtype):
+    g = torch.Generator().manual_seed(21)
+    x = randn16(g, (19, 3072), 2.0, dtype)
+    q, s = kernels.quantize_rows(x.to(gpu), convrot=True, round_rotated=False)
+    rot = o.convrot256(np_of(x).astype(np.float32))
+    wq, ws = o.quantize_rows(rot)
+    assert_bits_equal(np_of(s).reshape(-1), ws, 'fp32-rotation scale')
+    assert_bits_equal(np_of(q), wq, 'fp32-rotation codes')
+    ext = torch.rand((19,), generator=g) * 4 + 0.5
+    q, s = kernels.quantize_rows(x.to(gpu), row_max=ext.to(gpu))
+    wq, ws = o.quantize_rows(np_of(x).astype(np.float32), row_max=np_of(ext))
+    assert_bits_equal(np_of(s).reshape(-1), ws, 'external-max scale')
+    assert_bits_equal(np_of(q), wq, 'external-max codes (saturating)')
+
+
+def test_quantize_ties_and_strided_rows(gpu):
+    # Rows whose quotients land exactly on half-integers exercise the exact
+    # division path of the reciprocal quantizer.
+    x = torch.zeros((4, 64), dtype=torch.float32)
+    x[:, 0] = 254.0                      # scale exactly 2.0
+    x[:, 1:33] = 2 * torch.arange(-16, 16, dtype=torch.float32) + 1   # x / 2 = k + 0.5
+    x[1, 1:40] = torch.arange(1, 40, dtype=torch.float32) * 1.0
+    x[2] = torch.linspace(-254, 254, 64)
+    big = torch.zeros((4, 96), dtype=torch.float32)
+    big[:, :64] = x
+    q, s = kernels.quantize_rows(big.to(gpu)[:, :64])
+    wq, ws = o.quantize_rows(np_of(x))
+    assert_bits_equal(np_of(s).reshape(-1), ws, 'tie scales')
+    assert_bits_equal(np_of(q), wq, 'tie codes')
+
+
+# ------------------------------------------------------------------ FC2 prologue
+SWIGLU_CASES = [(1, 256), (3, 512), (64, 3072), (5, 8192), (2, 12800), (2, 20480), (130, 4096)]
+
+
+@pytest.mark.parametrize('rows,width', SWIGLU_CASES)
+def test_swiglu_quantize(gpu, rows, width):
+    g = torch.Generator().manual_seed(rows + width)
+    x = randn16(g, (rows, 2 * width), 3.0)
+    x[0, 0] = 60000.0        # huge gate: exp underflow branch
+    x[0, 1] = -60000.0       # huge negative gate: exp overflow branch
+    res = kernels.swiglu_quantize(x.to(gpu), want_row_max=True, want_group_max=True)
+    wq, ws, wg = o.fc2_prologue(np_of(x))
+    assert_bits_equal(np_of(res['group_max']), wg, f'group max {rows}x{width}')
+    assert_bits_equal(np_of(res['row_max']).reshape(-1), wg.max(-1), 'row max')
+    assert_bits_equal(np_of(res['scale']).reshape(-1), ws, 'scale')
+    assert_bits_equal(np_of(res['q']), wq, f'codes {rows}x{width}')
+
+
+def test_swiglu_external_max_fp32_input_and_phases(gpu):
+    g = torch.Generator().manual_seed(77)
+    x = randn16(g, (9, 2 * 1024), 2.0, torch.float32)
+    ext = torch.rand((9, 1), generator=g) * 3 + 1
+    res = kernels.swiglu_quantize(x.to(gpu), row_max=ext.to(gpu))
+    wq, ws, _ = o.fc2_prologue(np_of(x), x_dtype='f32', row_max=np_of(ext))
+    assert_bits_equal(np_of(res['scale']).reshape(-1), ws, 'external scale')
+    assert_bits_equal(np_of(res['q']), wq, 'external codes')
+    only = kernels.swiglu_quantize(x.to(gpu), quantize=False, want_row_max=True)
+    assert set(only) == {'row_max'}
+    assert_bits_equal(np_of(only['row_max']).reshape(-1), o.fc2_prologue(np_of(x), x_dtype='f32')[2].max(-1),
+                      'maximum phase')

@@ -1,0 +1,286 @@
+"""Pins of the CPU oracle: hand-computed answers, closed forms, invariants.
+
+Each check is chosen so a plausible slip (a /127 instead of *fp32(1/127),
+round-half-up, a wrong butterfly sign or summation order, swapped gate/up,
+transposed operands, a swapped dequantization order) fails it.
+"""
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import oracle as o
+
+F32 = np.float32
+
+
+def f32_bits(x):
+    return int(np.asarray(x, np.float32).view(np.uint32))
+
+
+# ------------------------------------------------------------------ quantizer
+def test_quantize_hand_computed_row():
+    # amax 254: 254 * fp32(1/127) rounds to exactly 2.0, so q = rne(x / 2).
+    x = np.array([[254.0, -127.0, 63.5, 0.0, 5.0, 7.0, -5.0, -7.0, 1.0, 3.0, -1.0, 0.5, 2.0, -2.0, 9.0, 11.0]],
+                 np.float32)
+    q, s = o.quantize_rows(x)
+    assert s.tolist() == [2.0]
+    # 127, -63.5->-64 (even), 31.75->32, 0, 2.5->2, 3.5->4, -2.5->-2, -3.5->-4,
+    # 0.5->0, 1.5->2, -0.5->-0, 0.25->0, 1, -1, 4.5->4, 5.5->6
+    assert q.tolist() == [[127, -64, 32, 0, 2, 4, -2, -4, 0, 2, 0, 0, 1, -1, 4, 6]]
+
+
+def test_scale_is_product_with_fp32_reciprocal_not_division():
+    # For amax 13 the two forms differ in the last bit.
+    x = np.zeros((1, 16), np.float32)
+    x[0, 3] = 13.0
+    _, s = o.quantize_rows(x)
+    assert f32_bits(s[0]) == 0x3DD1A346
+    assert f32_bits(F32(13.0) / F32(127.0)) == 0x3DD1A347
+
+
+def test_zero_row_scale_floor_and_codes():
+    q, s = o.quantize_rows(np.zeros((2, 32), np.float32))
+    assert f32_bits(s[0]) == f32_bits(F32(1e-30)) and f32_bits(s[1]) == f32_bits(F32(1e-30))
+    assert not q.any()
+
+
+def test_absmax_element_maps_to_pm127():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((64, 512)) * rng.uniform(1e-3, 1e3, (64, 1))).astype(np.float32)
+    q, _ = o.quantize_rows(x)
+    idx = np.abs(x).argmax(1)
+    assert np.array_equal(np.abs(q[np.arange(64), idx]), np.full(64, 127))
+    assert np.abs(q.astype(np.int32)).max() == 127
+
+
+def test_external_max_saturates():
+    x = np.array([[5.0, -5.0, 0.004, -0.006] + [0.0] * 12], np.float32)
+    q, s = o.quantize_rows(x, row_max=np.array([1.27], np.float32))
+    assert f32_bits(s[0]) == f32_bits(F32(1.27) * F32(1 / 127))
+    assert q[0, :4].tolist() == [127, -128, 0, -1]
+
+
+def test_quantize_matches_exact_rational_rounding():
+    # Independent evaluation: exact rational x / s rounded half-even, against
+    # the fp32 quotient the oracle rounds. They may differ only when the fp32
+    # quotient itself rounds across a half-integer, which is rare.
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal((8, 256)) * 3).astype(np.float32)
+    q, s = o.quantize_rows(x)
+    mism = 0
+    for r in range(8):
+        sr = Fraction(float(s[r]))
+        for c in range(256):
+            v = Fraction(float(x[r, c])) / sr
+            fl = v.numerator // v.denominator
+            rem = v - fl
+            n = fl + (1 if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2) else 0)
+            mism += int(max(-128, min(127, n)) != q[r, c])
+    assert mism <= 2
+
+
+# ------------------------------------------------------------------ ConvRot256
+def test_hadamard_closed_form_properties():
+    h = o.hadamard256()
+    assert np.array_equal(h, h.T)
+    assert np.array_equal(h @ h, np.eye(256))
+    # Regular H4 (not Sylvester): entry (i=3, j=0) has one digit pair summing to 3.
+    assert h[3, 0] == -1 / 16 and h[0, 3] == -1 / 16 and h[1, 2] == -1 / 16 and h[1, 1] == 1 / 16
+
+
+def test_butterfly_equals_closed_form_on_integers():
+    rng = np.random.default_rng(3)
+    x = rng.integers(-2000, 2000, (9, 768)).astype(np.float32)
+    ref = (x.reshape(-1, 256).astype(np.float64) @ o.hadamard256()).reshape(x.shape)
+    assert np.array_equal(o.convrot256(x).astype(np.float64), ref)
+
+
+def test_butterfly_unit_vectors_and_norm():
+    eye = np.eye(256, dtype=np.float32)
+    assert np.array_equal(o.convrot256(eye).astype(np.float64), o.hadamard256())
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((16, 1024)).astype(np.float32)
+    r = o.convrot256(x)
+    n0 = np.linalg.norm(x.reshape(-1, 256).astype(np.float64), axis=1)
+    n1 = np.linalg.norm(r.reshape(-1, 256).astype(np.float64), axis=1)
+    assert np.allclose(n0, n1, rtol=1e-6)
+
+
+def test_butterfly_summation_order_left_to_right():
+    # First quad [1e8, 1, -1e8, 1]: fp32 ((p+q)+r)+s gives -1, 2e8, 1, -2e8
+    # (exact arithmetic would give 0, 2e8+2, 0, -2e8+2). The later stages only
+    # spread these with signs (all other inputs are zero).
+    x = np.zeros((1, 256), np.float32)
+    x[0, :4] = [1e8, 1.0, -1e8, 1.0]
+    r = o.convrot256(x)[0] * 16
+    first = [-1.0, 2e8, 1.0, -2e8]
+    for i in range(256):
+        digits = [(i >> (2 * d)) & 3 for d in (1, 2, 3)]
+        sign = -1.0 if sum(d == 3 for d in digits) % 2 else 1.0
+        assert r[i] == F32(sign * first[i % 4]), i
+
+
+# ------------------------------------------------------------------ exp / SwiGLU
+def test_exp_accuracy_sweep():
+    x = np.linspace(-87.0, 88.5, 400001).astype(np.float32)
+    e = o.exp_f32(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.abs(e - ref) / np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert ulp.max() <= 2.0
+
+
+def test_exp_special_values():
+    assert o.exp_f32(np.float32(0.0)) == 1.0
+    assert np.isinf(o.exp_f32(np.float32(89.0))) and np.isinf(o.exp_f32(np.float32(1000.0)))
+    assert o.exp_f32(np.float32(-104.0)) < 1e-44 and o.exp_f32(np.float32(-1e4)) == 0.0
+    assert abs(float(o.exp_f32(np.float32(1.0))) - np.e) < 3e-7
+
+
+def test_swiglu_against_float64_and_special_values():
+    rng = np.random.default_rng(5)
+    g = (rng.standard_normal(200000) * 4).astype(np.float32)
+    u = (rng.standard_normal(200000) * 4).astype(np.float32)
+    a = o.swiglu_f32(g, u).astype(np.float64)
+    gd, ud = g.astype(np.float64), u.astype(np.float64)
+    ref = gd / (1 + np.exp(-gd)) * ud
+    assert np.all(np.abs(a - ref) <= 4 * np.spacing(np.abs(ref).astype(np.float32)) + 1e-30)
+    assert o.swiglu_f32(np.float32(0), np.float32(5)) == 0.0
+    assert o.swiglu_f32(np.float32(100), np.float32(3)) == 300.0
+    assert o.swiglu_f32(np.float32(-120), np.float32(3)) == 0.0
+    # gate and up are not interchangeable
+    assert o.swiglu_f32(np.float32(2), np.float32(-1)) != o.swiglu_f32(np.float32(-1), np.float32(2))
+
+
+# ------------------------------------------------------------------ GEMM
+def test_int_mm_brute_force():
+    rng = np.random.default_rng(6)
+    for m, n, k in ((1, 1, 16), (3, 5, 32), (13, 7, 64), (33, 17, 48)):
+        a = rng.integers(-128, 128, (m, k)).astype(np.int8)
+        b = rng.integers(-128, 128, (n, k)).astype(np.int8)
+        ref = np.zeros((m, n), np.int64)
+        for i in range(m):
+            for j in range(n):
+                ref[i, j] = sum(int(a[i, t]) * int(b[j, t]) for t in range(k))
+        assert np.array_equal(o.int_mm(a, b), ref.astype(np.int32))
+
+
+def test_int_mm_signed_extremes():
+    k = 5120
+    a = np.full((2, k), -128, np.int8)
+    b = np.full((8, k), -128, np.int8)
+    assert np.array_equal(o.int_mm(a, b), np.full((2, 8), k * 128 * 128, np.int32))
+    b[1] = 127
+    assert o.int_mm(a, b)[0, 1] == -128 * 127 * k
+
+
+# ------------------------------------------------------------------ epilogues
+def test_dequantize_reference_hand_example():
+    # benchmarks/test_fp16_fc2_experiment.py:11-29: q=[1,-2,3,4], w=[2,3,-1,4],
+    # accumulator 9, doubled by the fake SUM, scale .25, weight scale .125,
+    # plus 1 -> fp16 1.5625.
+    acc = o.int_mm(np.array([[1, -2, 3, 4]], np.int8), np.array([[2, 3, -1, 4]], np.int8)) * 2
+    assert acc.tolist() == [[18]]
+    y = o.dequantize_row(acc, np.array([0.25], np.float32), np.array([0.125], np.float32), 'f16',
+                         bias=np.array([1.0], np.float32))
+    assert y.dtype == np.float16 and y.tolist() == [[1.5625]]
+
+
+def _f32_exact(x):
+    return np.float32(float(x))
+
+
+def test_row_and_column_orders_are_distinct_and_pinned():
+    # Products of small integers and fp32 scales are exact in float64, so a
+    # single cast rounds each product once.
+    rng = np.random.default_rng(7)
+    c = rng.integers(-(2 ** 20), 2 ** 20, (64, 48)).astype(np.int32)
+    a = rng.uniform(1e-4, 1e-2, 64).astype(np.float32)
+    w = rng.uniform(1e-4, 1e-2, 48).astype(np.float32)
+    row = o.dequantize_row(c, a, w, 'f32')
+    col = o.dequantize_column(c, a, w, 'f32')
+    exp_row = np.empty_like(row)
+    exp_col = np.empty_like(col)
+    for i in range(64):
+        for j in range(48):
+            exp_row[i, j] = _f32_exact(float(_f32_exact(float(c[i, j]) * float(a[i]))) * float(w[j]))
+            exp_col[i, j] = _f32_exact(float(c[i, j]) * float(_f32_exact(float(a[i]) * float(w[j]))))
+    assert np.array_equal(row, exp_row)
+    assert np.array_equal(col, exp_col)
+    assert not np.array_equal(row, col)
+
+
+def test_bias_added_after_products_and_fp16_cast():
+    c = np.array([[1000, -3]], np.int32)
+    y = o.dequantize_row(c, np.array([0.5], np.float32), np.array([0.25, 2.0], np.float32), 'f16',
+                         bias=np.array([1.0, -0.5], np.float16))
+    assert y.tolist() == [[126.0, -3.5]]
+    big = o.dequantize_row(np.array([[2 ** 30]], np.int32), np.array([1.0], np.float32),
+                           np.array([1.0], np.float32), 'f16')
+    assert np.isinf(big[0, 0])
+
+
+def test_bf16_rounding():
+    x = np.array([1.0, 1.00390625, 1.005859375, -2.5, 3.0e38], np.float32)
+    b = o.to_bf16_bits(x)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 1.5*2^-8 rounds up to 1 + 2^-7.
+    assert o.from_bf16_bits(b).tolist()[:4] == [1.0, 1.0, 1.0078125, -2.5]
+
+
+def test_residual_add_fp16():
+    x = np.array([1.0, 2048.0], np.float16)
+    br = np.array([0.0004883, 1.0], np.float16)
+    out = o.residual_add(x, br)
+    assert out.dtype == np.float16 and out.tolist() == [1.0, 2048.0]
+
+
+# ------------------------------------------------------------------ composition
+def test_fc2_prologue_against_float64_rotation():
+    rng = np.random.default_rng(8)
+    m, w = 6, 512
+    x = (rng.standard_normal((m, 2 * w)) * 2).astype(np.float16)
+    q, s, gmax, rot = o.fc2_prologue(x, return_rotated=True)
+    g = x[:, :w].astype(np.float64)
+    u = x[:, w:].astype(np.float64)
+    act = g / (1 + np.exp(-g)) * u
+    ref = (act.reshape(-1, 256) @ o.hadamard256()).reshape(m, w)
+    assert np.allclose(rot, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+    assert np.array_equal(gmax, np.abs(rot).reshape(m, w // 256, 256).max(-1))
+    ref_q = np.clip(np.rint(ref / s[:, None].astype(np.float64)), -128, 127)
+    agree = (ref_q == q).mean()
+    assert agree > 0.995 and np.abs(ref_q - q).max() <= 1
+    # rotation preserves each group's norm (the 1/16 factor is present)
+    n0 = np.linalg.norm(act.reshape(-1, 256), axis=1)
+    n1 = np.linalg.norm(rot.reshape(-1, 256).astype(np.float64), axis=1)
+    assert np.allclose(n0, n1, rtol=1e-5)
+
+
+def test_fc2_prologue_external_max():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((3, 512)).astype(np.float16)
+    q1, s1, g1 = o.fc2_prologue(x)
+    q2, s2, _ = o.fc2_prologue(x, row_max=g1.max(-1) * 2)
+    assert np.array_equal(s2, np.maximum(g1.max(-1) * 2 * o.R127, o.SCALE_FLOOR))
+    assert np.abs(q2.astype(int)).max() <= 64
+
+
+def test_column_path_rounds_rotation_to_input_dtype():
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((4, 256)).astype(np.float16)
+    q16, s16 = o.prepare_activation(x, convrot=True, x_dtype='f16')
+    rot16 = o.convrot256(x.astype(np.float32)).astype(np.float16).astype(np.float32)
+    assert np.array_equal(s16, np.abs(rot16).max(1) * o.R127)
+    qn, sn = o.prepare_activation(x, convrot=False, x_dtype='f16')
+    assert np.array_equal(qn, o.quantize_rows(x.astype(np.float32))[0])
+
+
+def test_end_to_end_linear_close_to_float64():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((32, 512)).astype(np.float16)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float32)
+    wq, ws = o.quantize_weight(w)
+    y = o.column_linear(x, wq, ws, convrot=False).astype(np.float64)
+    ref = x.astype(np.float64) @ w.T.astype(np.float64)
+    assert np.abs(y - ref).max() / np.abs(ref).max() < 0.03
+    with pytest.raises(ValueError):
+        o.int_mm(np.zeros((2, 8), np.int8), np.zeros((3, 16), np.int8))
