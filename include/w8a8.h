@@ -145,7 +145,8 @@ int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
  * out: [m, n] of out_dtype (I32 for EPI_INT32; F16, BF16 or F32 otherwise),
  *   row stride ldc.
  * Requirements: k % 16 == 0; a, b 16-byte aligned; lda, ldb % 16 == 0;
- *   out 16-byte aligned; ldc % 4 == 0.
+ *   out element-aligned (rows are written with vector stores when out is
+ *   16-byte aligned and ldc % 4 == 0).
  */
 typedef struct W8A8GemmArgs {
   uint32_t struct_size;

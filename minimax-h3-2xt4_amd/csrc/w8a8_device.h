@@ -12,6 +12,7 @@
 namespace w8a8 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------- constants
 // fp32(1/127) = 0x3C010204 and the 1e-30 scale floor of the row quantizer.

@@ -147,8 +147,8 @@ def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dty
         if out_dtype != torch.float16 or residual.dtype != torch.float16:
             raise ValueError('the fused residual add is FP16 only')
         residual = _rows_2d(residual)
-        if residual.shape != (m, n) or residual.stride(0) % 4 or residual.data_ptr() % 8:
-            raise ValueError('residual must be [M, N] with an aligned row stride')
+        if residual.shape != (m, n):
+            raise ValueError('residual must be [M, N]')
         ldr = residual.stride(0)
         keep.append(residual)
     _device(a, w, bias, residual)

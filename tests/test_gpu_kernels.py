@@ -68,7 +68,8 @@ def test_gemm_strided_operands_and_empty(gpu):
 @pytest.mark.parametrize('bias_dtype', [None, torch.float16, torch.float32])
 def test_gemm_fused_epilogue(gpu, epi, out_dtype, bias_dtype):
     g = torch.Generator().manual_seed(11)
-    m, n, k = 197, 300, 256
+    # 521 x 300: full 256x256 tiles (staged epilogue) and ragged edge tiles
+    m, n, k = 521, 300, 256
     a = randi8(g, (m, k))
     b = randi8(g, (n, k))
     rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
