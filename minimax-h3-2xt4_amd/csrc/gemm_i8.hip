@@ -368,7 +368,7 @@ void gemm_i8_256x256(GemmParams p) {
 // registers. Each wave instruction writes 1 KB of LDS (16 rows x 64 bytes);
 // lane i fills physical chunk i % 4 of its row, so it loads the logical
 // chunk that the XOR swizzle places there. Requires K % 64 == 0.
-constexpr int kStages = 4;
+constexpr int kStages = 5;
 constexpr int kStageBytes = 2 * kTileBytes;
 
 template <int N>
@@ -414,8 +414,8 @@ void gemm_i8_256x256_dma(GemmParams p) {
     src_b[j] = p.b + (int64_t)min(n0 + row, p.n - 1) * p.ldb + dchunk * 16;
   }
   const int ktiles = p.k / kBK;
-  auto issue = [&](int kt) {
-    int8_t* st = smem + (kt % kStages) * kStageBytes + wave * 4 * 1024;
+  auto issue = [&](int kt, int buf) {
+    int8_t* st = smem + buf * kStageBytes + wave * 4 * 1024;
     const int kof = kt * kBK;
 #pragma unroll
     for (int j = 0; j < 4; ++j) dma16(src_a[j] + kof, st + j * 1024);
@@ -452,48 +452,59 @@ void gemm_i8_256x256_dma(GemmParams p) {
         wsc[nb][g][v] = EPI != kEpiInt32 ? p.col_scale[(int64_t)n * p.col_stride] : 0.0f;
       }
 
-  // Every iteration issues exactly one stage of DMA (past the last K step it
-  // re-reads the last stage into the free buffer, which is never consumed),
-  // so the loop body is one basic block with a constant vmcnt: stages
-  // kt+1 and kt+2 may still be in flight when stage kt is consumed.
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) issue(min(s, ktiles - 1));
-  for (int kt = 0; kt < ktiles; ++kt) {
-    wait_vmcnt<8 * (kStages - 2)>();
-    block_barrier();
-    issue(min(kt + kStages - 1, ktiles - 1));
-    const int8_t* sa = smem + (kt % kStages) * kStageBytes;
+  // Software pipeline over K steps. Stage s is DMA'd in the middle of step
+  // s - 4 into the buffer step s - 5 used (every wave finished reading it
+  // before that barrier). Within step kt: the MFMAs of sub-step 0 run while
+  // sub-step 1's fragments are read; then the barrier that publishes stage
+  // kt+1; then the MFMAs of sub-step 1 run while the fragments of step
+  // kt+1's sub-step 0 are read. Past the last K step the DMA re-reads the
+  // last stage into a buffer that is never consumed, so every step issues
+  // exactly one stage and the vmcnt bounds are constant.
+  auto read_frags = [&](int buf, int frag, v4i (&fa)[4], v4i (&fb)[4]) {
+    const int8_t* sa = smem + buf * kStageBytes;
     const int8_t* sb = sa + kTileBytes;
-    v4i fa0[4], fb0[4], fa1[4], fb1[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fa0[i] = *reinterpret_cast<const v4i*>(sb + b_row + frag0 + i * 32 * kBK);
-      fb0[i] = *reinterpret_cast<const v4i*>(sa + a_row + frag0 + i * 32 * kBK);
+      fa[i] = *reinterpret_cast<const v4i*>(sb + b_row + frag + i * 32 * kBK);
+      fb[i] = *reinterpret_cast<const v4i*>(sa + a_row + frag + i * 32 * kBK);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa1[i] = *reinterpret_cast<const v4i*>(sb + b_row + frag1 + i * 32 * kBK);
-      fb1[i] = *reinterpret_cast<const v4i*>(sa + a_row + frag1 + i * 32 * kBK);
-    }
+  };
+  auto mfma16 = [&](const v4i (&fa)[4], const v4i (&fb)[4]) {
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa0[nb], fb0[mb], acc[nb][mb], 0, 0, 0);
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa1[nb], fb1[mb], acc[nb][mb], 0, 0, 0);
-    // Order: the 8 fragments of sub-step 0, then its 16 MFMAs with the 8
-    // reads of sub-step 1 spread between them, then sub-step 1's MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[nb], fb[mb], acc[nb][mb], 0, 0, 0);
+  };
+  // 16 MFMAs with 8 fragment reads spread between them.
+  auto interleave = [&]() {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+  };
+
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s) issue(min(s, ktiles - 1), s);
+  wait_vmcnt<8 * (kStages - 2)>();  // stage 0 landed (stages 1..3 in flight)
+  block_barrier();
+  v4i fa0[4], fb0[4], fa1[4], fb1[4];
+  read_frags(0, frag0, fa0, fb0);
+  int cur = 0;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int nxt = cur + 1 == kStages ? 0 : cur + 1;
+    const int freeb = cur == 0 ? kStages - 1 : cur - 1;
+    mfma16(fa0, fb0);
+    read_frags(cur, frag1, fa1, fb1);
+    interleave();
+    wait_vmcnt<8 * (kStages - 3)>();  // stage kt+1 landed (kt+2, kt+3 in flight)
+    block_barrier();
+    issue(min(kt + kStages - 1, ktiles - 1), freeb);
+    mfma16(fa1, fb1);
+    read_frags(nxt, frag0, fa0, fb0);
+    interleave();
+    cur = nxt;
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
   if (p.vec16 && m0 + kBM <= p.m && n0 + kBN <= p.n) {
