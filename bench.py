@@ -148,8 +148,10 @@ def run_dit_ffn(args, torch, dev):
         else:
             v['frac'] = v['gbs'] / PEAK_HBM_GBS
     fc1 = kernels_out['fc1_gemm']
+    traffic = traffic_from_profiles('fc1_gemm')
     roofline = dict(bound='mfma', achieved=round(fc1['tops'], 1), peak=PEAK_INT8_TOPS, unit='TOPS',
-                    frac=round(fc1['frac'], 4), traffic=None, kernel='gemm_i8_256x256 (FC1 16384x16384x3072)',
+                    frac=round(fc1['frac'], 4), traffic=None if traffic is None else int(traffic),
+                    kernel='gemm_i8_256x256_dma (FC1 16384x16384x3072, column epilogue)',
                     algorithmic=f'{ops_fc1:.4g} int8 ops per launch (2*M*N*K)')
     tops = (ops_fc1 + ops_fc2) / (ms * 1e-3) / 1e12
     result = dict(metric=METRIC, value=round(tops, 1), unit='TOPS', n_gpus=1, steps=args.steps,
@@ -199,7 +201,199 @@ def cpu_baseline_ffn(args, data, block, m, ops_block):
                        f'numpy float64 BLAS for the exact int32 GEMM; CPU: {cpu_model()}')
 
 
-WORKLOADS = {'dit_ffn': run_dit_ffn}
+def traffic_from_profiles(kernel_key):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 summary.
+
+    profiles/hbm_traffic.txt holds, per kernel key, FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch) and the same counters' reading for a plain device copy
+    of known size (the calibration factor = counter bytes / true bytes).
+    """
+    path = ROOT / 'profiles' / 'hbm_traffic.txt'
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if '=' in line and not line.lstrip().startswith('#'):
+            k, v = line.split('=', 1)
+            try:
+                vals[k.strip()] = float(v.split()[0])
+            except ValueError:
+                pass
+    try:
+        fetch = vals[f'{kernel_key}.FETCH_KIB'] * 1024 / vals['copy.FETCH_FACTOR']
+        write = vals[f'{kernel_key}.WRITE_KIB'] * 1024 / vals['copy.WRITE_FACTOR']
+    except KeyError:
+        return None
+    return fetch + write
+
+
+def timed(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def run_copy(args, torch, dev):
+    """Calibration: a plain device-to-device copy of a known byte count."""
+    nbytes = 1 << 30
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = timed(torch, lambda: dst.copy_(src), args.steps, args.warmup)
+    return dict(metric='device copy bandwidth (calibration)', value=round(2 * nbytes / (ms * 1e-3) / 1e9, 1),
+                unit='GB/s', bytes_read=nbytes, bytes_written=nbytes, ms=round(ms, 4))
+
+
+def _cpu_rows_timing(fn, reps=3):
+    times = []
+    for rep in range(reps + 1):
+        t0 = time.perf_counter()
+        fn()
+        if rep:
+            times.append(time.perf_counter() - t0)
+    import numpy as np
+    return float(np.median(times))
+
+
+def run_w8a8_linear(args, torch, dev):
+    """Single W8A8 linear 4096x3072 -> 3072 with bias: quantize, GEMM + row-order dequant."""
+    from w8a8 import kernels, workloads
+    data = workloads.w8a8_linear()
+    m, k = data['x'].shape
+    n = data['w'].shape[0]
+    wq, ws = workloads.quantize_weight(data['w'], dev)
+    x, b = data['x'].to(dev), data['bias'].to(dev)
+    state = {}
+
+    def quant():
+        state['q'], state['a'] = kernels.quantize_rows(x)
+
+    def gemm():
+        return kernels.gemm(state['q'], wq, epilogue=kernels.EPI_ROW, row_scale=state['a'], col_scale=ws, bias=b)
+
+    quant()
+    tq = timed(torch, quant, args.steps, args.warmup)
+    tg = timed(torch, gemm, args.steps, args.warmup)
+    ops = 2.0 * m * n * k
+    qbytes = m * k * 2 + m * k + 4 * m
+    res = dict(metric='W8A8 linear 4096x3072x3072 (+bias) us', value=round((tq + tg) * 1e3, 1), unit='us',
+               higher_is_better=False, dtype='int8', config=dict(workload='w8a8_linear', m=m, k=k, n=n),
+               kernels=dict(quantize=dict(us=round(tq * 1e3, 1), gbs=round(qbytes / (tq * 1e-3) / 1e9, 1),
+                                          frac=round(qbytes / (tq * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)),
+                            gemm=dict(us=round(tg * 1e3, 1), tops=round(ops / (tg * 1e-3) / 1e12, 1),
+                                      frac=round(ops / (tg * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4))))
+    if not args.no_cpu_baseline:
+        import oracle as o
+        rows = min(args.cpu_rows, m)
+        xs, wqn, wsn, bn = data['x'][:rows].numpy(), wq.cpu().numpy(), ws.cpu().numpy().reshape(-1), data['bias'].numpy()
+        wf = wqn.astype('float64')
+
+        def cpu():
+            q, a = o.quantize_rows(xs.astype('float32'))
+            o.dequantize_row(o.int_mm(q, wqn, wf), a, wsn, 'f16', bn)
+        t = _cpu_rows_timing(cpu) * m / rows
+        res['cpu_baseline'] = dict(value=round(t * 1e6, 1), unit='us', cores=blas_threads(), kind='port',
+                                   sample=f'oracle quantize+int_mm+dequant on {rows} of {m} rows, scaled x{m / rows:g}')
+    return res
+
+
+def run_dit_qkv(args, torch, dev):
+    """DiT QKV projection M=53504, 3072 -> 9216: ConvRot256 quantize + GEMM (column order + bias)."""
+    from w8a8 import dit_column_linear, kernels, workloads
+    data = workloads.dit_qkv()
+    m, k = data['x'].shape
+    n = data['w'].shape[0]
+    wq, ws = workloads.quantize_weight(data['w'], dev)
+    x, b = data['x'].to(dev), data['bias'].to(dev)
+    state = {}
+
+    def quant():
+        state['q'], state['a'] = kernels.quantize_rows(x, convrot=True)
+
+    def gemm():
+        return kernels.gemm(state['q'], wq, epilogue=kernels.EPI_COLUMN, row_scale=state['a'], col_scale=ws, bias=b)
+
+    quant()
+    tq = timed(torch, quant, args.steps, args.warmup)
+    tg = timed(torch, gemm, args.steps, args.warmup)
+    tt = timed(torch, lambda: dit_column_linear.column_linear(x, wq, ws, bias=b), args.steps, args.warmup)
+    ops = 2.0 * m * n * k
+    qbytes = m * k * 2 + m * k + 4 * m
+    res = dict(metric='DiT QKV 53504x3072->9216 TOPS', value=round(ops / (tt * 1e-3) / 1e12, 1), unit='TOPS',
+               dtype='int8', config=dict(workload='dit_qkv', m=m, k=k, n=n), us=round(tt * 1e3, 1),
+               kernels=dict(quantize=dict(us=round(tq * 1e3, 1), gbs=round(qbytes / (tq * 1e-3) / 1e9, 1),
+                                          frac=round(qbytes / (tq * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)),
+                            gemm=dict(us=round(tg * 1e3, 1), tops=round(ops / (tg * 1e-3) / 1e12, 1),
+                                      frac=round(ops / (tg * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4))))
+    if not args.no_cpu_baseline:
+        import oracle as o
+        rows = min(args.cpu_rows, m)
+        xs, wqn, wsn, bn = data['x'][:rows].numpy(), wq.cpu().numpy(), ws.cpu().numpy().reshape(-1), data['bias'].numpy()
+        wf = wqn.astype('float64')
+        t = _cpu_rows_timing(lambda: o.column_linear(xs, wqn, wsn, bias=bn, w_f64=wf)) * m / rows
+        res['cpu_baseline'] = dict(value=round(ops / t / 1e12, 4), unit='TOPS', cores=blas_threads(), kind='port',
+                                   sample=f'oracle column projection on {rows} of {m} rows, scaled x{m / rows:g}')
+    return res
+
+
+def run_te_skinny(args, torch, dev):
+    """Text-encoder projections at M in {1, 64, 512}: up 4096 -> 14336, down 14336 -> 4096."""
+    from w8a8 import dit_column_linear, kernels, workloads
+    lines = []
+    for m in workloads.SHAPES['te_skinny']['ms']:
+        data = workloads.te_skinny(m)
+        wu, su = workloads.quantize_weight(data['w_up'], dev)
+        wd, sd = workloads.quantize_weight(data['w_down'], dev)
+        x, xd = data['x'].to(dev), data['x_down'].to(dev)
+        tu = timed(torch, lambda: dit_column_linear.column_linear(x, wu, su), args.steps, args.warmup)
+
+        def down():
+            q, a = kernels.quantize_rows(xd, convrot=True, round_rotated=False)
+            return kernels.gemm(q, wd, epilogue=kernels.EPI_ROW, row_scale=a, col_scale=sd)
+        td = timed(torch, down, args.steps, args.warmup)
+        for name, t, (n, k) in (('up', tu, wu.shape), ('down', td, wd.shape)):
+            nbytes = n * k + m * k * 2 + m * n * 2 + 4 * (m + n)
+            lines.append(dict(m=m, proj=name, n=n, k=k, us=round(t * 1e3, 2),
+                              weight_gbs=round(n * k / (t * 1e-3) / 1e9, 1),
+                              frac=round(nbytes / (t * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)))
+    return dict(metric='TE skinny INT8 projections (weight-streaming GB/s)', unit='GB/s', dtype='int8',
+                config=dict(workload='te_skinny'), value=round(min(l['weight_gbs'] for l in lines), 1), lines=lines)
+
+
+def run_dit_half_shard(args, torch, dev):
+    """One rank's half-shard DiT block projections at M=204336 in 16384-row chunks."""
+    from w8a8 import dit_column_linear, kernels, swiglu_quant, workloads
+    s = workloads.SHAPES['dit_half_shard']
+    m, hidden, chunk = s['m'], s['hidden'], s['chunk']
+    g = torch.Generator().manual_seed(s['seed'])
+    h = workloads.activations(g, m, hidden, s['outliers']).to(dev)
+    wqkv, sqkv = workloads.quantize_weight(workloads.weights(g, s['qkv'], hidden), dev)
+    w1, s1 = workloads.quantize_weight(workloads.weights(g, 2 * s['ffn'], hidden), dev)
+    w2, s2 = workloads.quantize_weight(workloads.weights(g, hidden, s['ffn']), dev)
+    out = torch.empty((m, hidden), dtype=torch.float32, device=dev)
+
+    def step():
+        for r0 in range(0, m, chunk):
+            hc = h[r0:r0 + chunk]
+            dit_column_linear.column_linear(hc, wqkv, sqkv)   # consumed by attention (not part of this path)
+            y1 = dit_column_linear.column_linear(hc, w1, s1)
+            out[r0:r0 + chunk] = swiglu_quant.row_linear(y1, w2, s2)
+    t = timed(torch, step, max(1, args.steps // 10), 1)
+    ops = 2.0 * m * hidden * (s['qkv'] + 2 * s['ffn'] + s['ffn'])
+    return dict(metric='DiT half-shard projections M=204336 (QKV, FC1, FC2 fp32 partial) TOPS',
+                value=round(ops / (t * 1e-3) / 1e12, 1), unit='TOPS', dtype='int8', ms=round(t, 3),
+                config=dict(workload='dit_half_shard', m=m, chunk=chunk, qkv=s['qkv'], ffn=s['ffn']))
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn, 'copy': run_copy, 'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv,
+             'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
 
 
 def main():
@@ -209,7 +403,7 @@ def main():
     ap.add_argument('--warmup', type=int, default=10)
     ap.add_argument('--workload', default='dit_ffn', choices=sorted(WORKLOADS))
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--cpu-rows', type=int, default=256)
+    ap.add_argument('--cpu-rows', type=int, default=4096)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py: this W8A8 path runs on one GPU; --gpus {args.gpus} is not supported '

@@ -1,0 +1,74 @@
+"""Write the small golden fixtures of the W8A8 path (run from the repository root).
+
+    python tests/golden/make_golden.py
+
+The reference holds no tensor fixtures for this path (its arithmetic pins need
+comfy-kitchen, TileLang and CUDA), so these vectors are produced by this
+build's oracle from seeded inputs, after the oracle itself is pinned by
+tests/test_oracle.py. They freeze the oracle's bits (a CPU test regenerates and
+compares) and give the GPU tests an input/output set that does not depend on
+running the oracle at test time. Inputs follow the reference's test patterns:
+row tails (benchmarks/test_bounded_column_int8.py:11-28), signed extremes
+(benchmarks/test_te_column_layout.py:28-34), adversarial INT32 values
+(benchmarks/test_tp2_p2_epilogue.py:18-25).
+"""
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parents[1]
+sys.path.insert(0, str(ROOT))
+
+import oracle as o  # noqa: E402
+
+
+def fixtures():
+    rng = np.random.default_rng(20261201)
+    out = {}
+    # 1. per-row quantize, fp16 rows incl. a zero row and outlier channels
+    x = (rng.standard_normal((13, 512)) * 2).astype(np.float16)
+    x[3] = 0
+    x[:, 7] *= 20
+    q, s = o.quantize_rows(x.astype(np.float32))
+    out['quant'] = dict(x=x, q=q, scale=s)
+    # 2. ConvRot256 column preparation (rotation rounded to fp16)
+    q, s = o.prepare_activation(x, convrot=True, x_dtype='f16')
+    out['quant_convrot'] = dict(x=x, q=q, scale=s)
+    # 3. FC2 prologue
+    xs = (rng.standard_normal((5, 1024)) * 3).astype(np.float16)
+    xs[0, 0], xs[0, 1] = 60000.0, -60000.0
+    q, s, g = o.fc2_prologue(xs)
+    out['swiglu'] = dict(x=xs, q=q, scale=s, group_max=g)
+    # 4. INT8 GEMM with signed extremes and a K tail
+    a = rng.integers(-128, 128, (33, 80)).astype(np.int8)
+    b = rng.integers(-128, 128, (48, 80)).astype(np.int8)
+    a[0] = -128
+    b[0] = -128
+    out['gemm'] = dict(a=a, b=b, c=o.int_mm(a, b))
+    # 5. epilogues on adversarial int32 accumulators
+    acc = rng.integers(-10_000_000, 10_000_000, (17, 256)).astype(np.int32)
+    acc[:, 0] = 16777217
+    acc[:, 1] = -8388609
+    acc[:, 2:10] = [1, -1, 3, -3, 127, -127, 65535, -65535]
+    acc[:, 10] = 7168 * 128 * 128
+    ra = (rng.random(17) * 0.1).astype(np.float32)
+    wa = (rng.random(256) * 0.001).astype(np.float32)
+    bias = (rng.standard_normal(256) * 0.01).astype(np.float16)
+    out['epilogue'] = dict(acc=acc, a=ra, w=wa, bias=bias,
+                           row_f16=o.dequantize_row(acc, ra, wa, 'f16', bias),
+                           row_f32=o.dequantize_row(acc, ra, wa, 'f32'),
+                           col_f16=o.dequantize_column(acc, ra, wa, 'f16', bias),
+                           col_bf16=o.dequantize_column(acc, ra, wa, 'bf16'))
+    return out
+
+
+def main():
+    for name, arrays in fixtures().items():
+        np.savez_compressed(HERE / f'{name}.npz', **arrays)
+        print('wrote', HERE / f'{name}.npz')
+
+
+if __name__ == '__main__':
+    main()
