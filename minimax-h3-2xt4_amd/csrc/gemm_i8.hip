@@ -515,6 +515,92 @@ void gemm_i8_256x256_dma(GemmParams p) {
   }
 }
 
+// Skinny GEMM for M <= 64 (text-encoder decode / short prefill): weight
+// streaming. A 512-thread workgroup owns NR weight rows (NR = 16 or 32); its
+// 8 wavefronts split K into contiguous ranges and multiply with
+// v_mfma_i32_16x16x64_i8 (weight rows as the MFMA A operand, up to four
+// 16-row activation blocks as B), loading both operands straight from memory
+// into registers, 4 K steps per batch so many loads are in flight. The 8
+// partial sums meet in LDS; the shared epilogue writes the outputs. The
+// activation rows (<= 64 x K) stay L2-resident across workgroups.
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyMaxMB = 4;
+constexpr int kSkinnyU = 4;
+
+template <int EPI, int OUT, int NR>
+__global__ __launch_bounds__(512) void gemm_i8_skinny(GemmParams p) {
+  constexpr int NB = NR / 16;
+  __shared__ int red[kSkinnyWaves][NR][kSkinnyMaxMB * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * NR;
+  const int mblocks = (p.m + 15) >> 4;
+  const int ksteps = p.k >> 6;
+  const int per = (ksteps + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int s0 = min(wave * per, ksteps), s1 = min(s0 + per, ksteps);
+  const int fr = lane & 15, fc = lane >> 4;
+
+  const int8_t* wrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) wrow[nb] = p.b + (int64_t)min(n0 + nb * 16 + fr, p.n - 1) * p.ldb + fc * 16;
+  const int8_t* arow[kSkinnyMaxMB];
+#pragma unroll
+  for (int mb = 0; mb < kSkinnyMaxMB; ++mb) arow[mb] = p.a + (int64_t)min(mb * 16 + fr, p.m - 1) * p.lda + fc * 16;
+
+  v4i acc[NB][kSkinnyMaxMB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < kSkinnyMaxMB; ++mb) acc[nb][mb] = v4i{0, 0, 0, 0};
+
+  for (int s = s0; s < s1; s += kSkinnyU) {
+    v4i wf[kSkinnyU][NB], af[kSkinnyU][kSkinnyMaxMB];
+#pragma unroll
+    for (int u = 0; u < kSkinnyU; ++u) {
+      const int kof = min(s + u, s1 - 1) * 64;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wf[u][nb] = *reinterpret_cast<const v4i*>(wrow[nb] + kof);
+#pragma unroll
+      for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+        if (mb < mblocks) af[u][mb] = *reinterpret_cast<const v4i*>(arow[mb] + kof);
+    }
+#pragma unroll
+    for (int u = 0; u < kSkinnyU; ++u) {
+      if (s + u < s1) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+            if (mb < mblocks)
+              acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[u][nb], af[u][mb], acc[nb][mb], 0, 0, 0);
+      }
+    }
+  }
+  // Lane holds C[m][n..n+3] for m = 16 mb + fr, n = 16 nb + 4 fc (local).
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][nb * 16 + 4 * fc + v][mb * 16 + fr] = acc[nb][mb][v];
+  __syncthreads();
+  // Thread -> (m, 4 consecutive n): sum the 8 partials, then the epilogue.
+  for (int idx = tid; idx < p.m * (NR / 4); idx += 512) {
+    const int m = idx / (NR / 4);
+    const int nl = (idx % (NR / 4)) * 4;
+    const int n = n0 + nl;
+    const int valid = min(4, p.n - n);
+    if (valid <= 0) continue;
+    int c[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < kSkinnyWaves; ++w)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) c[v] += red[w][nl + v][m];
+    const float a = EPI != kEpiInt32 ? p.row_scale[m] : 0.0f;
+    epilogue4<EPI, OUT>(p, m, n, valid, c, a);
+  }
+}
+
 // Standalone epilogue: thread -> 4 consecutive columns of one row.
 template <int EPI, int OUT>
 __global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, const int32_t* __restrict__ acc,
@@ -591,12 +677,26 @@ static int launch_tile(const GemmParams& p, dim3 grid, hipStream_t s) {
   return W8A8_OK;
 }
 
+template <int EPI, int OUT>
+static int launch_tile_or_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
+  if (p.m <= kSkinnyMaxMB * 16 && p.k % 64 == 0) {
+    // 32 weight rows per workgroup while that still fills 256 workgroups.
+    if (p.n / 32 >= 256) {
+      hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 32>), dim3((unsigned)((p.n + 31) / 32)), dim3(512), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 16>), dim3((unsigned)((p.n + 15) / 16)), dim3(512), 0, s, p);
+    }
+    return W8A8_OK;
+  }
+  return launch_tile<EPI, OUT>(p, grid, s);
+}
+
 template <int EPI>
 static int launch_gemm_out(int out, const GemmParams& p, dim3 grid, hipStream_t s) {
   switch (out) {
-    case kF16: return launch_tile<EPI, kF16>(p, grid, s);
-    case kBF16: return launch_tile<EPI, kBF16>(p, grid, s);
-    default: return launch_tile<EPI, kF32>(p, grid, s);
+    case kF16: return launch_tile_or_skinny<EPI, kF16>(p, grid, s);
+    case kBF16: return launch_tile_or_skinny<EPI, kBF16>(p, grid, s);
+    default: return launch_tile_or_skinny<EPI, kF32>(p, grid, s);
   }
 }
 
@@ -649,7 +749,7 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   int rc2;
   switch (a->epilogue) {
-    case W8A8_EPI_INT32: rc2 = launch_tile<kEpiInt32, kI32>(p, grid, s); break;
+    case W8A8_EPI_INT32: rc2 = launch_tile_or_skinny<kEpiInt32, kI32>(p, grid, s); break;
     case W8A8_EPI_ROW: rc2 = launch_gemm_out<kEpiRow>(a->out_dtype, p, grid, s); break;
     default: rc2 = launch_gemm_out<kEpiColumn>(a->out_dtype, p, grid, s); break;
   }

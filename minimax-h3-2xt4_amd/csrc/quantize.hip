@@ -105,8 +105,79 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   }
 }
 
+// Few rows (decode / short prefill): one 256-thread workgroup per row, thread
+// t owning units u = t + 256 j (J units, kept in registers), so a row is
+// spread over four wavefronts instead of one.
+template <int DT, int ROT, int J>
+__global__ __launch_bounds__(256) void quantize_row_wg_kernel(
+    const void* __restrict__ x, int64_t ldx, int64_t cols, const float* __restrict__ row_max,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+  __shared__ float lds[ROT ? 4 * 1024 : 1];
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int64_t row = blockIdx.x;
+  const int units = (int)(cols >> 4);
+  const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * dt_bytes<DT>();
+  float* buf = ROT ? lds + wave * 1024 + (lane >> 4) * 256 : nullptr;
+  const int t = lane & 15;
+  float v[J][16];
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int u = tid + 256 * j;
+    if (u < units) {
+      load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v[j]);
+      if constexpr (ROT != 0) {
+        convrot256_lanes<true>(v[j], buf, t);
+        if constexpr (ROT == 2) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) v[j][i] = round_to<DT>(v[j][i]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+    }
+  }
+  amax = wave_max(amax);
+  if (lane == 0) wmax[wave] = amax;
+  __syncthreads();
+  amax = row_max ? row_max[row] : fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  const float s = row_scale_of(amax);
+  const float rcp = 1.0f / s;
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int u = tid + 256 * j;
+    if (u < units) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = pack4(quant1(v[j][4 * i], s, rcp), quant1(v[j][4 * i + 1], s, rcp),
+                     quant1(v[j][4 * i + 2], s, rcp), quant1(v[j][4 * i + 3], s, rcp));
+      *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  if (tid == 0) scale[row] = s;
+}
+
 template <int DT, int ROT>
 static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
+  // Below 1024 rows a wavefront per row leaves most of the GPU idle: spread
+  // each row over a workgroup (up to 16384 columns).
+  if (a->rows < 1024 && a->cols <= 16384) {
+    const int jw = (int)((a->cols / 16 + 255) / 256);
+    const dim3 g((unsigned)a->rows), b(256);
+#define W8A8_WLAUNCH(JJ)                                                                              \
+  hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, JJ>), g, b, 0, stream, a->x, a->ldx, a->cols, \
+                     a->row_max, a->q, a->ldq, a->scale)
+    switch (jw) {
+      case 1: W8A8_WLAUNCH(1); break;
+      case 2: W8A8_WLAUNCH(2); break;
+      case 3: W8A8_WLAUNCH(3); break;
+      default: W8A8_WLAUNCH(4); break;
+    }
+#undef W8A8_WLAUNCH
+    return launch_status("w8a8_quantize_rows");
+  }
   const int units = (int)(a->cols >> 4);
   const int jneed = (units + 63) / 64;
   const dim3 grid((unsigned)((a->rows + kQuantWaves - 1) / kQuantWaves));

@@ -18,7 +18,9 @@ pytestmark = pytest.mark.gpu
 
 # ------------------------------------------------------------------ GEMM int32
 GEMM_SHAPES = [(1, 16, 16), (13, 48, 64), (64, 64, 128), (256, 256, 64), (300, 520, 192), (257, 260, 80),
-               (1000, 1100, 3072), (4096, 3072, 3072)]
+               (1000, 1100, 3072), (4096, 3072, 3072),
+               # weight-streaming (M <= 64) shapes: text-encoder up/down, ragged N
+               (1, 14336, 4096), (64, 4096, 14336), (37, 1000, 1024), (5, 520, 192), (65, 4096, 512)]
 
 
 @pytest.mark.parametrize('m,n,k', GEMM_SHAPES)
@@ -85,6 +87,28 @@ def test_gemm_fused_epilogue(gpu, epi, out_dtype, bias_dtype):
     assert_bits_equal(np_of(got), want, f'{epi} {out_dtype} {bias_dtype}')
 
 
+@pytest.mark.parametrize('m', [1, 33, 64])
+@pytest.mark.parametrize('epi,out_dtype,bias_dtype', [('row', torch.float16, torch.float16),
+                                                      ('column', torch.bfloat16, None),
+                                                      ('row', torch.float32, torch.float32),
+                                                      ('column', torch.float16, torch.float32)])
+def test_gemm_skinny_epilogues(gpu, m, epi, out_dtype, bias_dtype):
+    g = torch.Generator().manual_seed(m + 17)
+    n, k = 1000, 2048
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
+    ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
+    bias = None if bias_dtype is None else (torch.randn((n,), generator=g) * 0.5).to(bias_dtype)
+    code = kernels.EPI_ROW if epi == 'row' else kernels.EPI_COLUMN
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=code, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       bias=None if bias is None else bias.to(gpu), out_dtype=out_dtype)
+    fn = o.dequantize_row if epi == 'row' else o.dequantize_column
+    want = fn(o.int_mm(np_of(a), np_of(b)), np_of(rs).reshape(-1), np_of(ws).reshape(-1), tname(out_dtype),
+              None if bias is None else np_of(bias))
+    assert_bits_equal(np_of(got), want, f'skinny m={m} {epi} {out_dtype} {bias_dtype}')
+
+
 def test_gemm_scalar_weight_scale_and_residual(gpu):
     g = torch.Generator().manual_seed(12)
     m, n, k = 130, 96, 512
@@ -142,6 +166,8 @@ QUANT_CASES = [
     (1, 16, False), (7, 3072, False), (33, 4096, False), (5, 5120, False), (9, 8192, False),
     (3, 16384, False), (2, 2064, False),
     (1, 256, True), (7, 3072, True), (33, 4096, True), (4, 8192, True), (3, 12800, True), (2, 16384, True),
+    # >= 1024 rows: one wavefront per row (registers, then the streaming path past 8192 columns)
+    (1100, 512, False), (1030, 3072, True), (1024, 9216, False), (1050, 12800, True),
 ]
 
 
