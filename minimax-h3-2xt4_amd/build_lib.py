@@ -4,6 +4,8 @@
 
 Each csrc/*.hip compiles to an object under _build/ (in parallel), then one
 hipcc link produces w8a8/libw8a8.so next to the Python bindings.
+csrc/gemm_inst.hip compiles once per (epilogue, output dtype) pair of the
+GEMM (INST_VARIANTS), each with its own -D pair.
 """
 import argparse
 import concurrent.futures as cf
@@ -32,6 +34,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# (epilogue, output dtype) pairs of gemm_inst.hip: epilogue 0 int32, 1 row,
+# 2 column; output 1 f16, 2 bf16, 3 f32, 4 i32.
+INST_VARIANTS = [(0, 4), (1, 1), (1, 2), (1, 3), (2, 1), (2, 2), (2, 3)]
+
+
 def hipcc():
     path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
     if not Path(path).exists():
@@ -39,9 +46,23 @@ def hipcc():
     return path
 
 
-def _compile(src, verbose):
-    obj = BUILD / (src.stem + '.o')
-    cmd = [hipcc(), *HIPCC_FLAGS, '-c', str(src), '-o', str(obj)]
+def _units():
+    """(source, object name, extra flags) of every object in the library."""
+    units = []
+    for src in sorted(CSRC.glob('*.hip')):
+        if src.name == 'gemm_inst.hip':
+            for epi, out in INST_VARIANTS:
+                units.append((src, f'{src.stem}_{epi}_{out}.o',
+                              [f'-DW8A8_INST_EPI={epi}', f'-DW8A8_INST_OUT={out}']))
+        else:
+            units.append((src, src.stem + '.o', []))
+    return units
+
+
+def _compile(unit, verbose):
+    src, name, extra = unit
+    obj = BUILD / name
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra, '-c', str(src), '-o', str(obj)]
     if verbose:
         print(' '.join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -54,10 +75,10 @@ def _compile(src, verbose):
 
 def build(jobs=None, verbose=False):
     BUILD.mkdir(exist_ok=True)
-    sources = sorted(CSRC.glob('*.hip'))
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 4) // 2))
+    units = _units()
+    jobs = jobs or min(len(units), max(1, os.cpu_count() or 4))
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, verbose), sources))
+        objs = list(pool.map(lambda u: _compile(u, verbose), units))
     tmp = OUT.with_suffix('.so.tmp')
     cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', *map(str, objs), '-o', str(tmp)]
     if verbose:

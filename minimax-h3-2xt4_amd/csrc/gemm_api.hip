@@ -1,0 +1,132 @@
+// C ABI of the INT8 GEMM and the standalone epilogue: argument checks, then
+// dispatch to the (epilogue, output dtype) launcher instantiated in
+// gemm_inst.hip.
+#include "gemm_launch.h"
+#include "w8a8_device.h"
+
+namespace w8a8 {
+
+static int check_epilogue(int epi, int out_dtype, int bias_dtype, const void* bias, const void* residual,
+                          int64_t ldr, int64_t n, const float* row_scale, const float* col_scale,
+                          int64_t col_stride, const void* out, int64_t ldc) {
+  W8A8_REQUIRE(out != nullptr, "null output");
+  const int es = out_dtype == W8A8_F16 || out_dtype == W8A8_BF16 ? 2 : 4;
+  W8A8_REQUIRE(((uintptr_t)out % es) == 0 && ldc >= n, "out must be element-aligned with ldc >= n");
+  if (epi == W8A8_EPI_INT32) {
+    W8A8_REQUIRE(out_dtype == W8A8_I32, "EPI_INT32 requires out_dtype I32");
+    W8A8_REQUIRE(bias == nullptr && residual == nullptr, "EPI_INT32 takes no bias or residual");
+    return W8A8_OK;
+  }
+  W8A8_REQUIRE(epi == W8A8_EPI_ROW || epi == W8A8_EPI_COLUMN, "unknown epilogue %d", epi);
+  W8A8_REQUIRE(out_dtype == W8A8_F16 || out_dtype == W8A8_BF16 || out_dtype == W8A8_F32,
+               "dequantized out_dtype must be F16, BF16 or F32");
+  W8A8_REQUIRE(row_scale && col_scale, "row_scale and col_scale required");
+  W8A8_REQUIRE(col_stride == 0 || col_stride == 1, "col_scale_stride must be 0 (scalar) or 1");
+  W8A8_REQUIRE(bias == nullptr || bias_dtype == W8A8_F16 || bias_dtype == W8A8_F32,
+               "bias_dtype must be F16 or F32");
+  if (residual) {
+    W8A8_REQUIRE(out_dtype == W8A8_F16, "residual requires F16 output");
+    W8A8_REQUIRE(((uintptr_t)residual & 1u) == 0 && ldr >= n, "residual must be 2-byte aligned with ldr >= n");
+  }
+  return W8A8_OK;
+}
+
+template <int EPI>
+static int launch_gemm_out(int out, const GemmParams& p, hipStream_t s) {
+  switch (out) {
+    case kF16: return launch_gemm<EPI, kF16>(p, s);
+    case kBF16: return launch_gemm<EPI, kBF16>(p, s);
+    default: return launch_gemm<EPI, kF32>(p, s);
+  }
+}
+
+template <int EPI>
+static void launch_dequant_out(int out, const GemmParams& p, const int32_t* acc, int64_t ldacc, hipStream_t s) {
+  switch (out) {
+    case kF16: launch_dequant<EPI, kF16>(p, acc, ldacc, s); break;
+    case kBF16: launch_dequant<EPI, kBF16>(p, acc, ldacc, s); break;
+    default: launch_dequant<EPI, kF32>(p, acc, ldacc, s); break;
+  }
+}
+
+// Shared epilogue fields of W8A8GemmArgs / W8A8DequantArgs.
+template <typename Args>
+static void fill_epilogue(GemmParams& p, const Args* a) {
+  p.m = (int)a->m;
+  p.n = (int)a->n;
+  p.row_scale = a->row_scale;
+  p.col_scale = a->col_scale;
+  p.col_stride = (int)a->col_scale_stride;
+  p.cs_vec = a->col_scale_stride == 1 && aligned16(a->col_scale);
+  p.bias_dtype = a->bias ? a->bias_dtype : 0;
+  p.bias = a->bias;
+  p.residual = reinterpret_cast<const uint16_t*>(a->residual);
+  p.ldr = a->ldr;
+  p.out = a->out;
+  p.ldc = a->ldc;
+  p.vec_out = aligned16(a->out) && a->ldc % 4 == 0;
+}
+
+}  // namespace w8a8
+
+extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_gemm: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8GemmArgs), "w8a8_gemm: struct_size %u != %zu", a->struct_size,
+               sizeof(W8A8GemmArgs));
+  W8A8_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 0, "w8a8_gemm: negative shape");
+  W8A8_REQUIRE(a->m < (1LL << 31) && a->n < (1LL << 31) && a->k < (1LL << 31), "w8a8_gemm: shape too large");
+  W8A8_REQUIRE(a->k * 128 * 128 < (1LL << 31), "w8a8_gemm: k=%lld could overflow int32 accumulation",
+               (long long)a->k);
+  W8A8_REQUIRE(a->k % 16 == 0, "w8a8_gemm: k %lld not a multiple of 16", (long long)a->k);
+  if (a->m == 0 || a->n == 0) return W8A8_OK;
+  int rc = check_epilogue(a->epilogue, a->out_dtype, a->bias_dtype, a->bias, a->residual, a->ldr, a->n,
+                          a->row_scale, a->col_scale, a->col_scale_stride, a->out, a->ldc);
+  if (rc != W8A8_OK) return rc;
+  W8A8_REQUIRE(a->k == 0 || (a->a && a->b), "w8a8_gemm: null operand");
+  W8A8_REQUIRE(aligned16(a->a) && aligned16(a->b) && a->lda % 16 == 0 && a->ldb % 16 == 0 && a->lda >= a->k &&
+                   a->ldb >= a->k,
+               "w8a8_gemm: operands must be 16-byte aligned with lda, ldb %% 16 == 0 and >= k");
+  const int64_t tiles = ((a->m + 255) / 256) * ((a->n + 255) / 256);
+  W8A8_REQUIRE(tiles < (1LL << 31), "w8a8_gemm: too many tiles");
+  GemmParams p{};
+  fill_epilogue(p, a);
+  p.a = a->a; p.b = a->b; p.lda = a->lda; p.ldb = a->ldb;
+  p.k = (int)a->k;
+  {
+    const int es = (a->out_dtype == W8A8_F16 || a->out_dtype == W8A8_BF16) ? 2 : 4;
+    p.vec16 = aligned16(a->out) && (a->ldc * es) % 16 == 0 &&
+              (a->residual == nullptr || (aligned16(a->residual) && a->ldr % 8 == 0));
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
+  int rc2;
+  switch (a->epilogue) {
+    case W8A8_EPI_INT32: rc2 = launch_gemm<kEpiInt32, kI32>(p, s); break;
+    case W8A8_EPI_ROW: rc2 = launch_gemm_out<kEpiRow>(a->out_dtype, p, s); break;
+    default: rc2 = launch_gemm_out<kEpiColumn>(a->out_dtype, p, s); break;
+  }
+  if (rc2 != W8A8_OK) return rc2;
+  return launch_status("w8a8_gemm");
+}
+
+extern "C" int w8a8_dequantize(const W8A8DequantArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_dequantize: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8DequantArgs), "w8a8_dequantize: struct_size %u != %zu",
+               a->struct_size, sizeof(W8A8DequantArgs));
+  W8A8_REQUIRE(a->epilogue == W8A8_EPI_ROW || a->epilogue == W8A8_EPI_COLUMN,
+               "w8a8_dequantize: epilogue must be ROW or COLUMN");
+  W8A8_REQUIRE(a->m >= 0 && a->n >= 0 && a->m < (1LL << 31) && a->n < (1LL << 31), "w8a8_dequantize: bad shape");
+  if (a->m == 0 || a->n == 0) return W8A8_OK;
+  int rc = check_epilogue(a->epilogue, a->out_dtype, a->bias_dtype, a->bias, a->residual, a->ldr, a->n,
+                          a->row_scale, a->col_scale, a->col_scale_stride, a->out, a->ldc);
+  if (rc != W8A8_OK) return rc;
+  W8A8_REQUIRE(a->acc && a->ldacc >= a->n, "w8a8_dequantize: null acc or ldacc < n");
+  W8A8_REQUIRE((a->m * ((a->n + 3) / 4) + 255) / 256 < (1LL << 31), "w8a8_dequantize: too large");
+  GemmParams p{};
+  fill_epilogue(p, a);
+  hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
+  if (a->epilogue == W8A8_EPI_ROW) launch_dequant_out<kEpiRow>(a->out_dtype, p, a->acc, a->ldacc, s);
+  else launch_dequant_out<kEpiColumn>(a->out_dtype, p, a->acc, a->ldacc, s);
+  return launch_status("w8a8_dequantize");
+}

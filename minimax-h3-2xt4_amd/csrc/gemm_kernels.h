@@ -1,0 +1,833 @@
+// INT8 GEMM kernels on gfx950 i8 MFMA with a fused dequantization / bias /
+// residual epilogue, the skinny-M weight-streaming GEMM and the standalone
+// epilogue. Included only by gemm_inst.hip, which instantiates one
+// (epilogue, output dtype) pair per object file so the variants compile in
+// parallel.
+//
+// C[m][n] = sum_k A[m][k] * B[n][k], A = activations [M,K], B = weights
+// [N,K], both K-contiguous. The MFMA's A operand is the weight tile and its B
+// operand the activation tile, so each lane ends with four consecutive
+// output columns of one row.
+#pragma once
+
+#include <atomic>
+
+#include "gemm_launch.h"
+#include "w8a8_device.h"
+
+namespace w8a8 {
+
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kTileBytes = kBM * kBK;  // one operand tile per K step
+
+// 16-byte chunk swizzle of LDS row r (depends on r & 15 only): the 16 lanes
+// reading one fragment column of 64-byte rows hit distinct banks.
+__device__ __forceinline__ int chunk_swizzle(int r) {
+  return (((r >> 1) ^ (r >> 3)) & 1) | (((r >> 2) & 1) << 1);
+}
+
+// Grouped raster: logical tile pid -> (tm, tn), walking groups of 8
+// row-tiles column by column so neighbouring pids share A and B rows.
+__device__ __forceinline__ void raster(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int kGroupM = 8;
+  const int group = kGroupM * tiles_n;
+  const int first_m = (pid / group) * kGroupM;
+  const int gsize = min(tiles_m - first_m, kGroupM);
+  const int in = pid - (pid / group) * group;
+  tm = first_m + in % gsize;
+  tn = in / gsize;
+}
+
+// One workgroup per tile (the register-staged fallback): consecutive
+// workgroup ids are dispatched round-robin over the 8 XCDs, so remap them
+// to give each XCD a contiguous range of the raster.
+__device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  if ((total & 7) == 0) pid = (pid & 7) * (total >> 3) + (pid >> 3);
+  raster(pid, tiles_m, tiles_n, tm, tn);
+}
+
+__device__ __forceinline__ float load_bias(const GemmParams& p, int n) {
+  if (p.bias_dtype == kF16) return h2f(reinterpret_cast<const uint16_t*>(p.bias)[n]);
+  if (p.bias_dtype == kF32) return reinterpret_cast<const float*>(p.bias)[n];
+  return 0.0f;
+}
+
+// Epilogue of four consecutive columns n..n+3 of row m (valid of them in
+// range). Shared by the unstaged GEMM epilogues, the skinny GEMM and the
+// standalone dequantize.
+template <int EPI, int OUT>
+__device__ __forceinline__ void epilogue4(const GemmParams& p, int m, int n, int valid, const int (&c)[4],
+                                          float a) {
+  if constexpr (EPI == kEpiInt32) {
+    int* o = reinterpret_cast<int*>(p.out) + (int64_t)m * p.ldc + n;
+    if (valid == 4 && p.vec_out) {
+      *reinterpret_cast<int4*>(o) = make_int4(c[0], c[1], c[2], c[3]);
+    } else {
+      for (int v = 0; v < valid; ++v) o[v] = c[v];
+    }
+  } else {
+    float y[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int nn = v < valid ? n + v : n;
+      const float w = p.col_scale[(int64_t)nn * p.col_stride];
+      y[v] = dequant1<EPI>(c[v], a, w);
+      if (p.bias_dtype) y[v] = y[v] + load_bias(p, nn);
+    }
+    if constexpr (OUT == kF32) {
+      float* o = reinterpret_cast<float*>(p.out) + (int64_t)m * p.ldc + n;
+      if (valid == 4 && p.vec_out) *reinterpret_cast<float4*>(o) = make_float4(y[0], y[1], y[2], y[3]);
+      else for (int v = 0; v < valid; ++v) o[v] = y[v];
+    } else {
+      uint16_t h[4];
+      if constexpr (OUT == kF16) {
+        if (p.residual) {
+          const uint16_t* r = p.residual + (int64_t)m * p.ldr + n;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const float branch = h2f(f2h(y[v]));
+            const float res = v < valid ? h2f(r[v]) : 0.0f;
+            h[v] = f2h(res + branch);
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) h[v] = f2h(y[v]);
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) h[v] = f2bf(y[v]);
+      }
+      uint16_t* o = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldc + n;
+      if (valid == 4 && p.vec_out) {
+        *reinterpret_cast<uint2*>(o) =
+            make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      } else {
+        for (int v = 0; v < valid; ++v) o[v] = h[v];
+      }
+    }
+  }
+}
+
+// Epilogue of one wavefront's 128x128 quadrant in the 16x16 MFMA layout:
+// lane holds C[m][n..n+3] with m = mw + 16 mb + fr and n = nw + 16 nb + 4 fc
+// for MFMA tile T = 8 nb + mb. Expanded by template recursion so every
+// accumulator index is a constant and the accumulators never need
+// addressable storage.
+template <int EPI, int OUT, int T>
+__device__ __forceinline__ void store_tiles(const GemmParams& p, v4i (&acc)[8][8], const float (&as)[8], int mw,
+                                            int nw, int fr, int fc) {
+  constexpr int NB = T / 8, MB = T % 8;
+  const int n = nw + NB * 16 + 4 * fc;
+  const int m = mw + MB * 16 + fr;
+  const int valid = min(4, p.n - n);
+  if (valid > 0 && m < p.m) {
+    const int c[4] = {acc[NB][MB][0], acc[NB][MB][1], acc[NB][MB][2], acc[NB][MB][3]};
+    epilogue4<EPI, OUT>(p, m, n, valid, c, as[MB]);
+  }
+  if constexpr (T + 1 < 64) store_tiles<EPI, OUT, T + 1>(p, acc, as, mw, nw, fr, fc);
+}
+
+template <int EPI, int OUT>
+__device__ __forceinline__ void store_quadrant(const GemmParams& p, v4i (&acc)[8][8], int mw, int nw, int fr,
+                                               int fc) {
+  float as[8];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    const int m = mw + mb * 16 + fr;
+    as[mb] = (EPI != kEpiInt32 && m < p.m) ? p.row_scale[m] : 0.0f;
+  }
+  store_tiles<EPI, OUT, 0>(p, acc, as, mw, nw, fr, fc);
+}
+
+// The same for a 4x4 grid of 32x32 tiles (v_mfma_i32_32x32x32_i8 layout):
+// lane (fr = lane % 32, fh = lane / 32) holds, for register group g = 0..3,
+// C[m][n..n+3] with m = mw + 32 mb + fr and n = nw + 32 nb + 8 g + 4 fh.
+// Used for partial tiles at the matrix edge.
+template <int EPI, int OUT, int T>
+__device__ __forceinline__ void store_tiles32(const GemmParams& p, v16i (&acc)[4][4], const float (&as)[4], int mw,
+                                              int nw, int fr, int fh) {
+  constexpr int NB = T / 16, MB = (T / 4) % 4, G = T % 4;
+  const int n = nw + NB * 32 + 8 * G + 4 * fh;
+  const int m = mw + MB * 32 + fr;
+  const int valid = min(4, p.n - n);
+  if (valid > 0 && m < p.m) {
+    const int c[4] = {acc[NB][MB][4 * G], acc[NB][MB][4 * G + 1], acc[NB][MB][4 * G + 2], acc[NB][MB][4 * G + 3]};
+    epilogue4<EPI, OUT>(p, m, n, valid, c, as[MB]);
+  }
+  if constexpr (T + 1 < 64) store_tiles32<EPI, OUT, T + 1>(p, acc, as, mw, nw, fr, fh);
+}
+
+template <int EPI, int OUT>
+__device__ __forceinline__ void store_quadrant32(const GemmParams& p, v16i (&acc)[4][4], int mw, int nw, int fr,
+                                                 int fh) {
+  float as[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int m = mw + mb * 32 + fr;
+    as[mb] = (EPI != kEpiInt32 && m < p.m) ? p.row_scale[m] : 0.0f;
+  }
+  store_tiles32<EPI, OUT, 0>(p, acc, as, mw, nw, fr, fh);
+}
+
+// Output element bits of one accumulator (storage dtype OUT; with a residual
+// the FP16 branch is stored and the residual is added on write-out).
+template <int EPI, int OUT>
+__device__ __forceinline__ uint32_t out_bits(int c, float a, float w, float b, bool has_bias) {
+  if constexpr (EPI == kEpiInt32) {
+    return (uint32_t)c;
+  } else {
+    float y = dequant1<EPI>(c, a, w);
+    if (has_bias) y = y + b;
+    if constexpr (OUT == kF32) return __builtin_bit_cast(uint32_t, y);
+    else if constexpr (OUT == kF16) return f2h(y);
+    else return f2bf(y);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  // s_waitcnt vmcnt(N) with expcnt and lgkmcnt left unconstrained.
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt vmcnt(0) lgkmcnt(0): every vector-memory access of this wave
+// (LDS DMA included) completed and every LDS access returned.
+__device__ __forceinline__ void wait_vm_lgkm() { __builtin_amdgcn_s_waitcnt(0x7 << 4); }
+
+// Layout of the staged epilogue's read-out: a lane owns CPL consecutive
+// columns of a 64-column half of the quadrant (8 for 2-byte outputs, 4 for
+// 4-byte outputs: one 16-byte store either way) and LPR lanes cover a row.
+template <int OUT>
+struct Readout {
+  static constexpr int ES = (OUT == kF16 || OUT == kBF16) ? 2 : 4;
+  static constexpr int CPL = 16 / ES;
+  static constexpr int LPR = 64 / CPL;
+  static constexpr int RPI = 64 / LPR;  // rows per wave store
+  static constexpr int ITERS = 32 / RPI;
+};
+
+// Column scales (and biases) of the columns a lane writes in the staged
+// epilogue: half h (0, 1) of the quadrant, columns
+// nw + 64 h + (lane % LPR) * CPL + [0, CPL).
+template <int OUT>
+__device__ __forceinline__ int readout_col(int nw, int h, int lane) {
+  using R = Readout<OUT>;
+  return nw + 64 * h + (lane % R::LPR) * R::CPL;
+}
+
+// Staged epilogue of one 128x128 quadrant through an 8 KB wave-private LDS
+// slice, in 8 passes of 32 rows x 64 columns. Each pass writes the raw int32
+// accumulators into the slice (16-byte chunks XOR-swizzled by row), then
+// each lane reads CPL consecutive columns of one row back, dequantizes them
+// in the reference's order (ROW (C*a)*w, COLUMN C*(a*w), then + bias, then
+// the cast), adds the FP16 residual read with the same coalesced pattern
+// and writes 16 bytes. The row scale comes from the lane that holds it in
+// the MFMA layout; wsc holds the lane's read-out column scales
+// (readout_col); the biases are fetched here, once per tile. Rows past m and columns past n are masked, and
+// rows that are not 16-byte aligned (vec16 == 0) or straddle n are written
+// element by element.
+template <int EPI, int OUT>
+__device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[4][4],
+                                                        const float (&wsc)[2][8], const float (&as)[4], int mw,
+                                                        int nw, int lane, int8_t* stage) {
+  using R = Readout<OUT>;
+  constexpr int RB = 256;  // 64 int32 per staged row
+  const int fr = lane & 31, fh = lane >> 5;
+  const int orow = lane / R::LPR, ocol = (lane % R::LPR) * R::CPL;
+  const bool has_bias = EPI != kEpiInt32 && p.bias_dtype != 0;
+  // Raw bias bits, loaded in one batch (converted at use, so the loads
+  // share a single wait).
+  uint32_t braw[2][R::CPL];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < R::CPL; ++j) braw[h][j] = 0;
+  if (EPI != kEpiInt32 && p.bias_dtype == kF16) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < R::CPL; ++j)
+        braw[h][j] = reinterpret_cast<const uint16_t*>(p.bias)[min(readout_col<OUT>(nw, h, lane) + j, p.n - 1)];
+  } else if (EPI != kEpiInt32 && p.bias_dtype == kF32) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < R::CPL; ++j)
+        braw[h][j] = reinterpret_cast<const uint32_t*>(p.bias)[min(readout_col<OUT>(nw, h, lane) + j, p.n - 1)];
+  }
+  const bool has_res = OUT == kF16 && p.residual != nullptr;
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {
+    const int mb = pass >> 1, h = pass & 1;
+    const int mrow = mw + mb * 32;
+    const int ncol = nw + 64 * h + ocol;
+    const bool full_cols = p.vec16 && ncol + R::CPL <= p.n;
+    uint4 rres[R::ITERS];
+    if (has_res) {
+#pragma unroll
+      for (int it = 0; it < R::ITERS; ++it) {
+        const int m = mrow + it * R::RPI + orow;
+        const uint16_t* r = p.residual + (int64_t)m * p.ldr + ncol;
+        if (m < p.m && full_cols) {
+          rres[it] = *reinterpret_cast<const uint4*>(r);
+        } else {
+          uint32_t w[4] = {0, 0, 0, 0};
+          if (m < p.m) {
+#pragma unroll
+            for (int j = 0; j < R::CPL; ++j)
+              if (ncol + j < p.n) w[j >> 1] |= (uint32_t)r[j] << (16 * (j & 1));
+          }
+          rres[it] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+    }
+    // acc[nb][mb] group g holds columns 32 nb + 8 g + 4 fh + [0, 4) of row fr.
+#pragma unroll
+    for (int nbl = 0; nbl < 2; ++nbl)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nb = 2 * h + nbl;
+        const int chunk = nbl * 8 + 2 * g + fh;
+        *reinterpret_cast<v4i*>(stage + fr * RB + ((chunk ^ (fr & 15)) << 4)) =
+            v4i{acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2], acc[nb][mb][4 * g + 3]};
+      }
+    wave_lds_sync();
+    int c[R::ITERS][R::CPL];
+#pragma unroll
+    for (int it = 0; it < R::ITERS; ++it) {
+      const int row = it * R::RPI + orow;
+#pragma unroll
+      for (int q = 0; q < R::CPL / 4; ++q) {
+        const int chunk = ocol / 4 + q;
+        const v4i v = *reinterpret_cast<const v4i*>(stage + row * RB + ((chunk ^ (row & 15)) << 4));
+        c[it][4 * q] = v[0]; c[it][4 * q + 1] = v[1]; c[it][4 * q + 2] = v[2]; c[it][4 * q + 3] = v[3];
+      }
+    }
+    wave_lds_sync();  // the slice is free for the next pass once the reads returned
+#pragma unroll
+    for (int it = 0; it < R::ITERS; ++it) {
+      const int row = it * R::RPI + orow;
+      const int m = mrow + row;
+      const float a = EPI != kEpiInt32 ? __shfl(as[mb], row, 64) : 0.0f;
+      uint32_t bits[R::CPL];
+#pragma unroll
+      for (int j = 0; j < R::CPL; ++j)
+        bits[j] = out_bits<EPI, OUT>(c[it][j], a, wsc[h][j],
+                                     p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
+                                                          : __builtin_bit_cast(float, braw[h][j]),
+                                     has_bias);
+      if constexpr (OUT == kF16) {
+        if (has_res) {
+          const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
+#pragma unroll
+          for (int j = 0; j < R::CPL; ++j)
+            bits[j] = f2h(h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1)))) + h2f((uint16_t)bits[j]));
+        }
+      }
+      char* o = reinterpret_cast<char*>(p.out) + ((int64_t)m * p.ldc + ncol) * R::ES;
+      if (m < p.m && full_cols) {
+        if constexpr (R::ES == 2)
+          *reinterpret_cast<uint4*>(o) = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
+                                                    bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16));
+        else
+          *reinterpret_cast<uint4*>(o) = make_uint4(bits[0], bits[1], bits[2], bits[3]);
+      } else if (m < p.m) {
+#pragma unroll
+        for (int j = 0; j < R::CPL; ++j) {
+          if (ncol + j < p.n) {
+            if constexpr (R::ES == 2) reinterpret_cast<uint16_t*>(o)[j] = (uint16_t)bits[j];
+            else reinterpret_cast<uint32_t*>(o)[j] = bits[j];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Register-staged 256x256 tile with v_mfma_i32_16x16x64_i8 and a two-buffer
+// LDS pipeline; the fallback for K % 64 != 0 (K tail loads are zero-filled).
+template <int EPI, int OUT>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_i8_256x256(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) int8_t smem[2 * 2 * kTileBytes];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tiles_m = (p.m + kBM - 1) / kBM, tiles_n = (p.n + kBN - 1) / kBN;
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+
+  // Global -> LDS: thread (lrow, lchunk) moves 16 bytes of rows
+  // lrow + 64 s (s = 0..3) of each operand tile per K step.
+  const int lrow = tid >> 2, lchunk = tid & 3;
+  const int st_off = lrow * kBK + ((lchunk ^ chunk_swizzle(lrow)) << 4);
+  const int8_t* ga[4];
+  const int8_t* gb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int ra = min(m0 + 64 * s + lrow, p.m - 1);
+    const int rb = min(n0 + 64 * s + lrow, p.n - 1);
+    ga[s] = p.a + (int64_t)ra * p.lda + lchunk * 16;
+    gb[s] = p.b + (int64_t)rb * p.ldb + lchunk * 16;
+  }
+  const int ktiles = (p.k + kBK - 1) / kBK;
+
+  v4i ra[4], rb[4];
+  auto gload = [&](int kt) {
+    const int kof = kt * kBK;
+    const bool kin = kof + lchunk * 16 < p.k;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      ra[s] = kin ? *reinterpret_cast<const v4i*>(ga[s] + kof) : v4i{0, 0, 0, 0};
+      rb[s] = kin ? *reinterpret_cast<const v4i*>(gb[s] + kof) : v4i{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int buf) {
+    int8_t* sa = smem + buf * 2 * kTileBytes;
+    int8_t* sb = sa + kTileBytes;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      *reinterpret_cast<v4i*>(sa + s * 64 * kBK + st_off) = ra[s];
+      *reinterpret_cast<v4i*>(sb + s * 64 * kBK + st_off) = rb[s];
+    }
+  };
+
+  // Fragment reads: lane (fr = lane % 16, fc = lane / 16) reads row fr,
+  // 16-byte chunk fc of each 16-row block.
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 15, fc = lane >> 4;
+  const int frag = fr * kBK + ((fc ^ chunk_swizzle(fr)) << 4);
+  const int a_off = wm * 128 * kBK + frag;
+  const int b_off = wn * 128 * kBK + frag;
+
+  v4i acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < ktiles) gload(kt + 1);
+    const int8_t* sa = smem + cur * 2 * kTileBytes;
+    const int8_t* sb = sa + kTileBytes;
+    v4i fa[8], fb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) fb[i] = *reinterpret_cast<const v4i*>(sa + a_off + i * 16 * kBK);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) fa[i] = *reinterpret_cast<const v4i*>(sb + b_off + i * 16 * kBK);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb)
+        acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[nb], fb[mb], acc[nb][mb], 0, 0, 0);
+    if (kt + 1 < ktiles) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  store_quadrant<EPI, OUT>(p, acc, m0 + wm * 128, n0 + wn * 128, fr, fc);
+}
+
+// Column scales of the lane's read-out columns (readout_col) for both
+// halves of the quadrant at column offset nw: branch-free clamped loads
+// (columns past n are never written) whose registers stay untouched until
+// the epilogue, so no wait for them lands in the K loop.
+template <int EPI, int OUT>
+__device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw, int lane, float (&wsc)[2][8]) {
+  using R = Readout<OUT>;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (EPI == kEpiInt32) {
+        wsc[h][j] = 0.0f;
+      } else {
+        const int n = min(readout_col<OUT>(nw, h, lane) + j, p.n - 1);
+        wsc[h][j] = j < R::CPL ? p.col_scale[(int64_t)n * p.col_stride] : 0.0f;
+      }
+    }
+}
+
+// Persistent 256x256 GEMM fed by gfx950 direct global->LDS loads
+// (global_load_lds_dwordx4). One workgroup per CU walks its tiles; the
+// operand stream runs across tile boundaries.
+//
+// A stage holds K = 128 of both operand tiles (256 rows x 128 bytes each,
+// 64 KB): every row segment is a whole 128-byte line, which streams from L2
+// about 1.6x faster per CU than half lines. The LDS holds a two-stage ring
+// (128 KB) and a dedicated 32 KB epilogue staging area (8 KB per wave).
+// Stage s + 2 is issued into the buffer of stage s as soon as every wave has
+// finished reading it (a few MFMAs into the stage's last K sub-step), and is
+// awaited at the same point of stage s + 1: a whole stage time in flight.
+// Every wait is vmcnt(0), which also covers the epilogue's stores (they
+// share the counter).
+//
+// LDS rows are 128 bytes: 16-byte chunk c of row r sits at physical chunk
+// c ^ ((r >> 1) & 7), which keeps both the DMA writes (lane i writes bytes
+// [16 i, 16 i + 16) of its instruction's 1 KB) and the fragment reads (32
+// rows x one chunk per 16-lane group) free of bank conflicts. A DMA lane
+// therefore loads the logical chunk that lands on its physical slot.
+constexpr int kSK = 128;                    // K bytes per stage
+constexpr int kSTile = 256 * kSK;           // one operand tile per stage (32 KB)
+constexpr int kSStage = 2 * kSTile;         // 64 KB
+constexpr int kStagingOff = 2 * kSStage;    // the ring ends here
+constexpr int kPersistentLds = kStagingOff + 4 * 8192;
+
+__device__ __forceinline__ void dma16(const int8_t* g, int8_t* l) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+// Workgroup barrier without a memory fence: the DMA completion is awaited
+// explicitly (vmcnt) before it, and the empty asm keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ int lds_chunk(int row, int c) { return c ^ ((row >> 1) & 7); }
+
+template <int EPI, int OUT>
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
+void gemm_i8_persistent(GemmParams p) {
+  extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (p.m + kBM - 1) / kBM, tiles_n = (p.n + kBN - 1) / kBN;
+  // Tile schedule. Workgroup w runs on XCD w % 8 (round-robin dispatch).
+  // With a grid that is a multiple of 8, XCD x owns the contiguous raster
+  // range [x*T/8, (x+1)*T/8) and its G/8 workgroups walk it in lockstep, so
+  // the tiles resident on one XCD at any time are raster neighbours sharing
+  // operand rows in that XCD's L2.
+  const int total = tiles_m * tiles_n, G = gridDim.x, w = blockIdx.x;
+  const bool by_xcd = (G & 7) == 0;
+  const int t_start = by_xcd ? (int)(((int64_t)(w & 7) * total) >> 3) : 0;
+  const int t_count = by_xcd ? (int)(((int64_t)((w & 7) + 1) * total) >> 3) - t_start : total;
+  const int t_stride = by_xcd ? G >> 3 : G;
+  const int t_first = by_xcd ? w >> 3 : w;
+  const int ntiles = t_first < t_count ? (t_count - t_first + t_stride - 1) / t_stride : 0;
+  if (ntiles == 0) return;
+  auto tile_pid = [&](int i) { return t_start + t_first + i * t_stride; };
+  const int kstages = p.k / kSK;
+
+  // DMA cursor: the (tile, stage) of the next stage to issue. Wave w fills
+  // rows 64 w .. 64 w + 63 of both operand tiles, 8 rows per instruction;
+  // offsets are 32-bit (the host checks that the operands span < 4 GB).
+  uint32_t off_a[8], off_b[8];
+  auto point = [&](int i) {
+    int tm, tn;
+    raster(tile_pid(i), tiles_m, tiles_n, tm, tn);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = (wave * 8 + j) * 8 + (lane >> 3);
+      const int chunk = lds_chunk(row, lane & 7);
+      off_a[j] = (uint32_t)((int64_t)min(tm * kBM + row, p.m - 1) * p.lda + chunk * 16);
+      off_b[j] = (uint32_t)((int64_t)min(tn * kBN + row, p.n - 1) * p.ldb + chunk * 16);
+    }
+  };
+  int dma_i = 0, dma_ks = 0;
+  point(0);
+  // Issue one stage (16 DMA instructions per wave) into ring buffer buf and
+  // advance the cursor; past the last stage of the last tile it stays put
+  // and re-reads that stage into a buffer that is never consumed.
+  auto issue = [&](int buf) {
+    int8_t* st = smem + buf * kSStage + wave * 8 * 1024;
+    const uint32_t kof = (uint32_t)(dma_ks * kSK);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(p.a + (off_a[j] + kof), st + j * 1024);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(p.b + (off_b[j] + kof), st + kSTile + j * 1024);
+    if (dma_ks + 1 < kstages) {
+      ++dma_ks;
+    } else if (dma_i + 1 < ntiles) {
+      ++dma_i;
+      dma_ks = 0;
+      point(dma_i);
+    }
+  };
+
+  // v_mfma_i32_32x32x32_i8: for sub-step u (K bytes [32 u, 32 u + 32) of the
+  // stage), lane (r = lane % 32, h = lane / 32) supplies row r, logical
+  // chunk 2 u + h of both operands. Each wave holds a 4x4 grid of 32x32
+  // accumulator tiles (its 128x128 quadrant).
+  const int wm = wave >> 1, wn = wave & 1;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int a_row = wm * 128 * kSK + fr * kSK, b_row = wn * 128 * kSK + fr * kSK;
+  auto read_frags = [&](int buf, int u, v4i (&fa)[4], v4i (&fb)[4]) {
+    const int8_t* sa = smem + buf * kSStage;
+    const int8_t* sb = sa + kSTile;
+    const int off = lds_chunk(fr, 2 * u + fh) << 4;   // rows 32 i + fr share (row >> 1) & 7
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[i] = *reinterpret_cast<const v4i*>(sb + b_row + i * 32 * kSK + off);
+      fb[i] = *reinterpret_cast<const v4i*>(sa + a_row + i * 32 * kSK + off);
+    }
+  };
+  v16i acc[4][4];
+  auto mfma16 = [&](const v4i (&fa)[4], const v4i (&fb)[4]) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[nb], fb[mb], acc[nb][mb], 0, 0, 0);
+  };
+  // Block row nb of the 4x4 MFMA grid (4 MFMAs).
+  auto mfma_row = [&](int nb, const v4i (&fa)[4], const v4i (&fb)[4]) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+      acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[nb], fb[mb], acc[nb][mb], 0, 0, 0);
+  };
+  // 16 MFMAs with 8 fragment reads spread between them.
+  auto interleave = [&]() {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+  // 12 MFMAs with 8 fragment reads.
+  auto interleave12 = [&]() {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+  };
+
+  issue(0);
+  issue(1);
+  wait_vmcnt<16>();  // stage 0 landed (stage 1 in flight)
+  block_barrier();
+  v4i fa0[4], fb0[4], fa1[4], fb1[4];
+  read_frags(0, 0, fa0, fb0);
+  int cur = 0;
+  for (int i = 0; i < ntiles; ++i) {
+    int tm, tn;
+    raster(tile_pid(i), tiles_m, tiles_n, tm, tn);
+    const int mw = tm * kBM + wm * 128, nw = tn * kBN + wn * 128;
+    // Row scales in the MFMA layout and the column scales of the staged
+    // read-out, fetched before the K loop so the epilogue never waits on them.
+    float as[4], wsc[2][8];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+      as[mb] = EPI != kEpiInt32 ? p.row_scale[min(mw + mb * 32 + fr, p.m - 1)] : 0.0f;
+    load_readout_scales<EPI, OUT>(p, nw, lane, wsc);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
+    for (int ks = 0; ks < kstages; ++ks) {
+      const int nxt = cur ^ 1;
+      mfma16(fa0, fb0);
+      read_frags(cur, 1, fa1, fb1);
+      interleave();
+      mfma16(fa1, fb1);
+      read_frags(cur, 2, fa0, fb0);
+      interleave();
+      mfma16(fa0, fb0);
+      read_frags(cur, 3, fa1, fb1);
+      interleave();
+      // The first MFMAs of the last sub-step consume its fragments, so past
+      // them this wave is done reading the stage's buffer.
+      mfma_row(0, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vm_lgkm();    // the next stage landed and this wave's reads of this one returned
+      block_barrier();   // ... for every wave: the buffer is released
+      issue(cur);        // stage + 2 streams in for a whole stage time
+#pragma unroll
+      for (int nb = 1; nb < 4; ++nb) mfma_row(nb, fa1, fb1);
+      read_frags(nxt, 0, fa0, fb0);
+      interleave12();
+      cur = nxt;
+    }
+    store_quadrant32_passes<EPI, OUT>(p, acc, wsc, as, mw, nw, lane, smem + kStagingOff + wave * 8192);
+  }
+  wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
+}
+
+// Skinny GEMM for M <= 64 (text-encoder decode / short prefill): weight
+// streaming. A 512-thread workgroup owns NR weight rows (NR = 16 or 32); its
+// 8 wavefronts split K into contiguous ranges and multiply with
+// v_mfma_i32_16x16x64_i8 (weight rows as the MFMA A operand, up to four
+// 16-row activation blocks as B), loading both operands straight from memory
+// into registers, 4 K steps per batch so many loads are in flight. The 8
+// partial sums meet in LDS; the shared epilogue writes the outputs. The
+// activation rows (<= 64 x K) stay L2-resident across workgroups.
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyMaxMB = 4;
+constexpr int kSkinnyU = 4;
+
+template <int EPI, int OUT, int NR>
+__global__ __launch_bounds__(512) void gemm_i8_skinny(GemmParams p) {
+  constexpr int NB = NR / 16;
+  __shared__ int red[kSkinnyWaves][NR][kSkinnyMaxMB * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * NR;
+  const int mblocks = (p.m + 15) >> 4;
+  const int ksteps = p.k >> 6;
+  const int per = (ksteps + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int s0 = min(wave * per, ksteps), s1 = min(s0 + per, ksteps);
+  const int fr = lane & 15, fc = lane >> 4;
+
+  const int8_t* wrow[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) wrow[nb] = p.b + (int64_t)min(n0 + nb * 16 + fr, p.n - 1) * p.ldb + fc * 16;
+  const int8_t* arow[kSkinnyMaxMB];
+#pragma unroll
+  for (int mb = 0; mb < kSkinnyMaxMB; ++mb) arow[mb] = p.a + (int64_t)min(mb * 16 + fr, p.m - 1) * p.lda + fc * 16;
+
+  v4i acc[NB][kSkinnyMaxMB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < kSkinnyMaxMB; ++mb) acc[nb][mb] = v4i{0, 0, 0, 0};
+
+  for (int s = s0; s < s1; s += kSkinnyU) {
+    v4i wf[kSkinnyU][NB], af[kSkinnyU][kSkinnyMaxMB];
+#pragma unroll
+    for (int u = 0; u < kSkinnyU; ++u) {
+      const int kof = min(s + u, s1 - 1) * 64;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) wf[u][nb] = *reinterpret_cast<const v4i*>(wrow[nb] + kof);
+#pragma unroll
+      for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+        if (mb < mblocks) af[u][mb] = *reinterpret_cast<const v4i*>(arow[mb] + kof);
+    }
+#pragma unroll
+    for (int u = 0; u < kSkinnyU; ++u) {
+      if (s + u < s1) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+            if (mb < mblocks)
+              acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[u][nb], af[u][mb], acc[nb][mb], 0, 0, 0);
+      }
+    }
+  }
+  // Lane holds C[m][n..n+3] for m = 16 mb + fr, n = 16 nb + 4 fc (local).
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[wave][nb * 16 + 4 * fc + v][mb * 16 + fr] = acc[nb][mb][v];
+  __syncthreads();
+  // Thread -> (m, 4 consecutive n): sum the 8 partials, then the epilogue.
+  for (int idx = tid; idx < p.m * (NR / 4); idx += 512) {
+    const int m = idx / (NR / 4);
+    const int nl = (idx % (NR / 4)) * 4;
+    const int n = n0 + nl;
+    const int valid = min(4, p.n - n);
+    if (valid <= 0) continue;
+    int c[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < kSkinnyWaves; ++w)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) c[v] += red[w][nl + v][m];
+    const float a = EPI != kEpiInt32 ? p.row_scale[m] : 0.0f;
+    epilogue4<EPI, OUT>(p, m, n, valid, c, a);
+  }
+}
+
+// Standalone epilogue: thread -> 4 consecutive columns of one row.
+template <int EPI, int OUT>
+__global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, const int32_t* __restrict__ acc,
+                                                      int64_t ldacc) {
+  const int quads = (p.n + 3) >> 2;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.m * quads) return;
+  const int m = (int)(idx / quads);
+  const int n = (int)(idx - (int64_t)m * quads) * 4;
+  const int valid = min(4, p.n - n);
+  const int32_t* src = acc + (int64_t)m * ldacc + n;
+  int c[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) c[v] = v < valid ? src[v] : 0;
+  epilogue4<EPI, OUT>(p, m, n, valid, c, p.row_scale[m]);
+}
+
+// ------------------------------------------------------------------ launch
+
+// Per-device one-time records (bit d = device d done).
+struct DeviceOnce {
+  std::atomic<uint64_t> done{0};
+};
+
+inline int current_device(int& dev) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("w8a8_gemm: hipGetDevice failed");
+    return W8A8_ERR_LAUNCH;
+  }
+  return W8A8_OK;
+}
+
+// Compute units of device dev (cached per device).
+inline int device_cus(int dev) {
+  static std::atomic<int> cus[64];
+  int n = cus[dev].load(std::memory_order_acquire);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cus[dev].store(n, std::memory_order_release);
+  return n;
+}
+
+template <int EPI, int OUT>
+int launch_gemm(const GemmParams& p, hipStream_t s) {
+  if (p.m <= kSkinnyMaxMB * 16 && p.k % 64 == 0) {
+    // 32 weight rows per workgroup while that still fills 256 workgroups.
+    if (p.n / 32 >= 256) {
+      hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 32>), dim3((unsigned)((p.n + 31) / 32)), dim3(512), 0, s, p);
+    } else {
+      hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 16>), dim3((unsigned)((p.n + 15) / 16)), dim3(512), 0, s, p);
+    }
+    return W8A8_OK;
+  }
+  const int64_t tiles = (int64_t)((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
+  // The persistent kernel streams whole K = 128 stages and addresses the
+  // operands with 32-bit offsets; anything else takes the register-staged
+  // kernel.
+  const bool offsets32 = (int64_t)(p.m - 1) * p.lda + p.k < (1ll << 32) && (int64_t)(p.n - 1) * p.ldb + p.k < (1ll << 32);
+  if (p.k % kSK != 0 || !offsets32) {
+    hipLaunchKernelGGL((gemm_i8_256x256<EPI, OUT>), dim3((unsigned)tiles), dim3(256), 0, s, p);
+    return W8A8_OK;
+  }
+  int dev = 0;
+  int rc = current_device(dev);
+  if (rc != W8A8_OK) return rc;
+  // The LDS ring exceeds the 64 KB default: raise the kernel's dynamic LDS
+  // limit once per device.
+  static DeviceOnce lds_enabled;
+  const uint64_t bit = 1ull << dev;
+  if (!(lds_enabled.done.load(std::memory_order_acquire) & bit)) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_persistent<EPI, OUT>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kPersistentLds);
+    if (e != hipSuccess) {
+      set_error("w8a8_gemm: cannot enable %d bytes of LDS: %s", kPersistentLds, hipGetErrorString(e));
+      return W8A8_ERR_LAUNCH;
+    }
+    lds_enabled.done.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  // One workgroup per CU (the ring takes the whole LDS); a multiple of 8 so
+  // every XCD holds the same number of them.
+  int64_t grid = tiles < device_cus(dev) ? tiles : device_cus(dev);
+  if (grid >= 8) grid &= ~7ll;
+  hipLaunchKernelGGL((gemm_i8_persistent<EPI, OUT>), dim3((unsigned)grid), dim3(256), kPersistentLds, s, p);
+  return W8A8_OK;
+}
+
+template <int EPI, int OUT>
+void launch_dequant(const GemmParams& p, const int32_t* acc, int64_t ldacc, hipStream_t s) {
+  const int64_t threads = (int64_t)p.m * ((p.n + 3) / 4);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  hipLaunchKernelGGL((dequant_kernel<EPI, OUT>), grid, dim3(256), 0, s, p, acc, ldacc);
+}
+
+}  // namespace w8a8

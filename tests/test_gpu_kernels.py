@@ -129,6 +129,61 @@ def test_gemm_scalar_weight_scale_and_residual(gpu):
     assert_bits_equal(np_of(got), want, 'in-place residual')
 
 
+@pytest.mark.parametrize('k', [64, 128, 192, 256, 320])
+def test_gemm_more_tiles_than_cus(gpu, k):
+    # 17 x 17 = 289 tiles of 256x256 on at most 256 persistent workgroups: a
+    # workgroup runs several tiles (ragged edges included) and the operand
+    # ring crosses tile boundaries after 1..5 K steps.
+    g = torch.Generator().manual_seed(k)
+    m, n = 4352, 4200
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32)
+    assert_bits_equal(np_of(got), o.int_mm(np_of(a), np_of(b)), f'gemm {m}x{n}x{k}')
+
+
+@pytest.mark.parametrize('epi,out_dtype,bias_dtype,residual', [
+    ('column', torch.float16, torch.float16, False), ('row', torch.float16, None, True),
+    ('row', torch.float32, torch.float32, False), ('column', torch.bfloat16, None, False),
+    ('row', torch.float16, torch.float32, True)])
+def test_gemm_more_tiles_than_cus_epilogues(gpu, epi, out_dtype, bias_dtype, residual):
+    g = torch.Generator().manual_seed(99)
+    m, n, k = 4400, 4300, 128       # 18 x 17 tiles, ragged in both directions
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
+    ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
+    bias = None if bias_dtype is None else (torch.randn((n,), generator=g) * 0.5).to(bias_dtype)
+    res = randn16(g, (m, n), 0.25) if residual else None
+    code = kernels.EPI_ROW if epi == 'row' else kernels.EPI_COLUMN
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=code, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       bias=None if bias is None else bias.to(gpu), out_dtype=out_dtype,
+                       residual=None if res is None else res.to(gpu))
+    fn = o.dequantize_row if epi == 'row' else o.dequantize_column
+    want = fn(o.int_mm(np_of(a), np_of(b)), np_of(rs).reshape(-1), np_of(ws).reshape(-1), tname(out_dtype),
+              None if bias is None else np_of(bias))
+    if residual:
+        want = o.residual_add(np_of(res), want)
+    assert_bits_equal(np_of(got), want, f'{epi} {out_dtype} {bias_dtype} residual={residual}')
+
+
+def test_gemm_unaligned_output_rows(gpu):
+    # ldc * 2 bytes not a multiple of 16: every tile takes the element-wise
+    # store path of the staged epilogue.
+    g = torch.Generator().manual_seed(3)
+    m, n, k = 600, 517, 192
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
+    ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
+    res = randn16(g, (m, n), 0.25)
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       out_dtype=torch.float16, residual=res.to(gpu))
+    want = o.residual_add(np_of(res), o.dequantize_row(o.int_mm(np_of(a), np_of(b)), np_of(rs).reshape(-1),
+                                                       np_of(ws).reshape(-1), 'f16'))
+    assert_bits_equal(np_of(got), want, 'unaligned rows')
+
+
 ADVERSARIAL = ('random', 'zero', 'bounds', 'cancellation', 'ties_outliers')
 
 
