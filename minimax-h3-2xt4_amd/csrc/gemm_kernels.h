@@ -86,13 +86,13 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int m, int n, int
           const uint16_t* r = p.residual + (int64_t)m * p.ldr + n;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const float branch = h2f(f2h(y[v]));
+            const float branch = h2f(f2h_of_f32(y[v]));
             const float res = v < valid ? h2f(r[v]) : 0.0f;
             h[v] = f2h(res + branch);
           }
         } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) h[v] = f2h(y[v]);
+          for (int v = 0; v < 4; ++v) h[v] = f2h_of_f32(y[v]);
         }
       } else {
 #pragma unroll
@@ -180,7 +180,7 @@ __device__ __forceinline__ uint32_t out_bits(int c, float a, float w, float b, b
     float y = dequant1<EPI>(c, a, w);
     if (has_bias) y = y + b;
     if constexpr (OUT == kF32) return __builtin_bit_cast(uint32_t, y);
-    else if constexpr (OUT == kF16) return f2h(y);
+    else if constexpr (OUT == kF16) return f2h_of_f32(y);
     else return f2bf(y);
   }
 }
@@ -195,6 +195,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // s_waitcnt vmcnt(0) lgkmcnt(0): every vector-memory access of this wave
 // (LDS DMA included) completed and every LDS access returned.
 __device__ __forceinline__ void wait_vm_lgkm() { __builtin_amdgcn_s_waitcnt(0x7 << 4); }
+
+// Compile-time epilogue options of the persistent kernel (each variant
+// carries only the loads it uses).
+enum EpilogueFlags { kWithBias = 1, kWithResidual = 2 };
 
 // Layout of the staged epilogue's read-out: a lane owns CPL consecutive
 // columns of a 64-column half of the quadrant (8 for 2-byte outputs, 4 for
@@ -224,40 +228,24 @@ __device__ __forceinline__ int readout_col(int nw, int h, int lane) {
 // in the reference's order (ROW (C*a)*w, COLUMN C*(a*w), then + bias, then
 // the cast), adds the FP16 residual read with the same coalesced pattern
 // and writes 16 bytes. The row scale comes from the lane that holds it in
-// the MFMA layout; wsc holds the lane's read-out column scales
-// (readout_col); the biases are fetched here, once per tile. Rows past m and columns past n are masked, and
-// rows that are not 16-byte aligned (vec16 == 0) or straddle n are written
-// element by element.
-template <int EPI, int OUT>
+// the MFMA layout; wsc and bsc hold the column scales and biases of the
+// lane's read-out columns (readout_col). Rows past m and columns past n are
+// masked, and rows that are not 16-byte aligned (vec16 == 0) or straddle n
+// are written element by element. A wave's LDS accesses execute in order,
+// so the passes need only compiler ordering between the slice writes and
+// reads, and the next pass's writes may issue before this pass's reads
+// return.
+template <int EPI, int OUT, int FLAGS>
 __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[4][4],
-                                                        const float (&wsc)[2][8], const float (&as)[4], int mw,
-                                                        int nw, int lane, int8_t* stage) {
+                                                        const float (&wsc)[2][8], const float (&bsc)[2][8],
+                                                        const float (&as)[4], int mw, int nw, int lane,
+                                                        int8_t* stage) {
   using R = Readout<OUT>;
   constexpr int RB = 256;  // 64 int32 per staged row
+  constexpr bool has_bias = (FLAGS & kWithBias) != 0;
+  constexpr bool has_res = (FLAGS & kWithResidual) != 0;
   const int fr = lane & 31, fh = lane >> 5;
   const int orow = lane / R::LPR, ocol = (lane % R::LPR) * R::CPL;
-  const bool has_bias = EPI != kEpiInt32 && p.bias_dtype != 0;
-  // Raw bias bits, loaded in one batch (converted at use, so the loads
-  // share a single wait).
-  uint32_t braw[2][R::CPL];
-#pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int j = 0; j < R::CPL; ++j) braw[h][j] = 0;
-  if (EPI != kEpiInt32 && p.bias_dtype == kF16) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int j = 0; j < R::CPL; ++j)
-        braw[h][j] = reinterpret_cast<const uint16_t*>(p.bias)[min(readout_col<OUT>(nw, h, lane) + j, p.n - 1)];
-  } else if (EPI != kEpiInt32 && p.bias_dtype == kF32) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int j = 0; j < R::CPL; ++j)
-        braw[h][j] = reinterpret_cast<const uint32_t*>(p.bias)[min(readout_col<OUT>(nw, h, lane) + j, p.n - 1)];
-  }
-  const bool has_res = OUT == kF16 && p.residual != nullptr;
 #pragma unroll
   for (int pass = 0; pass < 8; ++pass) {
     const int mb = pass >> 1, h = pass & 1;
@@ -265,7 +253,7 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     const int ncol = nw + 64 * h + ocol;
     const bool full_cols = p.vec16 && ncol + R::CPL <= p.n;
     uint4 rres[R::ITERS];
-    if (has_res) {
+    if constexpr (has_res) {
 #pragma unroll
       for (int it = 0; it < R::ITERS; ++it) {
         const int m = mrow + it * R::RPI + orow;
@@ -293,7 +281,7 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
         *reinterpret_cast<v4i*>(stage + fr * RB + ((chunk ^ (fr & 15)) << 4)) =
             v4i{acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2], acc[nb][mb][4 * g + 3]};
       }
-    wave_lds_sync();
+    asm volatile("" ::: "memory");
     int c[R::ITERS][R::CPL];
 #pragma unroll
     for (int it = 0; it < R::ITERS; ++it) {
@@ -305,7 +293,7 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
         c[it][4 * q] = v[0]; c[it][4 * q + 1] = v[1]; c[it][4 * q + 2] = v[2]; c[it][4 * q + 3] = v[3];
       }
     }
-    wave_lds_sync();  // the slice is free for the next pass once the reads returned
+    asm volatile("" ::: "memory");  // the next pass's writes stay behind these reads
 #pragma unroll
     for (int it = 0; it < R::ITERS; ++it) {
       const int row = it * R::RPI + orow;
@@ -314,17 +302,12 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       uint32_t bits[R::CPL];
 #pragma unroll
       for (int j = 0; j < R::CPL; ++j)
-        bits[j] = out_bits<EPI, OUT>(c[it][j], a, wsc[h][j],
-                                     p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
-                                                          : __builtin_bit_cast(float, braw[h][j]),
-                                     has_bias);
-      if constexpr (OUT == kF16) {
-        if (has_res) {
-          const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
+        bits[j] = out_bits<EPI, OUT>(c[it][j], a, wsc[h][j], bsc[h][j], has_bias);
+      if constexpr (has_res) {
+        const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
 #pragma unroll
-          for (int j = 0; j < R::CPL; ++j)
-            bits[j] = f2h(h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1)))) + h2f((uint16_t)bits[j]));
-        }
+        for (int j = 0; j < R::CPL; ++j)
+          bits[j] = f2h(h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1)))) + h2f((uint16_t)bits[j]));
       }
       char* o = reinterpret_cast<char*>(p.out) + ((int64_t)m * p.ldc + ncol) * R::ES;
       if (m < p.m && full_cols) {
@@ -432,17 +415,19 @@ void gemm_i8_256x256(GemmParams p) {
   store_quadrant<EPI, OUT>(p, acc, m0 + wm * 128, n0 + wn * 128, fr, fc);
 }
 
-// Column scales of the lane's read-out columns (readout_col) for both
-// halves of the quadrant at column offset nw: branch-free clamped loads
-// (columns past n are never written) whose registers stay untouched until
-// the epilogue, so no wait for them lands in the K loop.
-template <int EPI, int OUT>
-__device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw, int lane, float (&wsc)[2][8]) {
+// Column scales and raw bias bits of the lane's read-out columns
+// (readout_col) for both halves of the quadrant at column offset nw:
+// clamped loads (columns past n are never written) whose registers stay
+// untouched until the epilogue, so no wait for them lands in the K loop.
+template <int EPI, int OUT, bool BIAS>
+__device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw, int lane, float (&wsc)[2][8],
+                                                    uint32_t (&braw)[2][8]) {
   using R = Readout<OUT>;
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
+      braw[h][j] = 0;
       if constexpr (EPI == kEpiInt32) {
         wsc[h][j] = 0.0f;
       } else {
@@ -450,6 +435,21 @@ __device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw,
         wsc[h][j] = j < R::CPL ? p.col_scale[(int64_t)n * p.col_stride] : 0.0f;
       }
     }
+  if constexpr (EPI != kEpiInt32 && BIAS) {
+    if (p.bias_dtype == kF16) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < R::CPL; ++j)
+          braw[h][j] = reinterpret_cast<const uint16_t*>(p.bias)[min(readout_col<OUT>(nw, h, lane) + j, p.n - 1)];
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < R::CPL; ++j)
+          braw[h][j] = reinterpret_cast<const uint32_t*>(p.bias)[min(readout_col<OUT>(nw, h, lane) + j, p.n - 1)];
+    }
+  }
 }
 
 // Persistent 256x256 GEMM fed by gfx950 direct global->LDS loads
@@ -493,7 +493,7 @@ __device__ __forceinline__ void block_barrier() {
 
 __device__ __forceinline__ int lds_chunk(int row, int c) { return c ^ ((row >> 1) & 7); }
 
-template <int EPI, int OUT>
+template <int EPI, int OUT, int FLAGS>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_i8_persistent(GemmParams p) {
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
@@ -515,6 +515,7 @@ void gemm_i8_persistent(GemmParams p) {
   if (ntiles == 0) return;
   auto tile_pid = [&](int i) { return t_start + t_first + i * t_stride; };
   const int kstages = p.k / kSK;
+  constexpr bool late_dma = (FLAGS & kWithResidual) != 0;
 
   // DMA cursor: the (tile, stage) of the next stage to issue. Wave w fills
   // rows 64 w .. 64 w + 63 of both operand tiles, 8 rows per instruction;
@@ -614,15 +615,17 @@ void gemm_i8_persistent(GemmParams p) {
     // Row scales in the MFMA layout and the column scales of the staged
     // read-out, fetched before the K loop so the epilogue never waits on them.
     float as[4], wsc[2][8];
+    uint32_t braw[2][8];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
       as[mb] = EPI != kEpiInt32 ? p.row_scale[min(mw + mb * 32 + fr, p.m - 1)] : 0.0f;
-    load_readout_scales<EPI, OUT>(p, nw, lane, wsc);
+    load_readout_scales<EPI, OUT, (FLAGS & kWithBias) != 0>(p, nw, lane, wsc, braw);
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
-    for (int ks = 0; ks < kstages; ++ks) {
+    int ks = 0;
+    do {  // kstages >= 1
       const int nxt = cur ^ 1;
       mfma16(fa0, fb0);
       read_frags(cur, 1, fa1, fb1);
@@ -639,14 +642,31 @@ void gemm_i8_persistent(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
       wait_vm_lgkm();    // the next stage landed and this wave's reads of this one returned
       block_barrier();   // ... for every wave: the buffer is released
-      issue(cur);        // stage + 2 streams in for a whole stage time
+      // Stage + 2 streams in for a whole stage time. With a residual the
+      // last stage's issue waits until after the epilogue: the residual
+      // loads there would otherwise queue behind it (loads return in order).
+      if (!(late_dma && ks + 1 == kstages)) issue(cur);
 #pragma unroll
       for (int nb = 1; nb < 4; ++nb) mfma_row(nb, fa1, fb1);
       read_frags(nxt, 0, fa0, fb0);
       interleave12();
       cur = nxt;
-    }
-    store_quadrant32_passes<EPI, OUT>(p, acc, wsc, as, mw, nw, lane, smem + kStagingOff + wave * 8192);
+    } while (++ks < kstages);
+    // Everything but the stage just issued (its 16 loads are the youngest)
+    // has landed, the scale and bias loads of this tile included.
+    if constexpr (late_dma) wait_vmcnt<0>();
+    else wait_vmcnt<16>();
+    float bsc[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        bsc[h][j] = (FLAGS & kWithBias) == 0       ? 0.0f
+                    : p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
+                                           : __builtin_bit_cast(float, braw[h][j]);
+    store_quadrant32_passes<EPI, OUT, FLAGS>(p, acc, wsc, bsc, as, mw, nw, lane,
+                                             smem + kStagingOff + wave * 8192);
+    if constexpr (late_dma) issue(cur ^ 1);
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }
@@ -779,6 +799,29 @@ inline int device_cus(int dev) {
   return n;
 }
 
+template <int EPI, int OUT, int FLAGS>
+int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s) {
+  // The LDS ring and staging area exceed the 64 KB default: raise the
+  // kernel's dynamic LDS limit once per device.
+  static DeviceOnce lds_enabled;
+  const uint64_t bit = 1ull << dev;
+  if (!(lds_enabled.done.load(std::memory_order_acquire) & bit)) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_persistent<EPI, OUT, FLAGS>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kPersistentLds);
+    if (e != hipSuccess) {
+      set_error("w8a8_gemm: cannot enable %d bytes of LDS: %s", kPersistentLds, hipGetErrorString(e));
+      return W8A8_ERR_LAUNCH;
+    }
+    lds_enabled.done.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  // One workgroup per CU (the ring takes the whole LDS); a multiple of 8 so
+  // every XCD holds the same number of them.
+  int64_t grid = tiles < device_cus(dev) ? tiles : device_cus(dev);
+  if (grid >= 8) grid &= ~7ll;
+  hipLaunchKernelGGL((gemm_i8_persistent<EPI, OUT, FLAGS>), dim3((unsigned)grid), dim3(256), kPersistentLds, s, p);
+  return W8A8_OK;
+}
+
 template <int EPI, int OUT>
 int launch_gemm(const GemmParams& p, hipStream_t s) {
   if (p.m <= kSkinnyMaxMB * 16 && p.k % 64 == 0) {
@@ -802,25 +845,19 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
   int dev = 0;
   int rc = current_device(dev);
   if (rc != W8A8_OK) return rc;
-  // The LDS ring exceeds the 64 KB default: raise the kernel's dynamic LDS
-  // limit once per device.
-  static DeviceOnce lds_enabled;
-  const uint64_t bit = 1ull << dev;
-  if (!(lds_enabled.done.load(std::memory_order_acquire) & bit)) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_persistent<EPI, OUT>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kPersistentLds);
-    if (e != hipSuccess) {
-      set_error("w8a8_gemm: cannot enable %d bytes of LDS: %s", kPersistentLds, hipGetErrorString(e));
-      return W8A8_ERR_LAUNCH;
+  if constexpr (EPI == kEpiInt32) {
+    return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
+  } else if constexpr (OUT != kF16) {  // a residual requires FP16 output
+    return p.bias_dtype ? launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s)
+                        : launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
+  } else {
+    switch ((p.bias_dtype ? kWithBias : 0) | (p.residual ? kWithResidual : 0)) {
+      case 0: return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
+      case kWithBias: return launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s);
+      case kWithResidual: return launch_persistent<EPI, OUT, kWithResidual>(p, tiles, dev, s);
+      default: return launch_persistent<EPI, OUT, kWithBias | kWithResidual>(p, tiles, dev, s);
     }
-    lds_enabled.done.fetch_or(bit, std::memory_order_acq_rel);
   }
-  // One workgroup per CU (the ring takes the whole LDS); a multiple of 8 so
-  // every XCD holds the same number of them.
-  int64_t grid = tiles < device_cus(dev) ? tiles : device_cus(dev);
-  if (grid >= 8) grid &= ~7ll;
-  hipLaunchKernelGGL((gemm_i8_persistent<EPI, OUT>), dim3((unsigned)grid), dim3(256), kPersistentLds, s, p);
-  return W8A8_OK;
 }
 
 template <int EPI, int OUT>

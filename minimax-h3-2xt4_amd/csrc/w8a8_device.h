@@ -31,6 +31,13 @@ __device__ __forceinline__ float h2f(uint16_t h) {
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// fp32 -> fp16 of a value that must first exist as a rounded fp32 (e.g. a
+// product): the empty asm hides the producer, so the compiler cannot fold
+// fptrunc(fmul) into one v_fma_mix that rounds the exact product to fp16.
+__device__ __forceinline__ uint16_t f2h_of_f32(float f) {
+  __asm__("" : "+v"(f));
+  return f2h(f);
+}
 __device__ __forceinline__ float bf2f(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
