@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 1
+#define W8A8_ABI_VERSION 2
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -144,6 +144,13 @@ int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
  *   May alias out (in-place residual update).
  * out: [m, n] of out_dtype (I32 for EPI_INT32; F16, BF16 or F32 otherwise),
  *   row stride ldc.
+ * workspace: optional device buffer of workspace_bytes bytes (16-byte
+ *   aligned). When w8a8_gemm_workspace_size() is non-zero for the shape and
+ *   the workspace holds at least that many bytes, grids too small to fill the
+ *   GPU split K across workgroups: each writes exact int32 partial sums into
+ *   the workspace and a second kernel adds them and runs the epilogue (the
+ *   result is bit-identical to the unsplit GEMM). NULL / 0 never splits.
+ *   Calls that share a workspace must not overlap.
  * Requirements: k % 16 == 0; a, b 16-byte aligned; lda, ldb % 16 == 0;
  *   out element-aligned (rows are written with vector stores when out is
  *   16-byte aligned and ldc % 4 == 0).
@@ -168,10 +175,20 @@ typedef struct W8A8GemmArgs {
   int64_t ldr;
   void* out;
   int64_t ldc;
+  void* workspace;
+  int64_t workspace_bytes;
   void* stream;
 } W8A8GemmArgs;
 
 int w8a8_gemm(const W8A8GemmArgs* args);
+
+/*
+ * Workspace bytes w8a8_gemm would use for an m x n x k GEMM on the current
+ * device (0: the shape does not split K). No counterpart in the reference
+ * (its int_mm calls a vendor GEMM that manages its own workspace); it lets
+ * the caller allocate the split-K scratch once.
+ */
+int64_t w8a8_gemm_workspace_size(int64_t m, int64_t n, int64_t k);
 
 /*
  * Standalone dequantization of an int32 accumulator (the epilogue of

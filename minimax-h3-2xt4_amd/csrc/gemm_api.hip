@@ -93,6 +93,11 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
   fill_epilogue(p, a);
   p.a = a->a; p.b = a->b; p.lda = a->lda; p.ldb = a->ldb;
   p.k = (int)a->k;
+  p.ksplit = 1;
+  W8A8_REQUIRE(a->workspace_bytes >= 0 && (a->workspace == nullptr || aligned16(a->workspace)),
+               "w8a8_gemm: workspace must be 16-byte aligned with workspace_bytes >= 0");
+  p.ws = a->workspace_bytes > 0 ? a->workspace : nullptr;
+  p.ws_bytes = a->workspace_bytes;
   {
     const int es = (a->out_dtype == W8A8_F16 || a->out_dtype == W8A8_BF16) ? 2 : 4;
     p.vec16 = aligned16(a->out) && (a->ldc * es) % 16 == 0 &&
@@ -107,6 +112,16 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
   }
   if (rc2 != W8A8_OK) return rc2;
   return launch_status("w8a8_gemm");
+}
+
+extern "C" int64_t w8a8_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
+  using namespace w8a8;
+  if (m <= 0 || n <= 0 || k <= 0 || m >= (1LL << 31) || n >= (1LL << 31) || k >= (1LL << 31)) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int64_t bytes = 0;
+  gemm_ksplit(m, n, k, dev, &bytes);
+  return bytes;
 }
 
 extern "C" int w8a8_dequantize(const W8A8DequantArgs* a) {
@@ -125,6 +140,7 @@ extern "C" int w8a8_dequantize(const W8A8DequantArgs* a) {
   W8A8_REQUIRE((a->m * ((a->n + 3) / 4) + 255) / 256 < (1LL << 31), "w8a8_dequantize: too large");
   GemmParams p{};
   fill_epilogue(p, a);
+  p.ksplit = 1;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   if (a->epilogue == W8A8_EPI_ROW) launch_dequant_out<kEpiRow>(a->out_dtype, p, a->acc, a->ldacc, s);
   else launch_dequant_out<kEpiColumn>(a->out_dtype, p, a->acc, a->ldacc, s);

@@ -239,7 +239,7 @@ template <int EPI, int OUT, int FLAGS>
 __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[4][4],
                                                         const float (&wsc)[2][8], const float (&bsc)[2][8],
                                                         const float (&as)[4], int mw, int nw, int lane,
-                                                        int8_t* stage) {
+                                                        int8_t* stage, int64_t out_off) {
   using R = Readout<OUT>;
   constexpr int RB = 256;  // 64 int32 per staged row
   constexpr bool has_bias = (FLAGS & kWithBias) != 0;
@@ -309,7 +309,7 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
         for (int j = 0; j < R::CPL; ++j)
           bits[j] = f2h(h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1)))) + h2f((uint16_t)bits[j]));
       }
-      char* o = reinterpret_cast<char*>(p.out) + ((int64_t)m * p.ldc + ncol) * R::ES;
+      char* o = reinterpret_cast<char*>(p.out) + (out_off + (int64_t)m * p.ldc + ncol) * R::ES;
       if (m < p.m && full_cols) {
         if constexpr (R::ES == 2)
           *reinterpret_cast<uint4*>(o) = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
@@ -505,7 +505,8 @@ void gemm_i8_persistent(GemmParams p) {
   // range [x*T/8, (x+1)*T/8) and its G/8 workgroups walk it in lockstep, so
   // the tiles resident on one XCD at any time are raster neighbours sharing
   // operand rows in that XCD's L2.
-  const int total = tiles_m * tiles_n, G = gridDim.x, w = blockIdx.x;
+  const int ksplit = max(p.ksplit, 1);
+  const int total = tiles_m * tiles_n * ksplit, G = gridDim.x, w = blockIdx.x;
   const bool by_xcd = (G & 7) == 0;
   const int t_start = by_xcd ? (int)(((int64_t)(w & 7) * total) >> 3) : 0;
   const int t_count = by_xcd ? (int)(((int64_t)((w & 7) + 1) * total) >> 3) - t_start : total;
@@ -513,8 +514,12 @@ void gemm_i8_persistent(GemmParams p) {
   const int t_first = by_xcd ? w >> 3 : w;
   const int ntiles = t_first < t_count ? (t_count - t_first + t_stride - 1) / t_stride : 0;
   if (ntiles == 0) return;
-  auto tile_pid = [&](int i) { return t_start + t_first + i * t_stride; };
+  // Work item i of this workgroup: output tile item / ksplit, K split
+  // item % ksplit (the splits of one tile are raster neighbours too).
+  auto item_of = [&](int i) { return t_start + t_first + i * t_stride; };
   const int kstages = p.k / kSK;
+  auto ks_begin = [&](int item) { return (item % ksplit) * kstages / ksplit; };
+  auto ks_end = [&](int item) { return (item % ksplit + 1) * kstages / ksplit; };
   constexpr bool late_dma = (FLAGS & kWithResidual) != 0;
 
   // DMA cursor: the (tile, stage) of the next stage to issue. Wave w fills
@@ -523,7 +528,7 @@ void gemm_i8_persistent(GemmParams p) {
   uint32_t off_a[8], off_b[8];
   auto point = [&](int i) {
     int tm, tn;
-    raster(tile_pid(i), tiles_m, tiles_n, tm, tn);
+    raster(item_of(i) / ksplit, tiles_m, tiles_n, tm, tn);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int row = (wave * 8 + j) * 8 + (lane >> 3);
@@ -532,7 +537,7 @@ void gemm_i8_persistent(GemmParams p) {
       off_b[j] = (uint32_t)((int64_t)min(tn * kBN + row, p.n - 1) * p.ldb + chunk * 16);
     }
   };
-  int dma_i = 0, dma_ks = 0;
+  int dma_i = 0, dma_ks = ks_begin(item_of(0));
   point(0);
   // Issue one stage (16 DMA instructions per wave) into ring buffer buf and
   // advance the cursor; past the last stage of the last tile it stays put
@@ -544,11 +549,11 @@ void gemm_i8_persistent(GemmParams p) {
     for (int j = 0; j < 8; ++j) dma16(p.a + (off_a[j] + kof), st + j * 1024);
 #pragma unroll
     for (int j = 0; j < 8; ++j) dma16(p.b + (off_b[j] + kof), st + kSTile + j * 1024);
-    if (dma_ks + 1 < kstages) {
+    if (dma_ks + 1 < ks_end(item_of(dma_i))) {
       ++dma_ks;
     } else if (dma_i + 1 < ntiles) {
       ++dma_i;
-      dma_ks = 0;
+      dma_ks = ks_begin(item_of(dma_i));
       point(dma_i);
     }
   };
@@ -609,8 +614,9 @@ void gemm_i8_persistent(GemmParams p) {
   read_frags(0, 0, fa0, fb0);
   int cur = 0;
   for (int i = 0; i < ntiles; ++i) {
+    const int item = item_of(i);
     int tm, tn;
-    raster(tile_pid(i), tiles_m, tiles_n, tm, tn);
+    raster(item / ksplit, tiles_m, tiles_n, tm, tn);
     const int mw = tm * kBM + wm * 128, nw = tn * kBN + wn * 128;
     // Row scales in the MFMA layout and the column scales of the staged
     // read-out, fetched before the K loop so the epilogue never waits on them.
@@ -624,8 +630,9 @@ void gemm_i8_persistent(GemmParams p) {
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
+    const int nks = ks_end(item) - ks_begin(item);
     int ks = 0;
-    do {  // kstages >= 1
+    do {  // nks >= 1
       const int nxt = cur ^ 1;
       mfma16(fa0, fb0);
       read_frags(cur, 1, fa1, fb1);
@@ -645,13 +652,13 @@ void gemm_i8_persistent(GemmParams p) {
       // Stage + 2 streams in for a whole stage time. With a residual the
       // last stage's issue waits until after the epilogue: the residual
       // loads there would otherwise queue behind it (loads return in order).
-      if (!(late_dma && ks + 1 == kstages)) issue(cur);
+      if (!(late_dma && ks + 1 == nks)) issue(cur);
 #pragma unroll
       for (int nb = 1; nb < 4; ++nb) mfma_row(nb, fa1, fb1);
       read_frags(nxt, 0, fa0, fb0);
       interleave12();
       cur = nxt;
-    } while (++ks < kstages);
+    } while (++ks < nks);
     // Everything but the stage just issued (its 16 loads are the youngest)
     // has landed, the scale and bias loads of this tile included.
     if constexpr (late_dma) wait_vmcnt<0>();
@@ -665,7 +672,7 @@ void gemm_i8_persistent(GemmParams p) {
                     : p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
                                            : __builtin_bit_cast(float, braw[h][j]);
     store_quadrant32_passes<EPI, OUT, FLAGS>(p, acc, wsc, bsc, as, mw, nw, lane,
-                                             smem + kStagingOff + wave * 8192);
+                                             smem + kStagingOff + wave * 8192, (item % ksplit) * p.split_stride);
     if constexpr (late_dma) issue(cur ^ 1);
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
@@ -774,6 +781,31 @@ __global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, const int32_
   epilogue4<EPI, OUT>(p, m, n, valid, c, p.row_scale[m]);
 }
 
+// Split-K finish: thread -> 4 consecutive columns of one row; adds the
+// ksplit int32 partial tiles (exact), then the shared epilogue.
+template <int EPI, int OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, const int32_t* __restrict__ ws,
+                                                            int ksplit, int64_t stride) {
+  const int quads = (p.n + 3) >> 2;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)p.m * quads) return;
+  const int m = (int)(idx / quads);
+  const int n = (int)(idx - (int64_t)m * quads) * 4;
+  const int valid = min(4, p.n - n);
+  const int32_t* src = ws + (int64_t)m * p.n + n;
+  int c[4] = {0, 0, 0, 0};
+  if (valid == 4 && (p.n & 3) == 0) {
+    for (int sp = 0; sp < ksplit; ++sp) {
+      const int4 v = *reinterpret_cast<const int4*>(src + sp * stride);
+      c[0] += v.x; c[1] += v.y; c[2] += v.z; c[3] += v.w;
+    }
+  } else {
+    for (int sp = 0; sp < ksplit; ++sp)
+      for (int v = 0; v < valid; ++v) c[v] += src[sp * stride + v];
+  }
+  epilogue4<EPI, OUT>(p, m, n, valid, c, EPI != kEpiInt32 ? p.row_scale[m] : 0.0f);
+}
+
 // ------------------------------------------------------------------ launch
 
 // Per-device one-time records (bit d = device d done).
@@ -816,7 +848,8 @@ int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s
   }
   // One workgroup per CU (the ring takes the whole LDS); a multiple of 8 so
   // every XCD holds the same number of them.
-  int64_t grid = tiles < device_cus(dev) ? tiles : device_cus(dev);
+  const int64_t items = tiles * (p.ksplit > 1 ? p.ksplit : 1);
+  int64_t grid = items < device_cus(dev) ? items : device_cus(dev);
   if (grid >= 8) grid &= ~7ll;
   hipLaunchKernelGGL((gemm_i8_persistent<EPI, OUT, FLAGS>), dim3((unsigned)grid), dim3(256), kPersistentLds, s, p);
   return W8A8_OK;
@@ -845,6 +878,24 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
   int dev = 0;
   int rc = current_device(dev);
   if (rc != W8A8_OK) return rc;
+  int64_t ws_need = 0;
+  const int ksplit = p.ws ? gemm_ksplit(p.m, p.n, p.k, dev, &ws_need) : 1;
+  if (ksplit > 1 && p.ws_bytes >= ws_need) {
+    GemmParams q = p;
+    q.out = p.ws;
+    q.ldc = p.n;
+    q.vec16 = (p.n & 3) == 0;
+    q.residual = nullptr;
+    q.bias_dtype = 0;
+    q.ksplit = ksplit;
+    q.split_stride = (int64_t)p.m * p.n;
+    rc = launch_gemm_partials(q, dev, s);
+    if (rc != W8A8_OK) return rc;
+    const int64_t threads = (int64_t)p.m * ((p.n + 3) / 4);
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, OUT>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                       p, reinterpret_cast<const int32_t*>(p.ws), ksplit, q.split_stride);
+    return W8A8_OK;
+  }
   if constexpr (EPI == kEpiInt32) {
     return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
   } else if constexpr (OUT != kF16) {  // a residual requires FP16 output

@@ -28,6 +28,14 @@ struct GemmParams {
   int64_t ldc;
   int vec_out;  // out rows allow 4-element vector stores (16-byte base, ldc % 4 == 0)
   int vec16;    // out (and residual) rows are 16-byte aligned: staged full-row stores
+  // Split K (persistent kernel): ksplit workgroups share each output tile,
+  // split s covering K stages [s*S/ksplit, (s+1)*S/ksplit) and writing its
+  // partial tile at out + s * split_stride elements (1 / 0: no split).
+  int ksplit;
+  int64_t split_stride;
+  // Caller's split-K workspace (may be null).
+  void* ws;
+  int64_t ws_bytes;
 };
 
 // EPI: kEpiInt32 / kEpiRow / kEpiColumn; OUT: kI32 / kF16 / kBF16 / kF32.
@@ -36,5 +44,13 @@ int launch_gemm(const GemmParams& p, hipStream_t s);
 
 template <int EPI, int OUT>
 void launch_dequant(const GemmParams& p, const int32_t* acc, int64_t ldacc, hipStream_t s);
+
+// Split-K choice for an m x n x k GEMM on device dev: the number of K splits
+// (1: none) and the workspace bytes it needs.
+int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_bytes);
+
+// The int32 partial-sum pass of a split-K GEMM (the persistent kernel with
+// the raw int32 epilogue, defined with the int32 instantiation).
+int launch_gemm_partials(const GemmParams& p, int dev, hipStream_t s);
 
 }  // namespace w8a8

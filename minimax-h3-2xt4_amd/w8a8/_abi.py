@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -39,7 +39,8 @@ class GemmArgs(ctypes.Structure):
                 ('b', _p), ('ldb', _c.c_int64), ('m', _c.c_int64), ('n', _c.c_int64), ('k', _c.c_int64),
                 ('row_scale', _p), ('col_scale', _p), ('col_scale_stride', _c.c_int64), ('bias', _p),
                 ('bias_dtype', _c.c_int32), ('out_dtype', _c.c_int32), ('residual', _p),
-                ('ldr', _c.c_int64), ('out', _p), ('ldc', _c.c_int64), ('stream', _p)]
+                ('ldr', _c.c_int64), ('out', _p), ('ldc', _c.c_int64), ('workspace', _p),
+                ('workspace_bytes', _c.c_int64), ('stream', _p)]
 
 
 class DequantArgs(ctypes.Structure):
@@ -52,7 +53,7 @@ class DequantArgs(ctypes.Structure):
 
 STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs)
 ENTRY_POINTS = ('w8a8_quantize_rows', 'w8a8_swiglu_quantize', 'w8a8_gemm', 'w8a8_dequantize',
-                'w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error')
+                'w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error', 'w8a8_gemm_workspace_size')
 
 _LIB = None
 
@@ -79,6 +80,8 @@ def load(path=None):
     lib.w8a8_struct_size.restype = _c.c_int64
     lib.w8a8_struct_size.argtypes = [_c.c_int32]
     lib.w8a8_last_error.restype = _c.c_char_p
+    lib.w8a8_gemm_workspace_size.restype = _c.c_int64
+    lib.w8a8_gemm_workspace_size.argtypes = [_c.c_int64, _c.c_int64, _c.c_int64]
     for name, st in zip(ENTRY_POINTS[:4], STRUCTS):
         fn = getattr(lib, name)
         fn.restype = _c.c_int

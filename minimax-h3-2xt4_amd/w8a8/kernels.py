@@ -160,14 +160,30 @@ def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dty
                 residual=_abi.ptr(residual), ldr=ldr), out, keep
 
 
+_WORKSPACE_BYTES = {}
+
+
+def gemm_workspace_bytes(m, n, k, device):
+    """Split-K workspace bytes libw8a8 uses for an m x n x k GEMM on device
+    (0 when the shape does not split); cached per shape and device."""
+    key = (m, n, k, device.index)
+    if key not in _WORKSPACE_BYTES:
+        with torch.cuda.device(device):
+            _WORKSPACE_BYTES[key] = int(_abi.load().w8a8_gemm_workspace_size(m, n, k))
+    return _WORKSPACE_BYTES[key]
+
+
 def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=None, residual=None,
-         out_dtype=torch.float16, out=None):
+         out_dtype=torch.float16, out=None, workspace=None):
     """C = q @ weight.T on i8 MFMA with a fused epilogue.
 
     q int8 [M, K], weight int8 [N, K]. epilogue EPI_INT32 -> int32 [M, N];
     EPI_ROW -> out_dtype((C * a) * w [+ bias]); EPI_COLUMN ->
     out_dtype(C * (a * w) [+ bias]); residual (FP16 [M, N]) -> FP16
     residual + FP16 branch, and out may be the residual itself.
+    workspace: optional uint8 device tensor for split K; by default one of
+    gemm_workspace_bytes() is allocated when the shape splits K (grids that
+    would leave CUs idle). An empty tensor disables the split.
     """
     q = _rows_2d(q)
     if weight.ndim != 2:
@@ -187,11 +203,18 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
                                        q.device)
     if m == 0 or n == 0:
         return out
+    if workspace is None:
+        nbytes = gemm_workspace_bytes(m, n, k, q.device)
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
+    elif not workspace.is_cuda or workspace.device != q.device or not workspace.is_contiguous():
+        raise ValueError('workspace must be a contiguous tensor on the operands\' device')
+    ws_ptr = workspace.data_ptr() if workspace is not None and workspace.numel() else None
+    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
     args = _abi.GemmArgs(epilogue=epilogue, a=q.data_ptr(), lda=q.stride(0), b=weight.data_ptr(),
                          ldb=weight.stride(0), m=m, n=n, k=k, out=out.data_ptr(), ldc=out.stride(0),
-                         stream=_abi.stream_of(q), **fields)
+                         workspace=ws_ptr, workspace_bytes=ws_bytes, stream=_abi.stream_of(q), **fields)
     _abi.call('w8a8_gemm', args)
-    del keep
+    del keep, workspace
     return out
 
 

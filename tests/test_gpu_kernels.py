@@ -167,6 +167,44 @@ def test_gemm_more_tiles_than_cus_epilogues(gpu, epi, out_dtype, bias_dtype, res
     assert_bits_equal(np_of(got), want, f'{epi} {out_dtype} {bias_dtype} residual={residual}')
 
 
+SPLITK_CASES = [
+    # (m, n, k, epilogue, out dtype, bias dtype, residual): grids smaller than the CU count
+    (512, 4096, 14336, 'int32', None, None, False),     # text-encoder down at M=512: 32 tiles
+    (300, 520, 2048, 'row', torch.float16, None, True),  # ragged rows and columns
+    (300, 520, 2048, 'column', torch.bfloat16, torch.float16, False),
+    (257, 1000, 1024, 'row', torch.float32, torch.float32, False),
+]
+
+
+@pytest.mark.parametrize('m,n,k,epi,out_dtype,bias_dtype,residual', SPLITK_CASES)
+def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
+    assert kernels.gemm_workspace_bytes(m, n, k, gpu) > 0, 'shape expected to split K'
+    g = torch.Generator().manual_seed(m + n + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    acc = o.int_mm(np_of(a), np_of(b))
+    if epi == 'int32':
+        got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32)
+        assert_bits_equal(np_of(got), acc, 'split-K int32')
+        return
+    rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
+    ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
+    bias = None if bias_dtype is None else (torch.randn((n,), generator=g) * 0.5).to(bias_dtype)
+    res = randn16(g, (m, n), 0.25) if residual else None
+    code = kernels.EPI_ROW if epi == 'row' else kernels.EPI_COLUMN
+    kw = dict(epilogue=code, row_scale=rs.to(gpu), col_scale=ws.to(gpu), out_dtype=out_dtype,
+              bias=None if bias is None else bias.to(gpu), residual=None if res is None else res.to(gpu))
+    got = kernels.gemm(a.to(gpu), b.to(gpu), **kw)
+    unsplit = kernels.gemm(a.to(gpu), b.to(gpu), workspace=torch.empty(0, dtype=torch.uint8, device=gpu), **kw)
+    fn = o.dequantize_row if epi == 'row' else o.dequantize_column
+    want = fn(acc, np_of(rs).reshape(-1), np_of(ws).reshape(-1), tname(out_dtype),
+              None if bias is None else np_of(bias))
+    if residual:
+        want = o.residual_add(np_of(res), want)
+    assert_bits_equal(np_of(got), want, f'split-K {epi} {out_dtype}')
+    assert_bits_equal(np_of(unsplit), np_of(got), 'split-K equals the unsplit GEMM')
+
+
 def test_gemm_unaligned_output_rows(gpu):
     # ldc * 2 bytes not a multiple of 16: every tile takes the element-wise
     # store path of the staged epilogue.
