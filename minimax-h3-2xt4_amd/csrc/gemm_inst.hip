@@ -27,7 +27,7 @@ int launch_gemm_partials(const GemmParams& p, int dev, hipStream_t s) {
 // write-and-read traffic at about 6.5 TB/s.
 int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_bytes) {
   *workspace_bytes = 0;
-  if (m <= kSkinnyMaxMB * 16 || k % kSK != 0) return 1;
+  if (m <= kSkinnyMaxM || k % kSK != 0) return 1;
   if ((m - 1) * k + k >= (1ll << 32) || (n - 1) * k + k >= (1ll << 32)) return 1;
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
   const int64_t kstages = k / kSK, cus = device_cus(dev);

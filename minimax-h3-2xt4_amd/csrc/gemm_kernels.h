@@ -679,76 +679,85 @@ void gemm_i8_persistent(GemmParams p) {
 }
 
 // Skinny GEMM for M <= 64 (text-encoder decode / short prefill): weight
-// streaming. A 512-thread workgroup owns NR weight rows (NR = 16 or 32); its
-// 8 wavefronts split K into contiguous ranges and multiply with
-// v_mfma_i32_16x16x64_i8 (weight rows as the MFMA A operand, up to four
-// 16-row activation blocks as B), loading both operands straight from memory
-// into registers, 4 K steps per batch so many loads are in flight. The 8
-// partial sums meet in LDS; the shared epilogue writes the outputs. The
-// activation rows (<= 64 x K) stay L2-resident across workgroups.
-constexpr int kSkinnyWaves = 8;
-constexpr int kSkinnyMaxMB = 4;
-constexpr int kSkinnyU = 4;
+// streaming. A workgroup of W wavefronts owns NR weight rows (NR = 16 with
+// W = 8, or NR = 32 with W = 4 when N / 32 still fills the GPU); the waves
+// split K into contiguous ranges and multiply with v_mfma_i32_16x16x64_i8
+// (weight rows as the MFMA A operand, MB 16-row activation blocks as B),
+// loading both operands straight from memory into registers in batches of U
+// K steps, double buffered so the next batch is in flight while the current
+// one multiplies. The W partial sums meet in LDS; the shared epilogue writes
+// the outputs. The activation rows (<= 64 x K) stay cache-resident across
+// workgroups.
+constexpr int kSkinnyMaxM = 64;
 
-template <int EPI, int OUT, int NR>
-__global__ __launch_bounds__(512) void gemm_i8_skinny(GemmParams p) {
+template <int EPI, int OUT, int NR, int MB>
+__global__ __launch_bounds__(NR == 16 ? 512 : 256) void gemm_i8_skinny(GemmParams p) {
   constexpr int NB = NR / 16;
-  __shared__ int red[kSkinnyWaves][NR][kSkinnyMaxMB * 16];
+  constexpr int W = NR == 16 ? 8 : 4;
+  constexpr int U = MB == 1 ? 4 : 2;
+  __shared__ int red[W][NR][MB * 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * NR;
-  const int mblocks = (p.m + 15) >> 4;
   const int ksteps = p.k >> 6;
-  const int per = (ksteps + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int per = (ksteps + W - 1) / W;
   const int s0 = min(wave * per, ksteps), s1 = min(s0 + per, ksteps);
   const int fr = lane & 15, fc = lane >> 4;
 
   const int8_t* wrow[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) wrow[nb] = p.b + (int64_t)min(n0 + nb * 16 + fr, p.n - 1) * p.ldb + fc * 16;
-  const int8_t* arow[kSkinnyMaxMB];
+  const int8_t* arow[MB];
 #pragma unroll
-  for (int mb = 0; mb < kSkinnyMaxMB; ++mb) arow[mb] = p.a + (int64_t)min(mb * 16 + fr, p.m - 1) * p.lda + fc * 16;
+  for (int mb = 0; mb < MB; ++mb) arow[mb] = p.a + (int64_t)min(mb * 16 + fr, p.m - 1) * p.lda + fc * 16;
 
-  v4i acc[NB][kSkinnyMaxMB];
+  v4i acc[NB][MB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < kSkinnyMaxMB; ++mb) acc[nb][mb] = v4i{0, 0, 0, 0};
+    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = v4i{0, 0, 0, 0};
 
-  for (int s = s0; s < s1; s += kSkinnyU) {
-    v4i wf[kSkinnyU][NB], af[kSkinnyU][kSkinnyMaxMB];
+  // Batch at K step s: U steps (past s1 the last step is re-read and not used).
+  auto load = [&](int s, v4i (&wf)[U][NB], v4i (&af)[U][MB]) {
 #pragma unroll
-    for (int u = 0; u < kSkinnyU; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int kof = min(s + u, s1 - 1) * 64;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) wf[u][nb] = *reinterpret_cast<const v4i*>(wrow[nb] + kof);
 #pragma unroll
-      for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
-        if (mb < mblocks) af[u][mb] = *reinterpret_cast<const v4i*>(arow[mb] + kof);
+      for (int mb = 0; mb < MB; ++mb) af[u][mb] = *reinterpret_cast<const v4i*>(arow[mb] + kof);
     }
+  };
+  auto mma = [&](int s, const v4i (&wf)[U][NB], const v4i (&af)[U][MB]) {
 #pragma unroll
-    for (int u = 0; u < kSkinnyU; ++u) {
+    for (int u = 0; u < U; ++u) {
       if (s + u < s1) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-          for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
-            if (mb < mblocks)
-              acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[u][nb], af[u][mb], acc[nb][mb], 0, 0, 0);
+          for (int mb = 0; mb < MB; ++mb)
+            acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[u][nb], af[u][mb], acc[nb][mb], 0, 0, 0);
       }
     }
+  };
+  v4i wa[U][NB], aa[U][MB], wb[U][NB], ab[U][MB];
+  if (s0 < s1) load(s0, wa, aa);
+  for (int s = s0; s < s1; s += 2 * U) {
+    if (s + U < s1) load(s + U, wb, ab);
+    mma(s, wa, aa);
+    if (s + 2 * U < s1) load(s + 2 * U, wa, aa);
+    if (s + U < s1) mma(s + U, wb, ab);
   }
   // Lane holds C[m][n..n+3] for m = 16 mb + fr, n = 16 nb + 4 fc (local).
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < kSkinnyMaxMB; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int v = 0; v < 4; ++v) red[wave][nb * 16 + 4 * fc + v][mb * 16 + fr] = acc[nb][mb][v];
   __syncthreads();
-  // Thread -> (m, 4 consecutive n): sum the 8 partials, then the epilogue.
-  for (int idx = tid; idx < p.m * (NR / 4); idx += 512) {
+  // Thread -> (m, 4 consecutive n): sum the W partials, then the epilogue.
+  for (int idx = tid; idx < p.m * (NR / 4); idx += W * 64) {
     const int m = idx / (NR / 4);
     const int nl = (idx % (NR / 4)) * 4;
     const int n = n0 + nl;
@@ -756,11 +765,21 @@ __global__ __launch_bounds__(512) void gemm_i8_skinny(GemmParams p) {
     if (valid <= 0) continue;
     int c[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int w = 0; w < kSkinnyWaves; ++w)
+    for (int w = 0; w < W; ++w)
 #pragma unroll
       for (int v = 0; v < 4; ++v) c[v] += red[w][nl + v][m];
     const float a = EPI != kEpiInt32 ? p.row_scale[m] : 0.0f;
     epilogue4<EPI, OUT>(p, m, n, valid, c, a);
+  }
+}
+
+template <int EPI, int OUT, int MB>
+void launch_skinny(const GemmParams& p, hipStream_t s) {
+  // 32 weight rows per workgroup while that still fills 256 workgroups.
+  if (p.n / 32 >= 256) {
+    hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 32, MB>), dim3((unsigned)((p.n + 31) / 32)), dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 16, MB>), dim3((unsigned)((p.n + 15) / 16)), dim3(512), 0, s, p);
   }
 }
 
@@ -857,13 +876,9 @@ int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s
 
 template <int EPI, int OUT>
 int launch_gemm(const GemmParams& p, hipStream_t s) {
-  if (p.m <= kSkinnyMaxMB * 16 && p.k % 64 == 0) {
-    // 32 weight rows per workgroup while that still fills 256 workgroups.
-    if (p.n / 32 >= 256) {
-      hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 32>), dim3((unsigned)((p.n + 31) / 32)), dim3(512), 0, s, p);
-    } else {
-      hipLaunchKernelGGL((gemm_i8_skinny<EPI, OUT, 16>), dim3((unsigned)((p.n + 15) / 16)), dim3(512), 0, s, p);
-    }
+  if (p.m <= kSkinnyMaxM && p.k % 64 == 0) {
+    if (p.m <= 16) launch_skinny<EPI, OUT, 1>(p, s);
+    else launch_skinny<EPI, OUT, 4>(p, s);
     return W8A8_OK;
   }
   const int64_t tiles = (int64_t)((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
