@@ -151,7 +151,7 @@ def run_dit_ffn(args, torch, dev):
     traffic = traffic_from_profiles('fc1_gemm')
     roofline = dict(bound='mfma', achieved=round(fc1['tops'], 1), peak=PEAK_INT8_TOPS, unit='TOPS',
                     frac=round(fc1['frac'], 4), traffic=None if traffic is None else int(traffic),
-                    kernel='gemm_i8_256x256_dma (FC1 16384x16384x3072, column epilogue)',
+                    kernel='gemm_i8_persistent<2,1,0> (FC1 16384x16384x3072, column epilogue)',
                     algorithmic=f'{ops_fc1:.4g} int8 ops per launch (2*M*N*K)')
     tops = (ops_fc1 + ops_fc2) / (ms * 1e-3) / 1e12
     result = dict(metric=METRIC, value=round(tops, 1), unit='TOPS', n_gpus=1, steps=args.steps,
