@@ -24,6 +24,8 @@
  *   ROW epilogue:    y = (f32(C) * a[m]) * w[n]   [+ f32(bias[n])]
  *   COLUMN epilogue: y = f32(C) * (a[m] * w[n])   [+ f32(bias[n])]
  *   residual:  out = f16(f32(res[m][n]) + f32(f16(y)))
+ *   gated residual: out = f16(fma(f32(f16(y)), gate[label[m]][n], f32(res[m][n])))
+ *              (one rounding, as __fmaf_rn)
  */
 #ifndef W8A8_H
 #define W8A8_H
@@ -34,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 2
+#define W8A8_ABI_VERSION 3
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -142,6 +144,12 @@ int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
  * bias: optional [n] of bias_dtype (F16 or F32), added after the products.
  * residual: optional [m, n] F16 (row stride ldr); requires out_dtype F16.
  *   May alias out (in-place residual update).
+ * gate, gate_labels, ldg: optional DiT modulation gate (requires residual):
+ *   gate fp32 table [R, ldg] (ldg >= n), gate_labels int32 [m] (each row's
+ *   table row, in [0, R)); the residual update becomes
+ *   f16(fma(f32(f16(y)), gate[gate_labels[m]][n], f32(res))).
+ *   Replaces patches/tilelang_dit_fusion.py:56-77 (row_gate_kernel) and
+ *   patches/h3_tensor_flow.py:145-152 (gated_add).
  * out: [m, n] of out_dtype (I32 for EPI_INT32; F16, BF16 or F32 otherwise),
  *   row stride ldc.
  * workspace: optional device buffer of workspace_bytes bytes (16-byte
@@ -173,6 +181,9 @@ typedef struct W8A8GemmArgs {
   int32_t out_dtype;
   const void* residual;
   int64_t ldr;
+  const float* gate;
+  const int32_t* gate_labels;
+  int64_t ldg;
   void* out;
   int64_t ldc;
   void* workspace;
@@ -213,6 +224,9 @@ typedef struct W8A8DequantArgs {
   int32_t out_dtype;
   const void* residual;
   int64_t ldr;
+  const float* gate;
+  const int32_t* gate_labels;
+  int64_t ldg;
   void* out;
   int64_t ldc;
   void* stream;

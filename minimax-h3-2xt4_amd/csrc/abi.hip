@@ -19,8 +19,8 @@ void set_error(const char* fmt, ...) {
 
 static_assert(sizeof(W8A8QuantArgs) == 88, "W8A8QuantArgs layout");
 static_assert(sizeof(W8A8SwigluArgs) == 96, "W8A8SwigluArgs layout");
-static_assert(sizeof(W8A8GemmArgs) == 160, "W8A8GemmArgs layout");
-static_assert(sizeof(W8A8DequantArgs) == 120, "W8A8DequantArgs layout");
+static_assert(sizeof(W8A8GemmArgs) == 184, "W8A8GemmArgs layout");
+static_assert(sizeof(W8A8DequantArgs) == 144, "W8A8DequantArgs layout");
 
 extern "C" int w8a8_abi_version(void) { return W8A8_ABI_VERSION; }
 

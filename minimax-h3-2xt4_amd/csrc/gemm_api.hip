@@ -7,14 +7,16 @@
 namespace w8a8 {
 
 static int check_epilogue(int epi, int out_dtype, int bias_dtype, const void* bias, const void* residual,
-                          int64_t ldr, int64_t n, const float* row_scale, const float* col_scale,
-                          int64_t col_stride, const void* out, int64_t ldc) {
+                          int64_t ldr, const float* gate, const int32_t* labels, int64_t ldg, int64_t n,
+                          const float* row_scale, const float* col_scale, int64_t col_stride, const void* out,
+                          int64_t ldc) {
   W8A8_REQUIRE(out != nullptr, "null output");
   const int es = out_dtype == W8A8_F16 || out_dtype == W8A8_BF16 ? 2 : 4;
   W8A8_REQUIRE(((uintptr_t)out % es) == 0 && ldc >= n, "out must be element-aligned with ldc >= n");
   if (epi == W8A8_EPI_INT32) {
     W8A8_REQUIRE(out_dtype == W8A8_I32, "EPI_INT32 requires out_dtype I32");
-    W8A8_REQUIRE(bias == nullptr && residual == nullptr, "EPI_INT32 takes no bias or residual");
+    W8A8_REQUIRE(bias == nullptr && residual == nullptr && gate == nullptr,
+                 "EPI_INT32 takes no bias, residual or gate");
     return W8A8_OK;
   }
   W8A8_REQUIRE(epi == W8A8_EPI_ROW || epi == W8A8_EPI_COLUMN, "unknown epilogue %d", epi);
@@ -27,6 +29,11 @@ static int check_epilogue(int epi, int out_dtype, int bias_dtype, const void* bi
   if (residual) {
     W8A8_REQUIRE(out_dtype == W8A8_F16, "residual requires F16 output");
     W8A8_REQUIRE(((uintptr_t)residual & 1u) == 0 && ldr >= n, "residual must be 2-byte aligned with ldr >= n");
+  }
+  if (gate) {
+    W8A8_REQUIRE(residual != nullptr, "gate requires a residual");
+    W8A8_REQUIRE(labels != nullptr && ldg >= n && ((uintptr_t)gate & 3u) == 0,
+                 "gate requires gate_labels, a 4-byte aligned table and ldg >= n");
   }
   return W8A8_OK;
 }
@@ -62,6 +69,9 @@ static void fill_epilogue(GemmParams& p, const Args* a) {
   p.bias = a->bias;
   p.residual = reinterpret_cast<const uint16_t*>(a->residual);
   p.ldr = a->ldr;
+  p.gate = a->gate;
+  p.labels = a->gate_labels;
+  p.ldg = a->ldg;
   p.out = a->out;
   p.ldc = a->ldc;
   p.vec_out = aligned16(a->out) && a->ldc % 4 == 0;
@@ -80,8 +90,9 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
                (long long)a->k);
   W8A8_REQUIRE(a->k % 16 == 0, "w8a8_gemm: k %lld not a multiple of 16", (long long)a->k);
   if (a->m == 0 || a->n == 0) return W8A8_OK;
-  int rc = check_epilogue(a->epilogue, a->out_dtype, a->bias_dtype, a->bias, a->residual, a->ldr, a->n,
-                          a->row_scale, a->col_scale, a->col_scale_stride, a->out, a->ldc);
+  int rc = check_epilogue(a->epilogue, a->out_dtype, a->bias_dtype, a->bias, a->residual, a->ldr, a->gate,
+                          a->gate_labels, a->ldg, a->n, a->row_scale, a->col_scale, a->col_scale_stride, a->out,
+                          a->ldc);
   if (rc != W8A8_OK) return rc;
   W8A8_REQUIRE(a->k == 0 || (a->a && a->b), "w8a8_gemm: null operand");
   W8A8_REQUIRE(aligned16(a->a) && aligned16(a->b) && a->lda % 16 == 0 && a->ldb % 16 == 0 && a->lda >= a->k &&
@@ -133,8 +144,9 @@ extern "C" int w8a8_dequantize(const W8A8DequantArgs* a) {
                "w8a8_dequantize: epilogue must be ROW or COLUMN");
   W8A8_REQUIRE(a->m >= 0 && a->n >= 0 && a->m < (1LL << 31) && a->n < (1LL << 31), "w8a8_dequantize: bad shape");
   if (a->m == 0 || a->n == 0) return W8A8_OK;
-  int rc = check_epilogue(a->epilogue, a->out_dtype, a->bias_dtype, a->bias, a->residual, a->ldr, a->n,
-                          a->row_scale, a->col_scale, a->col_scale_stride, a->out, a->ldc);
+  int rc = check_epilogue(a->epilogue, a->out_dtype, a->bias_dtype, a->bias, a->residual, a->ldr, a->gate,
+                          a->gate_labels, a->ldg, a->n, a->row_scale, a->col_scale, a->col_scale_stride, a->out,
+                          a->ldc);
   if (rc != W8A8_OK) return rc;
   W8A8_REQUIRE(a->acc && a->ldacc >= a->n, "w8a8_dequantize: null acc or ldacc < n");
   W8A8_REQUIRE((a->m * ((a->n + 3) / 4) + 255) / 256 < (1LL << 31), "w8a8_dequantize: too large");

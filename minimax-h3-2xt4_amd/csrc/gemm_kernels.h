@@ -84,11 +84,12 @@ __device__ __forceinline__ void epilogue4(const GemmParams& p, int m, int n, int
       if constexpr (OUT == kF16) {
         if (p.residual) {
           const uint16_t* r = p.residual + (int64_t)m * p.ldr + n;
+          const float* gr = p.gate ? p.gate + (int64_t)p.labels[m] * p.ldg + n : nullptr;
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const float branch = h2f(f2h_of_f32(y[v]));
             const float res = v < valid ? h2f(r[v]) : 0.0f;
-            h[v] = f2h(res + branch);
+            h[v] = gr ? f2h_of_f32(__builtin_fmaf(branch, gr[v < valid ? v : 0], res)) : f2h(res + branch);
           }
         } else {
 #pragma unroll
@@ -198,7 +199,7 @@ __device__ __forceinline__ void wait_vm_lgkm() { __builtin_amdgcn_s_waitcnt(0x7 
 
 // Compile-time epilogue options of the persistent kernel (each variant
 // carries only the loads it uses).
-enum EpilogueFlags { kWithBias = 1, kWithResidual = 2 };
+enum EpilogueFlags { kWithBias = 1, kWithResidual = 2, kWithGate = 4 };
 
 // Layout of the staged epilogue's read-out: a lane owns CPL consecutive
 // columns of a 64-column half of the quadrant (8 for 2-byte outputs, 4 for
@@ -238,12 +239,13 @@ __device__ __forceinline__ int readout_col(int nw, int h, int lane) {
 template <int EPI, int OUT, int FLAGS>
 __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[4][4],
                                                         const float (&wsc)[2][8], const float (&bsc)[2][8],
-                                                        const float (&as)[4], int mw, int nw, int lane,
-                                                        int8_t* stage, int64_t out_off) {
+                                                        const float (&as)[4], const int (&lbl)[4], int mw, int nw,
+                                                        int lane, int8_t* stage, int64_t out_off) {
   using R = Readout<OUT>;
   constexpr int RB = 256;  // 64 int32 per staged row
   constexpr bool has_bias = (FLAGS & kWithBias) != 0;
   constexpr bool has_res = (FLAGS & kWithResidual) != 0;
+  constexpr bool has_gate = (FLAGS & kWithGate) != 0;
   const int fr = lane & 31, fh = lane >> 5;
   const int orow = lane / R::LPR, ocol = (lane % R::LPR) * R::CPL;
 #pragma unroll
@@ -269,6 +271,18 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
           }
           rres[it] = make_uint4(w[0], w[1], w[2], w[3]);
         }
+      }
+    }
+    // Gate values of the lane's columns for each of its rows (the row's
+    // table row comes from the lane holding its label in the MFMA layout).
+    float gv[R::ITERS][R::CPL];
+    if constexpr (has_gate) {
+#pragma unroll
+      for (int it = 0; it < R::ITERS; ++it) {
+        const int row = it * R::RPI + orow;
+        const float* gr = p.gate + (int64_t)__shfl(lbl[mb], row, 64) * p.ldg;
+#pragma unroll
+        for (int j = 0; j < R::CPL; ++j) gv[it][j] = gr[min(ncol + j, p.n - 1)];
       }
     }
     // acc[nb][mb] group g holds columns 32 nb + 8 g + 4 fh + [0, 4) of row fr.
@@ -306,8 +320,12 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       if constexpr (has_res) {
         const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
 #pragma unroll
-        for (int j = 0; j < R::CPL; ++j)
-          bits[j] = f2h(h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1)))) + h2f((uint16_t)bits[j]));
+        for (int j = 0; j < R::CPL; ++j) {
+          const float res = h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1))));
+          const float branch = h2f((uint16_t)bits[j]);
+          if constexpr (has_gate) bits[j] = f2h_of_f32(__builtin_fmaf(branch, gv[it][j], res));
+          else bits[j] = f2h(res + branch);
+        }
       }
       char* o = reinterpret_cast<char*>(p.out) + (out_off + (int64_t)m * p.ldc + ncol) * R::ES;
       if (m < p.m && full_cols) {
@@ -622,9 +640,12 @@ void gemm_i8_persistent(GemmParams p) {
     // read-out, fetched before the K loop so the epilogue never waits on them.
     float as[4], wsc[2][8];
     uint32_t braw[2][8];
+    int lbl[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < 4; ++mb) {
       as[mb] = EPI != kEpiInt32 ? p.row_scale[min(mw + mb * 32 + fr, p.m - 1)] : 0.0f;
+      if constexpr ((FLAGS & kWithGate) != 0) lbl[mb] = p.labels[min(mw + mb * 32 + fr, p.m - 1)];
+    }
     load_readout_scales<EPI, OUT, (FLAGS & kWithBias) != 0>(p, nw, lane, wsc, braw);
 #pragma unroll
     for (int a = 0; a < 4; ++a)
@@ -671,7 +692,7 @@ void gemm_i8_persistent(GemmParams p) {
         bsc[h][j] = (FLAGS & kWithBias) == 0       ? 0.0f
                     : p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
                                            : __builtin_bit_cast(float, braw[h][j]);
-    store_quadrant32_passes<EPI, OUT, FLAGS>(p, acc, wsc, bsc, as, mw, nw, lane,
+    store_quadrant32_passes<EPI, OUT, FLAGS>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,
                                              smem + kStagingOff + wave * 8192, (item % ksplit) * p.split_stride);
     if constexpr (late_dma) issue(cur ^ 1);
   }
@@ -901,6 +922,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     q.ldc = p.n;
     q.vec16 = (p.n & 3) == 0;
     q.residual = nullptr;
+    q.gate = nullptr;
     q.bias_dtype = 0;
     q.ksplit = ksplit;
     q.split_stride = (int64_t)p.m * p.n;
@@ -917,11 +939,13 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     return p.bias_dtype ? launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s)
                         : launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
   } else {
-    switch ((p.bias_dtype ? kWithBias : 0) | (p.residual ? kWithResidual : 0)) {
+    switch ((p.bias_dtype ? kWithBias : 0) | (p.residual ? kWithResidual : 0) | (p.gate ? kWithGate : 0)) {
       case 0: return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
       case kWithBias: return launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s);
       case kWithResidual: return launch_persistent<EPI, OUT, kWithResidual>(p, tiles, dev, s);
-      default: return launch_persistent<EPI, OUT, kWithBias | kWithResidual>(p, tiles, dev, s);
+      case kWithBias | kWithResidual: return launch_persistent<EPI, OUT, kWithBias | kWithResidual>(p, tiles, dev, s);
+      case kWithResidual | kWithGate: return launch_persistent<EPI, OUT, kWithResidual | kWithGate>(p, tiles, dev, s);
+      default: return launch_persistent<EPI, OUT, kWithBias | kWithResidual | kWithGate>(p, tiles, dev, s);
     }
   }
 }

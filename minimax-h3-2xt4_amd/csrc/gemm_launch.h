@@ -24,6 +24,9 @@ struct GemmParams {
   const void* bias;
   const uint16_t* residual;
   int64_t ldr;
+  const float* gate;      // DiT gate table [R, ldg] (with residual), or null
+  const int32_t* labels;  // row -> gate-table row
+  int64_t ldg;
   void* out;
   int64_t ldc;
   int vec_out;  // out rows allow 4-element vector stores (16-byte base, ldc % 4 == 0)

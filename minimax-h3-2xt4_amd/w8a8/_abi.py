@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -39,7 +39,8 @@ class GemmArgs(ctypes.Structure):
                 ('b', _p), ('ldb', _c.c_int64), ('m', _c.c_int64), ('n', _c.c_int64), ('k', _c.c_int64),
                 ('row_scale', _p), ('col_scale', _p), ('col_scale_stride', _c.c_int64), ('bias', _p),
                 ('bias_dtype', _c.c_int32), ('out_dtype', _c.c_int32), ('residual', _p),
-                ('ldr', _c.c_int64), ('out', _p), ('ldc', _c.c_int64), ('workspace', _p),
+                ('ldr', _c.c_int64), ('gate', _p), ('gate_labels', _p), ('ldg', _c.c_int64), ('out', _p),
+                ('ldc', _c.c_int64), ('workspace', _p),
                 ('workspace_bytes', _c.c_int64), ('stream', _p)]
 
 
@@ -47,8 +48,8 @@ class DequantArgs(ctypes.Structure):
     _fields_ = [('struct_size', _c.c_uint32), ('epilogue', _c.c_int32), ('acc', _p), ('ldacc', _c.c_int64),
                 ('m', _c.c_int64), ('n', _c.c_int64), ('row_scale', _p), ('col_scale', _p),
                 ('col_scale_stride', _c.c_int64), ('bias', _p), ('bias_dtype', _c.c_int32),
-                ('out_dtype', _c.c_int32), ('residual', _p), ('ldr', _c.c_int64), ('out', _p),
-                ('ldc', _c.c_int64), ('stream', _p)]
+                ('out_dtype', _c.c_int32), ('residual', _p), ('ldr', _c.c_int64), ('gate', _p),
+                ('gate_labels', _p), ('ldg', _c.c_int64), ('out', _p), ('ldc', _c.c_int64), ('stream', _p)]
 
 
 STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs)

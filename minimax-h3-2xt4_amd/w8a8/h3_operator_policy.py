@@ -37,28 +37,40 @@ def configure_block(block, kind, policy):
     return block
 
 
-def row_linear(module, x, fallback, comm, input_act=None, residual=None):
+def row_linear(module, x, fallback, comm, input_act=None, residual=None, gate=None, segments=None):
     """Dispatch a row projection; the fused SwiGLU route when the policy selects it.
 
     ``residual`` (FP16, optional) is fused into the GEMM epilogue on the fused
-    route; on the fallback it is added after the storage cast.
+    route; on the fallback it is added after the storage cast. With ``gate``
+    (fp32 [R, N] DiT modulation table) and ``segments`` [(a, b, row)] the
+    update is the gated one (tp_dit.py:160-162 -> h3_tensor_flow.gated_add);
+    the fused route needs segments that tile the rows.
     """
     from . import swiglu_quant as quant
     policy = getattr(module, 'operator_policy', None)
     fused = (policy is not None and policy.fc2_quantizer in ('fused_stored', 'fused_recompute')
              and input_act == 'swiglu' and policy.row_linear_backend != 'native')
-    if fused and quant.supported(x, module.weight, module.weight_scale, module.world_size,
-                                 module.convrot_groupsize):
+    labels = None
+    if gate is not None:
+        if residual is None:
+            raise ValueError('the gate scales the residual update: residual required')
+        rows = x.reshape(-1, x.shape[-1]).shape[0]
+        from .h3_tensor_flow import labels_for
+        labels = labels_for(rows, segments, gate.shape[0], device=x.device)
+    if fused and (gate is None or labels is not None) and quant.supported(
+            x, module.weight, module.weight_scale, module.world_size, module.convrot_groupsize):
         return quant.row_linear(x, module.weight, module.weight_scale, comm, mode=policy.fc2_quantizer,
                                 scaled_transport=policy.row_linear_backend == 'tilelang_scaled_fp16',
-                                residual=residual)
+                                residual=residual, gate=gate, gate_labels=labels)
     if input_act == 'swiglu' or (policy is not None and policy.row_linear_backend == 'tilelang_scaled_fp16'):
         # FP32 preparation island, as the reference keeps on fallback geometry.
         x = x.float()
     out = fallback(x, module.weight, module.weight_scale, comm, module.world_size, module.convrot_groupsize,
                    input_act)
     if residual is not None:
-        from .h3_tensor_flow import residual_add
+        from .h3_tensor_flow import gated_add, residual_add
+        if gate is not None:
+            return gated_add(residual, gate, out.to(residual.dtype), segments)
         out = residual_add(residual, out.to(residual.dtype))
     return out
 

@@ -1,9 +1,10 @@
-"""FP16-fix tensor flow: residual divisor folding and the residual add.
+"""FP16-fix tensor flow: residual divisor folding and the residual updates.
 
 Mirrors the linear-path parts of patches/h3_tensor_flow.py: TensorFlowPolicy
 (:16-37), fold_linear (:82-103; the divisor goes into the FP32 INT8 weight
-scales of the row projections), prepare_tp (:114-127, projection folds) and
-residual_add (:130-131).
+scales of the row projections), prepare_tp (:114-127, projection folds),
+residual_add (:130-131) and gated_add (:145-152), plus the DiT modulation
+segment -> row-label map of patches/tilelang_dit_fusion.py:93-124.
 """
 from dataclasses import dataclass
 
@@ -69,3 +70,41 @@ def prepare_tp(block, kind, policy):
 def residual_add(x, branch):
     """x = cast(f32(x) + f32(branch)) to x's dtype."""
     return (x.float() + branch.float()).to(x.dtype)
+
+
+def segment_key(rows, segments, modulation_rows=9):
+    """Canonical segments when they tile [0, rows) exactly with valid table
+    rows, else None (patches/tilelang_dit_fusion.py:93-100)."""
+    key = tuple(tuple(seg) for seg in segments)
+    cursor = 0
+    for a, b, row in sorted(key):
+        if (any(type(v) is not int for v in (a, b, row)) or a != cursor
+                or not a < b <= rows or not 0 <= row < modulation_rows):
+            return None
+        cursor = b
+    return key if cursor == rows else None
+
+
+def labels_for(rows, segments, modulation_rows=9, device=None):
+    """int32 [rows] gate-table row of every row, or None when the segments do
+    not tile the rows (patches/tilelang_dit_fusion.py:106-124)."""
+    key = segment_key(rows, segments, modulation_rows)
+    if key is None:
+        return None
+    labels = torch.empty(rows, dtype=torch.int32)
+    for a, b, row in key:
+        labels[a:b] = row
+    return labels.to(device) if device is not None else labels
+
+
+def gated_add(x, gate, branch, segments):
+    """Eager DiT gated residual update (:145-152): per segment,
+    x[a:b] = cast(f32(x) + f32(branch) * gate[row]) with torch.addcmul.
+
+    The fused route (the GEMM epilogue with gate=/gate_labels=) computes the
+    same update with one fp32 FMA rounding, as the reference's fused
+    row_gate_kernel does; torch.addcmul's own rounding is not pinned.
+    """
+    for a, b, row in segments:
+        x[a:b].copy_(torch.addcmul(x[a:b].float(), branch[a:b].float(), gate[row].float()).to(x.dtype))
+    return x

@@ -114,15 +114,18 @@ def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_
     return res
 
 
-def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out, device):
+def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out, device, gate=None,
+                   gate_labels=None):
     if epilogue == EPI_INT32:
         if bias is not None or residual is not None:
             raise ValueError('raw int32 output takes no bias or residual')
         out = out if out is not None else torch.empty((m, n), dtype=torch.int32, device=device)
         if out.dtype != torch.int32:
             raise ValueError('int32 output required')
+        if gate is not None:
+            raise ValueError('raw int32 output takes no gate')
         return dict(row_scale=None, col_scale=None, col_scale_stride=0, bias=None, bias_dtype=0,
-                    out_dtype=_abi.I32, residual=None, ldr=0), out, ()
+                    out_dtype=_abi.I32, residual=None, ldr=0, gate=None, gate_labels=None, ldg=0), out, ()
     if epilogue not in (EPI_ROW, EPI_COLUMN):
         raise ValueError('unknown epilogue')
     if out_dtype not in _OUT_DTYPES:
@@ -151,13 +154,28 @@ def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dty
             raise ValueError('residual must be [M, N]')
         ldr = residual.stride(0)
         keep.append(residual)
-    _device(a, w, bias, residual)
+    ldg = 0
+    if gate is not None:
+        if residual is None:
+            raise ValueError('the gate scales the residual update: residual required')
+        gate = gate.to(torch.float32)
+        if gate.ndim != 2 or gate.shape[1] != n or gate.stride(-1) != 1:
+            gate = gate.reshape(-1, n).contiguous()
+        if gate_labels is None or gate_labels.numel() != m:
+            raise ValueError('gate_labels must give one gate-table row per output row')
+        gate_labels = gate_labels.to(torch.int32).reshape(-1).contiguous()
+        ldg = gate.stride(0)
+        keep += [gate, gate_labels]
+    elif gate_labels is not None:
+        raise ValueError('gate_labels without a gate')
+    _device(a, w, bias, residual, gate, gate_labels)
     out = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=device)
     if out.dtype != out_dtype or out.shape != (m, n) or out.stride(-1) != 1:
         raise ValueError('out must be [M, N] of out_dtype with unit column stride')
     return dict(row_scale=a.data_ptr(), col_scale=w.data_ptr(), col_scale_stride=wstride,
                 bias=_abi.ptr(bias), bias_dtype=bias_dtype, out_dtype=_abi.DTYPE_CODE[out_dtype],
-                residual=_abi.ptr(residual), ldr=ldr), out, keep
+                residual=_abi.ptr(residual), ldr=ldr, gate=_abi.ptr(gate), gate_labels=_abi.ptr(gate_labels),
+                ldg=ldg), out, keep
 
 
 _WORKSPACE_BYTES = {}
@@ -174,13 +192,15 @@ def gemm_workspace_bytes(m, n, k, device):
 
 
 def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=None, residual=None,
-         out_dtype=torch.float16, out=None, workspace=None):
+         out_dtype=torch.float16, out=None, workspace=None, gate=None, gate_labels=None):
     """C = q @ weight.T on i8 MFMA with a fused epilogue.
 
     q int8 [M, K], weight int8 [N, K]. epilogue EPI_INT32 -> int32 [M, N];
     EPI_ROW -> out_dtype((C * a) * w [+ bias]); EPI_COLUMN ->
     out_dtype(C * (a * w) [+ bias]); residual (FP16 [M, N]) -> FP16
-    residual + FP16 branch, and out may be the residual itself.
+    residual + FP16 branch, and out may be the residual itself. gate (fp32
+    [R, N]) with gate_labels (int32 [M], each row's table row) turns the
+    residual add into fp16(fma(fp16(branch), gate[label], residual)).
     workspace: optional uint8 device tensor for split K; by default one of
     gemm_workspace_bytes() is allocated when the shape splits K (grids that
     would leave CUs idle). An empty tensor disables the split.
@@ -200,7 +220,7 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
     if k % 16 or q.stride(0) % 16 or weight.stride(0) % 16:
         raise ValueError('K and the operand row strides must be multiples of 16')
     fields, out, keep = _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out,
-                                       q.device)
+                                       q.device, gate, gate_labels)
     if m == 0 or n == 0:
         return out
     if workspace is None:
@@ -219,7 +239,7 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
 
 
 def dequantize(acc, row_scale, col_scale, *, epilogue=EPI_ROW, out_dtype=torch.float16, bias=None, residual=None,
-               out=None):
+               out=None, gate=None, gate_labels=None):
     """Standalone epilogue of an int32 accumulator [M, N]."""
     acc = _rows_2d(acc)
     _device(acc)
@@ -229,7 +249,7 @@ def dequantize(acc, row_scale, col_scale, *, epilogue=EPI_ROW, out_dtype=torch.f
         raise ValueError('dequantize needs the ROW or COLUMN order')
     m, n = acc.shape
     fields, out, keep = _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out,
-                                       acc.device)
+                                       acc.device, gate, gate_labels)
     if m == 0 or n == 0:
         return out
     args = _abi.DequantArgs(epilogue=epilogue, acc=acc.data_ptr(), ldacc=acc.stride(0), m=m, n=n,

@@ -46,13 +46,16 @@ def supported(x, weight, weight_scale, world_size, groupsize):
 
 
 def row_linear(x, weight, weight_scale, comm=None, *, mode='fused_stored', scaled_transport=False,
-               finish_fn=None, consume_input=False, p0_b=False, residual=None):
+               finish_fn=None, consume_input=False, p0_b=False, residual=None, gate=None, gate_labels=None):
     """FC2 row projection; patches/tilelang_swiglu_quant.py:108-128 on one GPU.
 
     Without a residual it returns FP32 (C * a) * w, as the reference does
     before its caller's LoRA add. With ``residual`` (FP16 [M, N], the
     residual stream already divided by the tensor-flow divisor) the GEMM
-    epilogue returns fp16(f32(residual) + f32(fp16(branch))). The scaled FP16
+    epilogue returns fp16(f32(residual) + f32(fp16(branch))), or with
+    ``gate`` (fp32 [R, N]) and ``gate_labels`` (int32 [M]) the DiT gated
+    update fp16(fma(fp16(branch), gate[label], residual)) of the reference's
+    fused row_gate_kernel (patches/tilelang_dit_fusion.py:56-77). The scaled FP16
     transport is a two-rank codec; on one GPU the INT32 accumulator is exact
     and ``scaled_transport`` changes nothing.
     """
@@ -66,5 +69,6 @@ def row_linear(x, weight, weight_scale, comm=None, *, mode='fused_stored', scale
                            out_dtype=torch.float32)
     else:
         out = kernels.gemm(q, weight, epilogue=kernels.EPI_ROW, row_scale=scale, col_scale=weight_scale,
-                           out_dtype=torch.float16, residual=residual.reshape(-1, weight.shape[0]))
+                           out_dtype=torch.float16, residual=residual.reshape(-1, weight.shape[0]),
+                           gate=gate, gate_labels=gate_labels)
     return out.reshape(*shape[:-1], weight.shape[0])

@@ -76,14 +76,17 @@ class RowParallelLinearINT8(nn.Module):
         self.weight.data.copy_(full_weight[:, start:start + self.in_features_per_rank])
         self.weight_scale.data.copy_(full_scale)
 
-    def forward(self, x, reduce_sum=True, input_act=None, *, residual=None, out_dtype=None):
+    def forward(self, x, reduce_sum=True, input_act=None, *, residual=None, gate=None, segments=None,
+                out_dtype=None):
         """Row projection. With ``residual`` (FP16) the result is the updated
-        residual fp16(residual + fp16(branch)); otherwise the branch in
-        ``out_dtype`` (default x's dtype).
+        residual fp16(residual + fp16(branch)), or with the DiT modulation
+        ``gate`` table and ``segments`` the gated update (tp_dit.py:141-162);
+        otherwise the branch in ``out_dtype`` (default x's dtype).
         """
         if not reduce_sum and self.world_size > 1:
             raise ValueError('Quantization-preserving projection requires reduction')
-        out = dispatch_row(self, x, parallel_int8.row_linear, None, input_act, residual=residual)
+        out = dispatch_row(self, x, parallel_int8.row_linear, None, input_act, residual=residual, gate=gate,
+                           segments=segments)
         if residual is not None:
             return out
         return out.to(out_dtype or x.dtype)
@@ -105,9 +108,11 @@ class DiTFeedForwardINT8(nn.Module):
         self.fc1.operator_policy = policy
         self.fc2.operator_policy = policy
 
-    def forward(self, h, residual):
+    def forward(self, h, residual, gate=None, segments=None):
+        """residual <- residual + branch, or with the modulation ``gate`` table
+        and ``segments`` the DiT gated update (tp_dit.py:356-362)."""
         y = self.fc1(h)
-        return self.fc2(y, input_act='swiglu', residual=residual)
+        return self.fc2(y, input_act='swiglu', residual=residual, gate=gate, segments=segments)
 
 
 def chunked_rows(fn, x, *others, chunk_rows=16384, out=None):

@@ -27,6 +27,12 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   where (C*a)*w and C*(a*w) round differently.
 * ``fc2_prologue``      - composition of the pinned pieces, plus the
   invariant that rotated row norms equal the SwiGLU row norms.
+* ``fma_f32``           - exact rational arithmetic (fractions) on random
+  and constructed midpoint cases, where the unfused a*b+c rounds differently.
+* ``gated_residual_add`` - composition of fma_f32 with the FP16 branch and
+  residual casts; the reference's own torch restatement
+  (benchmarks/test_h3_dit_fusion.py:95-106) on inputs where fused and unfused
+  agree.
 
 Functions that only an import of the absent third-party comfy-kitchen 0.2.37
 could pin bit for bit (its GEMM-based rotation summation order) are noted
@@ -38,4 +44,5 @@ from .w8a8_oracle import (  # noqa: F401
     prepare_activation, fc2_prologue, int_mm, dequantize_row,
     dequantize_column, residual_add, to_bf16_bits, from_bf16_bits,
     cast_out, quantize_weight, column_linear, row_linear_fc2, ffn_block,
+    fma_f32, gated_residual_add,
 )

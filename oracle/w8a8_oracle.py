@@ -292,6 +292,47 @@ def residual_add(x, branch):
                 + np.asarray(branch, np.float16).astype(np.float32)).astype(np.float16)
 
 
+def fma_f32(a, b, c):
+    """fp32 fused multiply-add rounded once to nearest even: RN32(a*b + c).
+
+    The GPU's v_fma_f32 / CUDA's __fmaf_rn. numpy has no fma, so: the float64
+    product of two fp32 values is exact (48 significant bits); TwoSum gives
+    the float64 sum s and its exact error e (s + e = a*b + c); rounding s to
+    fp32 is then correct unless s sits exactly on an fp32 midpoint, where the
+    sign of e decides (e == 0 keeps the tie to even).
+    """
+    a64 = _f32(a).astype(np.float64)
+    b64 = _f32(b).astype(np.float64)
+    c64 = _f32(c).astype(np.float64)
+    with np.errstate(over='ignore', invalid='ignore'):
+        prod = a64 * b64
+        s = prod + c64
+        bb = s - prod
+        e = (prod - (s - bb)) + (c64 - bb)
+        r = s.astype(np.float32)
+        d = s - r.astype(np.float64)                      # exact: s and r are within half an fp32 ulp
+        toward = np.where(d > 0, np.float32(np.inf), np.float32(-np.inf))
+        other = np.nextafter(r, toward)                   # the fp32 neighbour on s's side of r
+        mid = (r.astype(np.float64) + other.astype(np.float64)) * 0.5
+        tie = (d != 0) & (s == mid) & (e != 0) & np.isfinite(s)
+        out = np.where(tie & (np.sign(e) == np.sign(d)), other, r)
+    return out.astype(np.float32)
+
+
+def gated_residual_add(x, branch, gate, labels):
+    """DiT gated residual update: f16(fma(f32(f16(branch)), gate[label], f32(x))).
+
+    patches/tilelang_dit_fusion.py:72-75 (row_gate_kernel: the branch is
+    rounded to FP16, then __fmaf_rn with the row's gate and the FP16
+    residual); the eager route is h3_tensor_flow.gated_add (:145-152). gate is
+    the fp32 table [R, N], labels the table row of every output row.
+    """
+    b16 = np.asarray(branch, np.float16).astype(np.float32)
+    g = _f32(gate)[np.asarray(labels, np.int64)]
+    with np.errstate(over='ignore'):
+        return fma_f32(b16, g, np.asarray(x, np.float16).astype(np.float32)).astype(np.float16)
+
+
 def quantize_weight(w):
     """Symmetric per-output-channel INT8 weights with fp32 scales.
 
@@ -311,28 +352,33 @@ def column_linear(x, wq, ws, convrot=True, x_dtype='f16', out_dtype='f16', bias=
     return dequantize_column(int_mm(q, wq, w_f64), a, ws, out_dtype, bias)
 
 
-def row_linear_fc2(x, wq, ws, residual=None, out_dtype='f16', x_dtype='f16', w_f64=None):
+def row_linear_fc2(x, wq, ws, residual=None, out_dtype='f16', x_dtype='f16', w_f64=None, gate=None, labels=None):
     """Row projection with the fused FC2 prologue (fused_stored route).
 
     Follows patches/tilelang_swiglu_quant.py:108-128 on one GPU (the SUM
     transport is the identity): prologue -> int_mm -> row-order dequantize;
     with a residual, the branch is cast to FP16 and added in FP32
-    (patches/h3_tensor_flow.py:130-131).
+    (patches/h3_tensor_flow.py:130-131), or with a gate table and row labels
+    applied as the DiT gated update (gated_residual_add).
     """
     q, a, _ = fc2_prologue(x, x_dtype=x_dtype)
     acc = int_mm(q, wq, w_f64)
     if residual is None:
         return dequantize_row(acc, a, ws, out_dtype)
-    return residual_add(residual, dequantize_row(acc, a, ws, 'f16'))
+    branch = dequantize_row(acc, a, ws, 'f16')
+    if gate is not None:
+        return gated_residual_add(residual, branch, gate, labels)
+    return residual_add(residual, branch)
 
 
-def ffn_block(h, w1q, ws1, w2q, ws2, residual, convrot=True, w1_f64=None, w2_f64=None):
+def ffn_block(h, w1q, ws1, w2q, ws2, residual, convrot=True, w1_f64=None, w2_f64=None, gate=None, labels=None):
     """DiT FFN block of the FP16-fix flow on one GPU.
 
     FC1 column projection (patches/tp_dit.py:356 -> dit_column_linear),
     then FC2 row projection with the fused SwiGLU/ConvRot256 prologue and the
-    residual add (patches/tp_dit.py:360); ws2 already carries the residual
+    residual add (patches/tp_dit.py:360), or with the modulation gate table
+    and row labels the DiT gated update; ws2 already carries the residual
     divisor (patches/h3_tensor_flow.py:82-103,114-127).
     """
     y1 = column_linear(h, w1q, ws1, convrot=convrot, w_f64=w1_f64)
-    return row_linear_fc2(y1, w2q, ws2, residual=residual, w_f64=w2_f64)
+    return row_linear_fc2(y1, w2q, ws2, residual=residual, w_f64=w2_f64, gate=gate, labels=labels)

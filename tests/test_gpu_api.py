@@ -139,6 +139,27 @@ def test_dit_ffn_block_small_exact(gpu):
     assert_bits_equal(np_of(out), want, 'ffn block')
 
 
+def test_dit_ffn_block_gated(gpu):
+    # The DiT block's FC2 with the gate_mlp modulation table and per-frame
+    # segments (patches/tp_dit.py:356-362): the fused gated residual update.
+    data = workloads.dit_ffn(m=512, hidden=768, ffn=1024)
+    block = _ffn_module(data, gpu, 768, 1024)
+    g = torch.Generator().manual_seed(4)
+    gate = torch.randn((9, 768), generator=g)
+    segments = [(0, 200, 3), (200, 450, 0), (450, 512, 8)]
+    out = block(data['h'].to(gpu), data['residual'].to(gpu), gate=gate.to(gpu), segments=segments)
+    labels = np.zeros(512, np.int64)
+    for a, b, row in segments:
+        labels[a:b] = row
+    want = o.ffn_block(np_of(data['h']), np_of(block.fc1.weight), np_of(block.fc1.weight_scale).reshape(-1),
+                       np_of(block.fc2.weight), np_of(block.fc2.weight_scale).reshape(-1), np_of(data['residual']),
+                       gate=np_of(gate), labels=labels)
+    assert_bits_equal(np_of(out), want, 'gated ffn block')
+    with pytest.raises(ValueError):
+        block.fc2(torch.zeros((4, 2048), dtype=torch.float16, device=gpu), input_act='swiglu',
+                  gate=gate.to(gpu), segments=[(0, 4, 0)])
+
+
 def test_dit_ffn_block_full_size_sampled_rows(gpu):
     data = workloads.dit_ffn()
     block = _ffn_module(data, gpu, 3072, 8192)

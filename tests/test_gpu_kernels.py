@@ -342,3 +342,43 @@ def test_swiglu_external_max_fp32_input_and_phases(gpu):
     assert set(only) == {'row_max'}
     assert_bits_equal(np_of(only['row_max']).reshape(-1), o.fc2_prologue(np_of(x), x_dtype='f32')[2].max(-1),
                       'maximum phase')
+
+
+# ------------------------------------------------------------------ DiT gated residual update
+GATE_CASES = [
+    # (m, n, k): persistent tiles with ragged edges, the skinny path, split K
+    (600, 520, 512), (4400, 3072, 256), (48, 1000, 1024), (300, 520, 2048),
+]
+
+
+@pytest.mark.parametrize('m,n,k', GATE_CASES)
+def test_gemm_gated_residual(gpu, m, n, k):
+    g = torch.Generator().manual_seed(m + 3 * n + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.01 + 1e-4
+    ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
+    res = randn16(g, (m, n), 1 / 512)
+    gate = torch.randn((9, n), generator=g)
+    labels = torch.randint(0, 9, (m,), generator=g, dtype=torch.int32)
+    got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       out_dtype=torch.float16, residual=res.to(gpu), gate=gate.to(gpu), gate_labels=labels.to(gpu))
+    branch = o.dequantize_row(o.int_mm(np_of(a), np_of(b)), np_of(rs).reshape(-1), np_of(ws).reshape(-1), 'f16')
+    want = o.gated_residual_add(np_of(res), branch, np_of(gate), np_of(labels))
+    assert_bits_equal(np_of(got), want, f'gated residual {m}x{n}x{k}')
+
+
+def test_dequantize_gated_residual(gpu):
+    g = torch.Generator().manual_seed(17)
+    rows, width = 37, 300
+    acc = torch.randint(-3000000, 3000000, (rows, width), generator=g, dtype=torch.int32)
+    a = torch.rand((rows, 1), generator=g) * 1e-3
+    w = torch.rand((width,), generator=g) * 1e-3
+    res = randn16(g, (rows, width))
+    gate = torch.randn((3, width), generator=g)
+    labels = torch.randint(0, 3, (rows,), generator=g, dtype=torch.int32)
+    got = kernels.dequantize(acc.to(gpu), a.to(gpu), w.to(gpu), epilogue=kernels.EPI_ROW, residual=res.to(gpu),
+                             gate=gate.to(gpu), gate_labels=labels.to(gpu))
+    want = o.gated_residual_add(np_of(res), o.dequantize_row(np_of(acc), np_of(a), np_of(w), 'f16'), np_of(gate),
+                                np_of(labels))
+    assert_bits_equal(np_of(got), want, 'dequantize gated')

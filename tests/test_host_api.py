@@ -89,3 +89,12 @@ def test_workload_shapes_and_determinism():
     assert 1 <= big <= 8
     f = workloads.dit_ffn(m=32)
     assert f['w1'].shape == (16384, 3072) and f['w2'].shape == (3072, 8192) and f['residual'].shape == (32, 3072)
+
+
+def test_segment_labels():
+    from w8a8.h3_tensor_flow import labels_for, segment_key
+    assert segment_key(5, [(0, 2, 7), (2, 5, 0)]) == ((0, 2, 7), (2, 5, 0))
+    for segments in ([(0, 2, 0)], [(0, 3, 0), (2, 5, 1)], [(0, 5, 9)]):
+        assert segment_key(5, segments) is None      # gap, overlap, row out of range
+    assert labels_for(5, [(2, 5, 0), (0, 2, 7)]).tolist() == [7, 7, 0, 0, 0]
+    assert labels_for(5, [(0, 4, 1)]) is None

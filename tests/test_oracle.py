@@ -284,3 +284,53 @@ def test_end_to_end_linear_close_to_float64():
     assert np.abs(y - ref).max() / np.abs(ref).max() < 0.03
     with pytest.raises(ValueError):
         o.int_mm(np.zeros((2, 8), np.int8), np.zeros((3, 16), np.int8))
+
+
+# ------------------------------------------------------------------ fused multiply-add and the DiT gate
+def _rn32_exact(value):
+    """Round an exact Fraction to fp32 (nearest, ties to even) by brute force."""
+    from fractions import Fraction
+    f = np.float32(float(value))
+    cands = [np.nextafter(f, np.float32(-np.inf)), f, np.nextafter(f, np.float32(np.inf))]
+    dist = [abs(Fraction(float(c)) - value) for c in cands]
+    best = [c for c, d in zip(cands, dist) if d == min(dist)]
+    if len(best) > 1:
+        best = [c for c in best if (np.asarray(c, np.float32).view(np.uint32) & 1) == 0]
+    return best[0]
+
+
+def test_fma_f32_matches_exact_rational_rounding():
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    a = (rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 8, 3000)).astype(np.float32)
+    b = (rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 8, 3000)).astype(np.float32)
+    c = (rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 8, 3000)).astype(np.float32)
+    got = o.fma_f32(a, b, c)
+    for i in range(3000):
+        want = _rn32_exact(Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i])))
+        assert got[i] == want, (i, a[i], b[i], c[i], got[i], want)
+
+
+def test_fma_f32_single_rounding_and_midpoint_correction():
+    one = np.float32(1 + 2.0 ** -12)
+    # fused keeps the 2^-24 term that the unfused product rounds away (tie to even)
+    assert o.fma_f32(one, one, np.float32(-1.0)) == np.float32(2.0 ** -11 + 2.0 ** -24)
+    assert (one * one) - np.float32(1.0) == np.float32(2.0 ** -11)
+    # a*b = 1 + 2^-11 + 2^-24 is an fp32 midpoint; the float64 sum loses +-2^-80,
+    # which must still decide the direction
+    assert o.fma_f32(one, one, np.float32(2.0 ** -80)) == np.float32(1 + 2.0 ** -11 + 2.0 ** -23)
+    assert o.fma_f32(one, one, np.float32(-(2.0 ** -80))) == np.float32(1 + 2.0 ** -11)
+    assert o.fma_f32(one, one, np.float32(0.0)) == np.float32(1 + 2.0 ** -11)   # exact tie: even
+
+
+def test_gated_residual_add_composition():
+    x = np.array([[1.0, -2.0], [0.5, 3.0]], np.float16)
+    branch = np.array([[0.25, 1.0], [2.0, -1.0]], np.float32)
+    gate = np.array([[2.0, 0.5], [-1.0, 4.0], [0.0, 0.0]], np.float32)
+    labels = np.array([1, 0])
+    got = o.gated_residual_add(x, branch, gate, labels)
+    want = np.array([[1.0 - 0.25, -2.0 + 4.0], [0.5 + 4.0, 3.0 - 0.5]], np.float16)
+    assert np.array_equal(got, want)
+    # the branch is rounded to FP16 before the FMA (tilelang_dit_fusion.py:72-75)
+    b = np.array([[1 + 2.0 ** -12]], np.float32)
+    assert o.gated_residual_add(np.zeros((1, 1), np.float16), b, np.ones((1, 1), np.float32), [0])[0, 0] == 1.0
