@@ -440,7 +440,46 @@ def run_dit_half_shard(args, torch, dev):
                 config=dict(workload='dit_half_shard', m=m, chunk=chunk, qkv=s['qkv'], ffn=s['ffn']))
 
 
-WORKLOADS = {'dit_ffn': run_dit_ffn, 'copy': run_copy, 'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv,
+def run_dit_norm(args, torch, dev):
+    """DiT norm2 -> FC1 input at M=16384, hidden 3072: modulated RMSNorm fused
+    with ConvRot256 and per-row INT8 (one kernel), against the same work as two
+    kernels (norm to an FP16 tensor, then the quantizer)."""
+    from w8a8 import h3_tensor_flow as flow, kernels, workloads
+    data = workloads.dit_norm()
+    m, k = data['x'].shape
+    x, w, shift, scale = (data[n].to(dev) for n in ('x', 'weight', 'shift', 'scale'))
+    labels = flow.labels_for(m, data['segments'], shift.shape[0], device=dev)
+    eps = data['eps']
+
+    def fused():
+        return kernels.norm_quantize(x, w, shift, scale, labels, eps=eps)
+
+    def unfused():
+        y = kernels.norm_quantize(x, w, shift, scale, labels, eps=eps, quantize=False)['y']
+        return kernels.quantize_rows(y, convrot=True, round_rotated=True)
+
+    tf = graph_timed(torch, fused, args.steps * 4, args.warmup)
+    tu = graph_timed(torch, unfused, args.steps * 4, args.warmup)
+    nbytes = m * k * 2 + m * k + 4 * m          # x read, codes and scales written (tables stay in cache)
+    gbs = nbytes / (tf * 1e-3) / 1e9
+    res = dict(metric='DiT modulated RMSNorm -> ConvRot256 -> INT8, 16384x3072 us', value=round(tf * 1e3, 2),
+               unit='us', higher_is_better=False, dtype='f32', data='synthetic',
+               config=dict(workload='dit_norm', m=m, k=k, mod_rows=shift.shape[0], segments=len(data['segments'])),
+               roofline=dict(bound='hbm', achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit='GB/s',
+                             frac=round(gbs / PEAK_HBM_GBS, 4), traffic=None),
+               unfused_us=round(tu * 1e3, 2), fusion_speedup=round(tu / tf, 3))
+    if not args.no_cpu_baseline:
+        import oracle as o
+        rows = min(args.cpu_rows, m)
+        lab = labels[:rows].cpu().numpy()
+        xs, wn, sh, sc = (t.cpu().numpy() for t in (data['x'][:rows], data['weight'], data['shift'], data['scale']))
+        t = _cpu_rows_timing(lambda: o.norm_quantize(xs, wn, sh, sc, lab, eps=eps)) * m / rows
+        res['cpu_baseline'] = dict(value=round(t * 1e6, 1), unit='us', cores=1, kind='port',
+                                   sample=f'oracle norm_quantize (numpy) on {rows} of {m} rows, scaled x{m / rows:g}')
+    return res
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_norm': run_dit_norm, 'copy': run_copy, 'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
 
 

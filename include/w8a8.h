@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 3
+#define W8A8_ABI_VERSION 4
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -128,6 +128,57 @@ typedef struct W8A8SwigluArgs {
 } W8A8SwigluArgs;
 
 int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
+
+/*
+ * DiT modulated RMSNorm, optionally fused with ConvRot256 and the per-row
+ * quantizer (the QKV / FC1 input preparation), so the normalized tensor
+ * need not make an HBM round trip before its quantization.
+ * Replaces: patches/tilelang_dit_fusion.py:10-36 (norm_kernel) and
+ *           :127-135 (modulated_norm), patches/h3_tensor_flow.py:134-142
+ *           (modulated_norm), then patches/dit_column_linear.py:13-21
+ *           (_prepare_activation) on its output.
+ * x: [rows, cols] F16 or BF16, row stride ldx elements.
+ * weight: optional [cols] fp32 norm gain (NULL: no gain).
+ * mod_shift, mod_scale: optional fp32 AdaLN tables [mod_rows, ld_mod] (both
+ *   or neither); labels: int32 [rows], each row's table row in
+ *   [0, mod_rows) (values outside are clamped into that range).
+ * Per row, in fp32 (round to nearest even, no contraction):
+ *   ss   = sum of x*x in a fixed order: lane l of 64 adds, in order, the
+ *          squares of elements 16u..16u+15 of units u = l, l+64, l+128, ...;
+ *          the 64 partials then meet in an xor butterfly (offsets 32..1)
+ *   inv  = 1 / sqrt(ss * fp32(1/cols) + eps)      (IEEE sqrt and division)
+ *   y    = x_dtype(((((x * inv) * w) * (1 + mod_scale[l])) + mod_shift[l]))
+ * y: optional [rows, cols] x_dtype output of the normalized rows (ldy).
+ * convrot, round_rotated, q, ldq, q_scale: as w8a8_quantize_rows applied to
+ *   y. q NULL runs the norm alone (y required).
+ * Requirements: cols % 16 == 0 (cols % 256 == 0 with convrot and q), x, y,
+ *   q and every table 16-byte aligned with 16-byte row strides.
+ */
+typedef struct W8A8NormArgs {
+  uint32_t struct_size;
+  int32_t x_dtype;
+  const void* x;
+  int64_t ldx;
+  int64_t rows;
+  int64_t cols;
+  const float* weight;
+  const float* mod_shift;
+  const float* mod_scale;
+  int64_t ld_mod;
+  int32_t mod_rows;
+  float eps;
+  const int32_t* labels;
+  void* y;
+  int64_t ldy;
+  int32_t convrot;
+  int32_t round_rotated;
+  int8_t* q;
+  int64_t ldq;
+  float* q_scale;
+  void* stream;
+} W8A8NormArgs;
+
+int w8a8_norm_quantize(const W8A8NormArgs* args);
 
 /*
  * INT8 GEMM on gfx950 i8 MFMA with a fused epilogue.
@@ -238,7 +289,7 @@ int w8a8_dequantize(const W8A8DequantArgs* args);
 int w8a8_abi_version(void);
 
 /* sizeof of each argument struct, by index: 0 Quant, 1 Swiglu, 2 Gemm,
- * 3 Dequant; -1 for an unknown index. Lets bindings verify their layout. */
+ * 3 Dequant, 4 Norm; -1 for an unknown index. Lets bindings verify their layout. */
 int64_t w8a8_struct_size(int32_t which);
 
 /* Message describing the last error returned on the calling thread. */

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -52,9 +52,20 @@ class DequantArgs(ctypes.Structure):
                 ('gate_labels', _p), ('ldg', _c.c_int64), ('out', _p), ('ldc', _c.c_int64), ('stream', _p)]
 
 
-STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs)
-ENTRY_POINTS = ('w8a8_quantize_rows', 'w8a8_swiglu_quantize', 'w8a8_gemm', 'w8a8_dequantize',
-                'w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error', 'w8a8_gemm_workspace_size')
+class NormArgs(ctypes.Structure):
+    _fields_ = [('struct_size', _c.c_uint32), ('x_dtype', _c.c_int32), ('x', _p), ('ldx', _c.c_int64),
+                ('rows', _c.c_int64), ('cols', _c.c_int64), ('weight', _p), ('mod_shift', _p),
+                ('mod_scale', _p), ('ld_mod', _c.c_int64), ('mod_rows', _c.c_int32), ('eps', _c.c_float),
+                ('labels', _p), ('y', _p), ('ldy', _c.c_int64), ('convrot', _c.c_int32),
+                ('round_rotated', _c.c_int32), ('q', _p), ('ldq', _c.c_int64), ('q_scale', _p), ('stream', _p)]
+
+
+# Argument structs in w8a8_struct_size() index order, with their entry points.
+STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs, NormArgs)
+STRUCT_ENTRY_POINTS = ('w8a8_quantize_rows', 'w8a8_swiglu_quantize', 'w8a8_gemm', 'w8a8_dequantize',
+                       'w8a8_norm_quantize')
+ENTRY_POINTS = STRUCT_ENTRY_POINTS + ('w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error',
+                                      'w8a8_gemm_workspace_size')
 
 _LIB = None
 
@@ -83,7 +94,7 @@ def load(path=None):
     lib.w8a8_last_error.restype = _c.c_char_p
     lib.w8a8_gemm_workspace_size.restype = _c.c_int64
     lib.w8a8_gemm_workspace_size.argtypes = [_c.c_int64, _c.c_int64, _c.c_int64]
-    for name, st in zip(ENTRY_POINTS[:4], STRUCTS):
+    for name, st in zip(STRUCT_ENTRY_POINTS, STRUCTS):
         fn = getattr(lib, name)
         fn.restype = _c.c_int
         fn.argtypes = [ctypes.POINTER(st)]

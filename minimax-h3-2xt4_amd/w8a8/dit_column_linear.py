@@ -74,6 +74,18 @@ def column_linear(x, weight, weight_scale, *, convrot=True, convrot_groupsize=25
     return output.reshape(*shape[:-1], weight.shape[0])
 
 
+def column_linear_quantized(codes, row_scale, weight, weight_scale, *, out_dtype=torch.float16, bias=None):
+    """Column projection of an activation already prepared (ConvRot256 and
+    per-row INT8, e.g. by the fused modulated-norm kernel): the GEMM with the
+    column-order epilogue of column_linear, without the preparation.
+    """
+    if codes.dtype != torch.int8 or codes.ndim != 2 or codes.shape[1] != weight.shape[-1]:
+        raise ValueError('codes must be int8 [M, in_features]')
+    weight = weight.to(device=codes.device).contiguous()
+    scale = _weight_scale(weight, weight_scale, codes.device)
+    return _column(codes, row_scale, weight, scale, out_dtype, bias)
+
+
 def _eager_column(x, weight, weight_scale, *, convrot, convrot_groupsize, out_dtype, backend='preallocated'):
     return column_linear(x, weight, weight_scale, convrot=convrot, convrot_groupsize=convrot_groupsize,
                          out_dtype=out_dtype, backend=backend)

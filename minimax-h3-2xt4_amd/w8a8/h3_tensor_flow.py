@@ -3,13 +3,16 @@
 Mirrors the linear-path parts of patches/h3_tensor_flow.py: TensorFlowPolicy
 (:16-37), fold_linear (:82-103; the divisor goes into the FP32 INT8 weight
 scales of the row projections), prepare_tp (:114-127, projection folds),
-residual_add (:130-131) and gated_add (:145-152), plus the DiT modulation
-segment -> row-label map of patches/tilelang_dit_fusion.py:93-124.
+residual_add (:130-131), modulated_norm (:134-142) and gated_add
+(:145-152), plus the DiT modulation segment -> row-label map of
+patches/tilelang_dit_fusion.py:93-124.
 """
 from dataclasses import dataclass
 
 import torch
 from torch import nn
+
+from . import kernels
 
 
 @dataclass(frozen=True)
@@ -108,3 +111,54 @@ def gated_add(x, gate, branch, segments):
     for a, b, row in segments:
         x[a:b].copy_(torch.addcmul(x[a:b].float(), branch[a:b].float(), gate[row].float()).to(x.dtype))
     return x
+
+
+def _norm_args(norm, x, shift, scale, segments):
+    if x.ndim != 2:
+        raise ValueError('modulated_norm expects [tokens, hidden] rows')
+    if tuple(norm.normalized_shape) != (x.shape[1],) or getattr(norm, 'layer_norm', False):
+        raise ValueError('an RMSNorm over the hidden dimension is required')
+    weight = getattr(norm, 'weight', None)
+    if weight is not None:
+        weight = weight.detach().to(device=x.device, dtype=torch.float32)
+    eps = norm.eps if norm.eps is not None else torch.finfo(torch.float32).eps
+    labels = None
+    if shift is not None:
+        labels = labels_for(x.shape[0], segments, shift.shape[0], device=x.device)
+        if labels is None:
+            raise ValueError('segments must tile the rows with valid modulation-table rows')
+        shift = shift.to(torch.float32)
+        scale = scale.to(torch.float32)
+    return weight, eps, labels, shift, scale
+
+
+def modulated_norm(norm, x, shift, scale, segments, *, fused=False):
+    """DiT modulated RMSNorm (patches/h3_tensor_flow.py:134-142, fused route
+    patches/tilelang_dit_fusion.py:10-36,127-135) on the libw8a8 kernel:
+
+    y = cast((((x * inv) * w) * (1 + scale[row])) + shift[row]) per segment
+    row, inv = 1 / sqrt(mean(x*x) + eps), in fp32. ``fused`` is accepted for
+    API compatibility; both routes run the one kernel (the sum of squares in
+    its fixed order, IEEE sqrt and division in place of rsqrtf). shift and
+    scale are the [R, hidden] modulation tables; None for a plain RMSNorm.
+    """
+    weight, eps, labels, shift, scale = _norm_args(norm, x, shift, scale, segments)
+    return kernels.norm_quantize(x, weight, shift, scale, labels, eps=eps, quantize=False)['y']
+
+
+def modulated_norm_quantize(norm, x, shift, scale, segments, *, convrot=True, convrot_groupsize=256,
+                            want_normalized=False):
+    """modulated_norm fused with the column path's activation preparation
+    (ConvRot256 rounded to x's dtype, then per-row INT8): returns
+    (codes int8 [M, hidden], row_scale fp32 [M, 1]) and, with
+    want_normalized, the normalized rows as a third item. The codes equal
+    those of quantizing modulated_norm's output (patches/dit_column_linear.py:13-21).
+    """
+    if convrot and convrot_groupsize != 256:
+        raise ValueError('only the regular-H4 ConvRot256 group size is supported')
+    weight, eps, labels, shift, scale = _norm_args(norm, x, shift, scale, segments)
+    r = kernels.norm_quantize(x, weight, shift, scale, labels, eps=eps, convrot=bool(convrot),
+                              want_normalized=want_normalized)
+    if want_normalized:
+        return r['q'], r['scale'], r['y']
+    return r['q'], r['scale']

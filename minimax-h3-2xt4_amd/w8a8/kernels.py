@@ -74,6 +74,78 @@ def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=Non
     return q, scale
 
 
+def _table(t, name, cols):
+    if t.dtype != torch.float32 or t.ndim != 2 or t.shape[1] != cols:
+        raise ValueError(f'{name} must be a float32 [rows, {cols}] table')
+    if t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, *, eps, quantize=True, convrot=True,
+                  round_rotated=True, want_normalized=False):
+    """Modulated RMSNorm of x [M, K] (F16/BF16), optionally fused with
+    ConvRot256 and per-row INT8 quantization.
+
+    y = x_dtype(((((x * inv) * weight) * (1 + scale[label])) + shift[label]))
+    with inv = 1 / sqrt(sum(x*x) * fp32(1/K) + eps); weight [K] fp32 (None:
+    no gain); shift/scale fp32 [R, K] AdaLN tables with labels int32 [M]
+    (each row's table row), or None for a plain RMSNorm.
+    Returns a dict with 'q' [M,K] int8 and 'scale' [M,1] fp32 when quantize,
+    and 'y' [M,K] (x's dtype) when want_normalized or not quantize.
+    """
+    x = _rows_2d(x)
+    _device(x, weight, shift, scale, labels)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError('x must be float16 or bfloat16')
+    rows, cols = x.shape
+    if cols % 16 or (quantize and convrot and cols % 256):
+        raise ValueError('input features must be a multiple of 16 (256 with ConvRot256)')
+    if x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    if weight is not None:
+        weight = weight.reshape(-1)
+        if weight.dtype != torch.float32 or weight.numel() != cols:
+            raise ValueError(f'weight must be float32 with {cols} entries')
+        weight = weight.contiguous()
+        if weight.data_ptr() % 16:
+            weight = weight.clone()
+    if (shift is None) != (scale is None):
+        raise ValueError('shift and scale go together')
+    if shift is not None:
+        shift = _table(shift, 'shift', cols)
+        scale = _table(scale, 'scale', cols)
+        if scale.shape[0] != shift.shape[0] or scale.stride(0) != shift.stride(0):
+            scale = scale.contiguous()
+            shift = shift.contiguous()
+            if scale.shape[0] != shift.shape[0]:
+                raise ValueError('shift and scale tables must have the same rows')
+        if labels is None or labels.dtype != torch.int32 or labels.numel() != rows:
+            raise ValueError('modulation tables need int32 labels, one per row')
+        labels = labels.reshape(-1).contiguous()
+    out = {}
+    want_y = want_normalized or not quantize
+    y = torch.empty((rows, cols), dtype=x.dtype, device=x.device) if want_y else None
+    q = torch.empty((rows, cols), dtype=torch.int8, device=x.device) if quantize else None
+    qs = torch.empty((rows, 1), dtype=torch.float32, device=x.device) if quantize else None
+    if quantize:
+        out['q'], out['scale'] = q, qs
+    if want_y:
+        out['y'] = y
+    if rows == 0:
+        return out
+    args = _abi.NormArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows, cols=cols,
+                         weight=_abi.ptr(weight), mod_shift=_abi.ptr(shift), mod_scale=_abi.ptr(scale),
+                         ld_mod=shift.stride(0) if shift is not None else 0,
+                         mod_rows=shift.shape[0] if shift is not None else 0, eps=float(eps),
+                         labels=_abi.ptr(labels), y=_abi.ptr(y), ldy=cols if y is not None else 0,
+                         convrot=256 if convrot else 0, round_rotated=1 if round_rotated else 0,
+                         q=_abi.ptr(q), ldq=cols if q is not None else 0, q_scale=_abi.ptr(qs),
+                         stream=_abi.stream_of(x))
+    _abi.call('w8a8_norm_quantize', args)
+    return out
+
+
 def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_group_max=False):
     """Fused FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8 of x [M, 2W].
 

@@ -12,7 +12,8 @@ import torch
 from torch import nn
 
 from . import parallel_int8
-from .dit_column_linear import column_linear
+from .dit_column_linear import column_linear, column_linear_quantized
+from .h3_tensor_flow import modulated_norm_quantize
 from .h3_operator_policy import H3OperatorPolicy, row_linear as dispatch_row
 
 
@@ -42,7 +43,13 @@ class ColumnParallelLinearINT8(nn.Module):
         self.weight.data.copy_(w)
         self.weight_scale.data.copy_(scale)
 
-    def forward(self, x):
+    def forward(self, x, *, prepared=None):
+        """``prepared`` = (codes, row_scale) of x already rotated and quantized
+        (modulated_norm_quantize); x then only supplies the shape and dtype."""
+        if prepared is not None:
+            out = column_linear_quantized(prepared[0], prepared[1], self.weight, self.weight_scale,
+                                          out_dtype=x.dtype)
+            return out.view(*x.shape[:-1], self.out_features_per_rank)
         policy = getattr(self, 'operator_policy', None)
         backend = 'preallocated' if policy is None else policy.column_linear_backend
         out = column_linear(x.reshape(-1, self.in_features), self.weight, self.weight_scale,
@@ -113,6 +120,17 @@ class DiTFeedForwardINT8(nn.Module):
         and ``segments`` the DiT gated update (tp_dit.py:356-362)."""
         y = self.fc1(h)
         return self.fc2(y, input_act='swiglu', residual=residual, gate=gate, segments=segments)
+
+    def forward_modulated(self, x, norm, shift, scale, gate, segments):
+        """The DiT FFN sublayer from the residual stream (patches/tp_dit.py:347-362):
+        x + gate * FFN(modulated_norm(norm, x, shift, scale)), with the norm
+        fused into FC1's activation quantization (the normalized rows never
+        reach HBM) and the gated residual update in FC2's epilogue.
+        """
+        codes, row_scale = modulated_norm_quantize(norm, x, shift, scale, segments, convrot=self.fc1.convrot,
+                                                   convrot_groupsize=self.fc1.convrot_groupsize)
+        y = self.fc1(x, prepared=(codes, row_scale))
+        return self.fc2(y, input_act='swiglu', residual=x, gate=gate, segments=segments)
 
 
 def chunked_rows(fn, x, *others, chunk_rows=16384, out=None):

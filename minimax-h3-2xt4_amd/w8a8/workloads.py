@@ -26,6 +26,9 @@ SHAPES = {
     'dit_qkv': dict(seed=2, m=53504, k=3072, n=9216, outliers=3),
     'te_skinny': dict(seed=3, ms=(1, 64, 512), hidden=4096, ffn=14336),
     'dit_half_shard': dict(seed=4, m=204336, hidden=3072, qkv=4608, ffn=4096, chunk=16384, outliers=8),
+    # DiT residual stream -> norm2 with the AdaLN tables (9 modulation rows,
+    # per-frame segments) -> FC1 input; eps after the 512^2 fold.
+    'dit_norm': dict(seed=5, m=16384, hidden=3072, mod_rows=9, frames=16, eps=1e-6 / RESIDUAL_DIVISOR ** 2),
 }
 
 
@@ -95,6 +98,22 @@ def dit_half_shard(m=None, seed=None):
     w1 = weights(g, 2 * s['ffn'], s['hidden'])
     w2 = weights(g, s['hidden'], s['ffn'])
     return dict(h=h, w_qkv=w_qkv, w1=w1, w2=w2)
+
+
+def dit_norm(m=None, hidden=None, seed=None):
+    """Residual-stream rows, RMSNorm gain, AdaLN shift/scale tables and
+    per-frame segments (equal row blocks cycling over the table rows)."""
+    s = SHAPES['dit_norm']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m, hidden = m or s['m'], hidden or s['hidden']
+    x = activations(g, m, hidden, 8, sigma=3.0)
+    weight = torch.rand((hidden,), generator=g) + 0.5
+    shift = torch.randn((s['mod_rows'], hidden), generator=g) * 0.1
+    scale = torch.randn((s['mod_rows'], hidden), generator=g) * 0.1
+    frames = min(s['frames'], m)
+    bounds = [m * i // frames for i in range(frames + 1)]
+    segments = [(bounds[i], bounds[i + 1], i % s['mod_rows']) for i in range(frames) if bounds[i] < bounds[i + 1]]
+    return dict(x=x, weight=weight, shift=shift, scale=scale, segments=segments, eps=s['eps'])
 
 
 def quantize_weight(w, device):

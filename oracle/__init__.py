@@ -33,6 +33,17 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   residual casts; the reference's own torch restatement
   (benchmarks/test_h3_dit_fusion.py:95-106) on inputs where fused and unfused
   agree.
+* ``rms_sum_squares``   - exact totals on integer squares (any order),
+  hand-computed known answers whose value depends on the lane order and on
+  the butterfly (absorption of small squares by a 2^24 partial), padding
+  of a partial last lane block, and a float64 error bound on random rows.
+* ``modulated_rms_norm`` - numpy's float32 sqrt and division checked against
+  float64 rounded once (exact for these two operations); closed cases
+  (constant power-of-two rows give +-1 exactly; scale = -1 yields the shift
+  table row exactly, which pins the label indexing), and a float64 bound
+  against torch's own fp32 F.rms_norm on random rows.
+* ``norm_quantize``     - composition of the pinned norm with the pinned
+  ``prepare_activation`` / ``convrot256`` + ``quantize_rows``.
 
 Functions that only an import of the absent third-party comfy-kitchen 0.2.37
 could pin bit for bit (its GEMM-based rotation summation order) are noted
@@ -44,5 +55,6 @@ from .w8a8_oracle import (  # noqa: F401
     prepare_activation, fc2_prologue, int_mm, dequantize_row,
     dequantize_column, residual_add, to_bf16_bits, from_bf16_bits,
     cast_out, quantize_weight, column_linear, row_linear_fc2, ffn_block,
-    fma_f32, gated_residual_add,
+    fma_f32, gated_residual_add, rms_sum_squares, modulated_rms_norm,
+    norm_quantize,
 )

@@ -333,6 +333,91 @@ def gated_residual_add(x, branch, gate, labels):
         return fma_f32(b16, g, np.asarray(x, np.float16).astype(np.float32)).astype(np.float16)
 
 
+LANES = 64
+
+
+def rms_sum_squares(x):
+    """Per-row fp32 sum of squares in this build's fixed order.
+
+    The reference sums the squares with TileLang's T.reduce_sum
+    (patches/tilelang_dit_fusion.py:21-26: squares via __fmul_rn, zero past
+    the width), whose order is the compiler's; this build fixes one: the
+    row is cut into 16-element units, lane l of 64 adds, in order, the squares
+    of units l, l+64, l+128, ... (elements in column order) to a partial
+    starting at +0, then the 64 partials meet in an xor butterfly (offsets
+    32, 16, 8, 4, 2, 1: p[l] = p[l] + p[l ^ off]). Addition is commutative
+    in IEEE arithmetic, so every lane ends with the same total.
+    """
+    x = _f32(x)
+    rows, cols = x.shape
+    if cols % 16:
+        raise ValueError('whole 16-element units required')
+    units = cols // 16
+    j = max(1, -(-units // LANES))
+    sq = np.zeros((rows, j * LANES * 16), np.float32)
+    with np.errstate(over='ignore'):
+        sq[:, :cols] = x * x
+    sq = sq.reshape(rows, j, LANES, 16)
+    part = np.zeros((rows, LANES), np.float32)
+    with np.errstate(over='ignore', invalid='ignore'):
+        for jj in range(j):
+            for i in range(16):
+                part = part + sq[:, jj, :, i]
+        lane = np.arange(LANES)
+        for off in (32, 16, 8, 4, 2, 1):
+            part = part + part[:, lane ^ off]
+    return part[:, 0].copy()
+
+
+def modulated_rms_norm(x, weight=None, shift=None, scale=None, labels=None, eps=1e-6, x_dtype='f16'):
+    """DiT modulated RMSNorm in the fused kernel's fp32 operation order.
+
+    patches/tilelang_dit_fusion.py:27-34 (norm_kernel): mean = ss * fp32(1/W);
+    inv = rsqrtf(mean + eps); value = x * inv; gain = value * w;
+    factor = 1 + scale[label]; y = x_dtype((gain * factor) + shift[label]),
+    each step one fp32 rounding (__fmul_rn / __fadd_rn). Here rsqrtf (CUDA's
+    approximate reciprocal square root, not reproduced) is replaced by a
+    correctly rounded sqrt followed by a correctly rounded division, and the
+    sum of squares follows ``rms_sum_squares``. The eager route
+    (patches/h3_tensor_flow.py:134-142: F.rms_norm in fp32, then
+    mul_(1 + scale).add_(shift) per segment) has the same sequence of
+    operations. weight None: no gain; shift/scale None: plain RMSNorm.
+    Returns x_dtype values (float16, or bf16 bit patterns as uint16).
+    """
+    xf = _to_f32(x, x_dtype)
+    rows, cols = xf.shape
+    ss = rms_sum_squares(xf)
+    with np.errstate(over='ignore', invalid='ignore', divide='ignore'):
+        mean = ss * F32(1.0 / cols)
+        inv = F32(1.0) / np.sqrt(mean + F32(eps))
+        y = xf * inv[:, None]
+        if weight is not None:
+            y = y * _f32(weight).reshape(1, -1)
+        if shift is not None:
+            lab = np.asarray(labels, np.int64).reshape(-1)
+            factor = F32(1.0) + _f32(scale)[lab]
+            y = y * factor
+            y = y + _f32(shift)[lab]
+    return cast_out(y.astype(np.float32), x_dtype)
+
+
+def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, eps=1e-6, x_dtype='f16', convrot=True,
+                  round_rotated=True):
+    """Modulated RMSNorm followed by the column path's activation preparation.
+
+    The composition of patches/tilelang_dit_fusion.py:10-36 (normalized rows
+    stored in x's dtype) and patches/dit_column_linear.py:13-21 on them;
+    round_rotated=False keeps the rotated values in fp32 instead.
+    Returns (q int8, scale fp32 [M], y) with y the normalized rows.
+    """
+    y = modulated_rms_norm(x, weight, shift, scale, labels, eps, x_dtype)
+    if convrot and not round_rotated:
+        q, s = quantize_rows(convrot256(_to_f32(y, x_dtype)))
+    else:
+        q, s = prepare_activation(y, convrot, x_dtype)
+    return q, s, y
+
+
 def quantize_weight(w):
     """Symmetric per-output-channel INT8 weights with fp32 scales.
 

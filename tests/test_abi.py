@@ -35,7 +35,7 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 184, 144]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 184, 144, 144]
 
 
 def _expect_invalid(name, args, fragment):
@@ -93,6 +93,27 @@ def test_dequantize_argument_checks():
     _expect_invalid('w8a8_dequantize', _abi.DequantArgs(**base), 'ROW or COLUMN')
     _expect_invalid('w8a8_dequantize', _abi.DequantArgs(**{**base, 'epilogue': _abi.EPI_ROW,
                                                             'col_scale_stride': 3}), 'stride')
+
+
+def test_norm_argument_checks():
+    base = dict(struct_size=ctypes.sizeof(_abi.NormArgs), x_dtype=_abi.F16, x=4096, ldx=256, rows=4, cols=256,
+                eps=1e-6, convrot=256, round_rotated=1, q=8192, ldq=256, q_scale=16384)
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'x_dtype': _abi.F32}), 'x_dtype')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'q': None}), 'neither y nor q')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'cols': 272, 'ldx': 272, 'ldq': 272}),
+                    'multiple of 256')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'q_scale': None}), 'q_scale')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'mod_shift': 4096}), 'together')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'mod_shift': 4096, 'mod_scale': 8192,
+                                                            'ld_mod': 256, 'mod_rows': 3}), 'labels')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'mod_shift': 4096, 'mod_scale': 8192,
+                                                            'ld_mod': 250, 'mod_rows': 3, 'labels': 64}), 'ld_mod')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'weight': 4100}), 'weight')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'ldx': 200}), 'ldx')
+    # without quantization a 16-column multiple is enough
+    n = _abi.NormArgs(**{**base, 'q': None, 'q_scale': None, 'y': 8192, 'ldy': 272, 'cols': 272, 'ldx': 272,
+                         'rows': 0})
+    assert _abi.load().w8a8_norm_quantize(ctypes.byref(n)) == _abi.OK
 
 
 def test_empty_problems_return_ok_without_launch():

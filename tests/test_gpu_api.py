@@ -160,6 +160,42 @@ def test_dit_ffn_block_gated(gpu):
                   gate=gate.to(gpu), segments=[(0, 4, 0)])
 
 
+def test_dit_ffn_sublayer_with_fused_modulated_norm(gpu):
+    # x <- x + gate * FFN(modulated_norm(norm2, x, shift, scale)) (patches/tp_dit.py:347-362) with the
+    # norm fused into FC1's activation quantization.
+    from w8a8 import h3_tensor_flow as flow
+    data = workloads.dit_ffn(m=512, hidden=768, ffn=1024)
+    block = _ffn_module(data, gpu, 768, 1024)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn((512, 768), generator=g) * 3).half()
+    norm = torch.nn.RMSNorm(768, eps=1e-6 / 512 ** 2)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(768, generator=g) + 0.5)
+    shift = torch.randn((9, 768), generator=g) * 0.1
+    scale = torch.randn((9, 768), generator=g) * 0.1
+    gate = torch.randn((9, 768), generator=g)
+    segments = [(0, 100, 2), (100, 512, 7)]
+    labels = np.zeros(512, np.int64)
+    for a, b, row in segments:
+        labels[a:b] = row
+    out = block.forward_modulated(x.to(gpu), norm, shift.to(gpu), scale.to(gpu), gate.to(gpu), segments)
+    h = o.modulated_rms_norm(np_of(x), np_of(norm.weight.detach()), np_of(shift), np_of(scale), labels,
+                             eps=norm.eps)
+    want = o.ffn_block(h, np_of(block.fc1.weight), np_of(block.fc1.weight_scale).reshape(-1),
+                       np_of(block.fc2.weight), np_of(block.fc2.weight_scale).reshape(-1), np_of(x),
+                       gate=np_of(gate), labels=labels)
+    assert_bits_equal(np_of(out), want, 'ffn sublayer with fused norm')
+    # the standalone norm (both routes) returns the rows the fused kernel quantized
+    y = flow.modulated_norm(norm, x.to(gpu), shift.to(gpu), scale.to(gpu), segments, fused=True)
+    assert_bits_equal(np_of(y), h, 'modulated_norm')
+    codes, row_scale = flow.modulated_norm_quantize(norm, x.to(gpu), shift.to(gpu), scale.to(gpu), segments)
+    q, s = o.prepare_activation(h, convrot=True)
+    assert_bits_equal(np_of(codes), q, 'modulated_norm_quantize codes')
+    assert_bits_equal(np_of(row_scale).reshape(-1), s, 'modulated_norm_quantize scales')
+    with pytest.raises(ValueError):
+        flow.modulated_norm(norm, x.to(gpu), shift.to(gpu), scale.to(gpu), [(0, 100, 2)])
+
+
 def test_dit_ffn_block_full_size_sampled_rows(gpu):
     data = workloads.dit_ffn()
     block = _ffn_module(data, gpu, 3072, 8192)

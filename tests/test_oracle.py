@@ -334,3 +334,113 @@ def test_gated_residual_add_composition():
     # the branch is rounded to FP16 before the FMA (tilelang_dit_fusion.py:72-75)
     b = np.array([[1 + 2.0 ** -12]], np.float32)
     assert o.gated_residual_add(np.zeros((1, 1), np.float16), b, np.ones((1, 1), np.float32), [0])[0, 0] == 1.0
+
+
+# ------------------------------------------------------- modulated RMSNorm
+def test_rms_sum_squares_exact_on_integer_squares():
+    rng = np.random.default_rng(11)
+    x = rng.integers(-8, 9, (7, 3072)).astype(np.float32)   # every partial sum < 2^24: any order is exact
+    assert np.array_equal(o.rms_sum_squares(x), (x.astype(np.int64) ** 2).sum(1).astype(np.float32))
+    x = rng.integers(-8, 9, (3, 336 * 16)).astype(np.float32)  # 336 units: a partial last lane block
+    assert np.array_equal(o.rms_sum_squares(x), (x.astype(np.int64) ** 2).sum(1).astype(np.float32))
+
+
+def test_rms_sum_squares_lane_order_known_answer():
+    # Lane 0 owns units 0 and 64: its 16 unit-64 squares of 1 are absorbed one
+    # at a time by 2^24 (2^24 + 1 rounds to even); lanes 1..63 hold 16 each and
+    # meet lane 0 in the butterfly: 2^24 + 16 + 32 + 64 + 128 + 256 + 512.
+    x = np.zeros((1, 2048), np.float32)
+    x[0, 0] = 4096.0
+    x[0, 16:64 * 16] = 1.0
+    x[0, 64 * 16:65 * 16] = 1.0
+    assert o.rms_sum_squares(x)[0] == np.float32(2 ** 24 + 1008)
+    # A plain left-to-right sum would give 2^24, the exact sum 2^24 + 1024.
+
+
+def test_rms_sum_squares_butterfly_offsets_descend():
+    # Partials: lane 0 = 2^24, lane 32 = 3, the others 1. Offset 32 first:
+    # 2^24 + 3 is a tie and rounds to 2^24 + 4; then + 2 + 4 + 8 + 16 + 32.
+    x = np.zeros((1, 1024), np.float32)
+    x[0, 0] = 4096.0
+    for lane in range(1, 64):
+        x[0, 16 * lane] = 1.0
+    x[0, 16 * 32:16 * 32 + 3] = 1.0
+    assert o.rms_sum_squares(x)[0] == np.float32(2 ** 24 + 66)
+    # Ascending offsets would absorb lane 1's 1 first (2^24 + 1 -> 2^24).
+
+
+def test_rms_sum_squares_error_bound():
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((16, 5376)) * 3).astype(np.float16).astype(np.float32)
+    exact = (x.astype(np.float64) ** 2).sum(1)
+    n = 6 * 16 + 6   # terms per lane plus butterfly stages
+    assert np.all(np.abs(o.rms_sum_squares(x) - exact) <= n * 2.0 ** -24 * exact)
+
+
+def test_float32_sqrt_and_reciprocal_are_correctly_rounded():
+    # Rounding the float64 result once to fp32 is correctly rounded for sqrt
+    # and division (53 >= 2*24 + 2), so numpy's float32 ops must agree.
+    rng = np.random.default_rng(13)
+    d = np.exp(rng.uniform(-80, 80, 200000)).astype(np.float32)
+    r = np.sqrt(d)
+    assert np.array_equal(r, np.sqrt(d.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(np.float32(1.0) / r, (1.0 / r.astype(np.float64)).astype(np.float32))
+
+
+def test_modulated_norm_constant_rows_are_unit():
+    for cols in (1024, 4096):
+        x = np.zeros((4, cols), np.float16)
+        x[0], x[1], x[2], x[3] = 0.5, -2.0, 0.0625, 8.0
+        y = o.modulated_rms_norm(x, eps=0.0)
+        assert np.array_equal(y, np.sign(x.astype(np.float32)).astype(np.float16))
+
+
+def test_modulated_norm_scale_minus_one_selects_shift_row():
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((6, 512)).astype(np.float16)
+    w = rng.uniform(0.5, 2, 512).astype(np.float32)
+    shift = rng.standard_normal((5, 512)).astype(np.float32)
+    scale = np.full((5, 512), -1.0, np.float32)
+    labels = np.array([4, 0, 2, 2, 1, 3], np.int32)
+    y = o.modulated_rms_norm(x, w, shift, scale, labels, eps=1e-6)
+    assert np.array_equal(y, shift[labels].astype(np.float16))
+
+
+def test_modulated_norm_against_torch_rms_norm():
+    import torch
+    rng = np.random.default_rng(15)
+    x = (rng.standard_normal((9, 3072)) * 4).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 3072).astype(np.float32)
+    shift = (rng.standard_normal((3, 3072)) * 0.1).astype(np.float32)
+    scale = (rng.standard_normal((3, 3072)) * 0.1).astype(np.float32)
+    labels = np.array([0, 0, 1, 1, 1, 2, 2, 0, 1], np.int32)
+    eps = 1e-6 / 512 ** 2
+    y = o.modulated_rms_norm(x, w, shift, scale, labels, eps=eps)
+    h = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (3072,), torch.from_numpy(w).double(), eps)
+    h = h * (1 + torch.from_numpy(scale[labels]).double()) + torch.from_numpy(shift[labels]).double()
+    ref = h.numpy()
+    # fp16 output rounding (2^-11 relative) plus a few fp32 roundings.
+    assert np.all(np.abs(y.astype(np.float64) - ref) <= 2.0 ** -11 * np.abs(ref) + 1e-6)
+    yb = o.from_bf16_bits(o.modulated_rms_norm(o.to_bf16_bits(x.astype(np.float32)), w, shift, scale, labels,
+                                               eps=eps, x_dtype='bf16'))
+    xb = o.from_bf16_bits(o.to_bf16_bits(x.astype(np.float32))).astype(np.float64)
+    hb = torch.nn.functional.rms_norm(torch.from_numpy(xb), (3072,), torch.from_numpy(w).double(), eps)
+    refb = (hb * (1 + torch.from_numpy(scale[labels]).double()) + torch.from_numpy(shift[labels]).double()).numpy()
+    assert np.all(np.abs(yb - refb) <= 2.0 ** -8 * np.abs(refb) + 1e-6)
+
+
+def test_norm_quantize_composition():
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal((5, 512)).astype(np.float16)
+    shift = np.zeros((2, 512), np.float32)
+    scale = np.full((2, 512), -1.0, np.float32)
+    shift[1, :] = 0.25
+    labels = np.array([0, 1, 1, 0, 1], np.int32)
+    q, s, y = o.norm_quantize(x, None, shift, scale, labels, eps=1e-6, convrot=False)
+    # rows on label 0 are all zero (scale floor, codes 0); label 1 rows are constant 0.25 -> 127
+    assert np.array_equal(s[labels == 0], np.full(2, o.SCALE_FLOOR))
+    assert np.all(q[labels == 0] == 0) and np.all(q[labels == 1] == 127)
+    q2, s2, y2 = o.norm_quantize(x, None, shift, scale, labels, eps=1e-6, convrot=True)
+    # the rotated constant rows quantize like the rotation of a constant 0.25 row
+    r = o.convrot256(np.full((1, 512), 0.25, np.float32))
+    assert np.array_equal(q2[1], o.quantize_rows(r)[0][0])
