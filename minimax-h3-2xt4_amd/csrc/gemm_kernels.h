@@ -11,6 +11,7 @@
 #pragma once
 
 #include <atomic>
+#include <type_traits>
 
 #include "gemm_launch.h"
 #include "w8a8_device.h"
@@ -196,6 +197,16 @@ __device__ __forceinline__ void wait_vmcnt() {
 // s_waitcnt vmcnt(0) lgkmcnt(0): every vector-memory access of this wave
 // (LDS DMA included) completed and every LDS access returned.
 __device__ __forceinline__ void wait_vm_lgkm() { __builtin_amdgcn_s_waitcnt(0x7 << 4); }
+
+// s_waitcnt vmcnt(N) lgkmcnt(0).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// s_waitcnt lgkmcnt(0) alone.
+__device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
 
 // Compile-time epilogue options of the persistent kernel (each variant
 // carries only the loads it uses).
@@ -490,10 +501,9 @@ __device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw,
 // rows x one chunk per 16-lane group) free of bank conflicts. A DMA lane
 // therefore loads the logical chunk that lands on its physical slot.
 constexpr int kSK = 128;                    // K bytes per stage
-constexpr int kSTile = 256 * kSK;           // one operand tile per stage (32 KB)
-constexpr int kSStage = 2 * kSTile;         // 64 KB
-constexpr int kStagingOff = 2 * kSStage;    // the ring ends here
-constexpr int kPersistentLds = kStagingOff + 4 * 8192;
+constexpr int kSTile = 256 * kSK;           // one operand tile of one stage (32 KB): a ring slot
+constexpr int kSlots = 5;                   // ring of half stages
+constexpr int kPersistentLds = kSlots * kSTile;
 
 __device__ __forceinline__ void dma16(const int8_t* g, int8_t* l) {
   __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
@@ -538,7 +548,6 @@ void gemm_i8_persistent(GemmParams p) {
   const int kstages = p.k / kSK;
   auto ks_begin = [&](int item) { return (item % ksplit) * kstages / ksplit; };
   auto ks_end = [&](int item) { return (item % ksplit + 1) * kstages / ksplit; };
-  constexpr bool late_dma = (FLAGS & kWithResidual) != 0;
 
   // DMA cursor: the (tile, stage) of the next stage to issue. Wave w fills
   // rows 64 w .. 64 w + 63 of both operand tiles, 8 rows per instruction;
@@ -557,24 +566,36 @@ void gemm_i8_persistent(GemmParams p) {
   };
   int dma_i = 0, dma_ks = ks_begin(item_of(0));
   point(0);
-  // Issue one stage (16 DMA instructions per wave) into ring buffer buf and
-  // advance the cursor; past the last stage of the last tile it stays put
-  // and re-reads that stage into a buffer that is never consumed.
-  auto issue = [&](int buf) {
-    int8_t* st = smem + buf * kSStage + wave * 8 * 1024;
+  // The ring: unit h (the A tile of global stage h / 2 for even h, its B
+  // tile for odd h) goes to slot h % kSlots. A unit is 8 DMA instructions
+  // per wave, issued in halves of 4 spread between MFMAs (a burst of them
+  // would stall the issuing wave behind the address unit). The cursor
+  // advances after a B tile's second half; past the last stage of the last
+  // tile it stays put and re-reads that stage into slots never consumed.
+  auto issue_half = [&](auto b_tag, auto h_tag, int slot) {
+    constexpr bool B = decltype(b_tag)::value;
+    constexpr int H = decltype(h_tag)::value;
+    int8_t* st = smem + slot * kSTile + wave * 8 * 1024;
     const uint32_t kof = (uint32_t)(dma_ks * kSK);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dma16(p.a + (off_a[j] + kof), st + j * 1024);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dma16(p.b + (off_b[j] + kof), st + kSTile + j * 1024);
-    if (dma_ks + 1 < ks_end(item_of(dma_i))) {
-      ++dma_ks;
-    } else if (dma_i + 1 < ntiles) {
-      ++dma_i;
-      dma_ks = ks_begin(item_of(dma_i));
-      point(dma_i);
+    for (int j = 4 * H; j < 4 * H + 4; ++j) {
+      if constexpr (B) dma16(p.b + (off_b[j] + kof), st + j * 1024);
+      else dma16(p.a + (off_a[j] + kof), st + j * 1024);
+    }
+    if constexpr (B && H == 1) {
+      if (dma_ks + 1 < ks_end(item_of(dma_i))) {
+        ++dma_ks;
+      } else if (dma_i + 1 < ntiles) {
+        ++dma_i;
+        dma_ks = ks_begin(item_of(dma_i));
+        point(dma_i);
+      }
     }
   };
+  using A_ = std::false_type;
+  using B_ = std::true_type;
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
 
   // v_mfma_i32_32x32x32_i8: for sub-step u (K bytes [32 u, 32 u + 32) of the
   // stage), lane (r = lane % 32, h = lane / 32) supplies row r, logical
@@ -583,9 +604,9 @@ void gemm_i8_persistent(GemmParams p) {
   const int wm = wave >> 1, wn = wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
   const int a_row = wm * 128 * kSK + fr * kSK, b_row = wn * 128 * kSK + fr * kSK;
-  auto read_frags = [&](int buf, int u, v4i (&fa)[4], v4i (&fb)[4]) {
-    const int8_t* sa = smem + buf * kSStage;
-    const int8_t* sb = sa + kSTile;
+  auto read_frags = [&](int slot_a, int slot_b, int u, v4i (&fa)[4], v4i (&fb)[4]) {
+    const int8_t* sa = smem + slot_a * kSTile;
+    const int8_t* sb = smem + slot_b * kSTile;
     const int off = lds_chunk(fr, 2 * u + fh) << 4;   // rows 32 i + fr share (row >> 1) & 7
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -623,21 +644,49 @@ void gemm_i8_persistent(GemmParams p) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
   };
+  // The same with 4 DMA instructions between them.
+  auto interleave_dma = [&]() {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  };
+  auto interleave12_dma = [&]() {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+  };
 
-  issue(0);
-  issue(1);
-  wait_vmcnt<16>();  // stage 0 landed (stage 1 in flight)
+  // Stage g computes from units 2g, 2g + 1 (slots c, c + 1 with
+  // c = 2g mod 5). During it the second half of unit 2g + 3 and unit 2g + 4
+  // are issued (slots c + 3, c + 4, freed by stage g - 1); its end releases
+  // slots c, c + 1, and the first half of unit 2g + 5 goes to slot c.
+  issue_half(A_{}, H0{}, 0);
+  issue_half(A_{}, H1{}, 0);
+  issue_half(B_{}, H0{}, 1);
+  issue_half(B_{}, H1{}, 1);
+  issue_half(A_{}, H0{}, 2);
+  issue_half(A_{}, H1{}, 2);
+  issue_half(B_{}, H0{}, 3);
+  wait_vmcnt<12>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
   block_barrier();
   v4i fa0[4], fb0[4], fa1[4], fb1[4];
-  read_frags(0, 0, fa0, fb0);
-  int cur = 0;
+  read_frags(0, 1, 0, fa0, fb0);
+  auto next_slot = [](int slot) { return slot == kSlots - 1 ? 0 : slot + 1; };
+  int cur_a = 0;   // slot of the current stage's A tile; its B tile is the next slot
   for (int i = 0; i < ntiles; ++i) {
     const int item = item_of(i);
     int tm, tn;
     raster(item / ksplit, tiles_m, tiles_n, tm, tn);
     const int mw = tm * kBM + wm * 128, nw = tn * kBN + wn * 128;
-    // Row scales in the MFMA layout and the column scales of the staged
-    // read-out, fetched before the K loop so the epilogue never waits on them.
+    // Row scales in the MFMA layout, the column scales (and biases) of the
+    // staged read-out and the gate labels, fetched before the K loop so the
+    // epilogue never waits on them.
     float as[4], wsc[2][8];
     uint32_t braw[2][8];
     int lbl[4] = {0, 0, 0, 0};
@@ -651,39 +700,46 @@ void gemm_i8_persistent(GemmParams p) {
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
-    const int nks = ks_end(item) - ks_begin(item);
+    const int nks = ks_end(item) - ks_begin(item);   // >= 1
+    // One stage: 64 MFMAs, 32 fragment reads and 16 DMA instructions.
+    int stg = 0;   // the last stage's B slot: the epilogue's staging area
     int ks = 0;
     do {  // nks >= 1
-      const int nxt = cur ^ 1;
+      const int cur_b = next_slot(cur_a);
+      const int nxt_a = next_slot(cur_b), nxt_b = next_slot(nxt_a), fill = next_slot(nxt_b);
       mfma16(fa0, fb0);
-      read_frags(cur, 1, fa1, fb1);
-      interleave();
+      read_frags(cur_a, cur_b, 1, fa1, fb1);
+      issue_half(B_{}, H1{}, nxt_b);
+      interleave_dma();
       mfma16(fa1, fb1);
-      read_frags(cur, 2, fa0, fb0);
-      interleave();
+      read_frags(cur_a, cur_b, 2, fa0, fb0);
+      issue_half(A_{}, H0{}, fill);
+      interleave_dma();
       mfma16(fa0, fb0);
-      read_frags(cur, 3, fa1, fb1);
-      interleave();
+      read_frags(cur_a, cur_b, 3, fa1, fb1);
+      issue_half(A_{}, H1{}, fill);
+      interleave_dma();
       // The first MFMAs of the last sub-step consume its fragments, so past
-      // them this wave is done reading the stage's buffer.
+      // them this wave is done reading the stage's slots.
       mfma_row(0, fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
-      wait_vm_lgkm();    // the next stage landed and this wave's reads of this one returned
-      block_barrier();   // ... for every wave: the buffer is released
-      // Stage + 2 streams in for a whole stage time. With a residual the
-      // last stage's issue waits until after the epilogue: the residual
-      // loads there would otherwise queue behind it (loads return in order).
-      if (!(late_dma && ks + 1 == nks)) issue(cur);
+      // The next stage (units 2g + 2, 2g + 3) landed - only unit 2g + 4,
+      // issued after them, may still be in flight - and this wave's reads of
+      // this stage returned;
+      wait_vm_lgkm<8>();
+      block_barrier();   // ... for every wave: both slots are released.
+      issue_half(B_{}, H0{}, cur_a);
 #pragma unroll
       for (int nb = 1; nb < 4; ++nb) mfma_row(nb, fa1, fb1);
-      read_frags(nxt, 0, fa0, fb0);
-      interleave12();
-      cur = nxt;
+      read_frags(nxt_a, nxt_b, 0, fa0, fb0);
+      interleave12_dma();
+      stg = cur_b;
+      cur_a = nxt_a;
     } while (++ks < nks);
-    // Everything but the stage just issued (its 16 loads are the youngest)
-    // has landed, the scale and bias loads of this tile included.
-    if constexpr (late_dma) wait_vmcnt<0>();
-    else wait_vmcnt<16>();
+    // The tile's scale and bias loads have landed: at most unit 2g + 4 and
+    // the first half of unit 2g + 5 are younger and in flight. (The
+    // epilogue's residual loads queue behind those 12 instructions.)
+    wait_vmcnt<12>();
     float bsc[2][8];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -693,8 +749,11 @@ void gemm_i8_persistent(GemmParams p) {
                     : p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
                                            : __builtin_bit_cast(float, braw[h][j]);
     store_quadrant32_passes<EPI, OUT, FLAGS>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,
-                                             smem + kStagingOff + wave * 8192, (item % ksplit) * p.split_stride);
-    if constexpr (late_dma) issue(cur ^ 1);
+                                             smem + stg * kSTile + wave * 8192, (item % ksplit) * p.split_stride);
+    // The staging slot's next unit (2g + 6) is issued during the next
+    // stage; a wave's DMA into a slot writes the same 8 KB it used for
+    // staging, so its own staging reads returning is all that unit waits for.
+    wait_lgkm();
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }
