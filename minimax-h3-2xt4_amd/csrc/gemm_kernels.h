@@ -572,25 +572,32 @@ void gemm_i8_persistent(GemmParams p) {
   // would stall the issuing wave behind the address unit). The cursor
   // advances after a B tile's second half; past the last stage of the last
   // tile it stays put and re-reads that stage into slots never consumed.
-  auto issue_half = [&](auto b_tag, auto h_tag, int slot) {
+  auto advance = [&]() {
+    if (dma_ks + 1 < ks_end(item_of(dma_i))) {
+      ++dma_ks;
+    } else if (dma_i + 1 < ntiles) {
+      ++dma_i;
+      dma_ks = ks_begin(item_of(dma_i));
+      point(dma_i);
+    }
+  };
+  // DMA instruction J (0..7) of this wave's part of the cursor stage's A or
+  // B tile into slot.
+  auto dma_one = [&](auto b_tag, auto j_tag, int slot) {
     constexpr bool B = decltype(b_tag)::value;
-    constexpr int H = decltype(h_tag)::value;
-    int8_t* st = smem + slot * kSTile + wave * 8 * 1024;
+    constexpr int J = decltype(j_tag)::value;
+    int8_t* st = smem + slot * kSTile + wave * 8 * 1024 + J * 1024;
     const uint32_t kof = (uint32_t)(dma_ks * kSK);
-#pragma unroll
-    for (int j = 4 * H; j < 4 * H + 4; ++j) {
-      if constexpr (B) dma16(p.b + (off_b[j] + kof), st + j * 1024);
-      else dma16(p.a + (off_a[j] + kof), st + j * 1024);
-    }
-    if constexpr (B && H == 1) {
-      if (dma_ks + 1 < ks_end(item_of(dma_i))) {
-        ++dma_ks;
-      } else if (dma_i + 1 < ntiles) {
-        ++dma_i;
-        dma_ks = ks_begin(item_of(dma_i));
-        point(dma_i);
-      }
-    }
+    if constexpr (B) dma16(p.b + (off_b[J] + kof), st);
+    else dma16(p.a + (off_a[J] + kof), st);
+    if constexpr (B && J == 7) advance();
+  };
+  auto issue_half = [&](auto b_tag, auto h_tag, int slot) {
+    constexpr int H = decltype(h_tag)::value;
+    dma_one(b_tag, std::integral_constant<int, 4 * H>{}, slot);
+    dma_one(b_tag, std::integral_constant<int, 4 * H + 1>{}, slot);
+    dma_one(b_tag, std::integral_constant<int, 4 * H + 2>{}, slot);
+    dma_one(b_tag, std::integral_constant<int, 4 * H + 3>{}, slot);
   };
   using A_ = std::false_type;
   using B_ = std::true_type;
@@ -612,6 +619,24 @@ void gemm_i8_persistent(GemmParams p) {
     for (int i = 0; i < 4; ++i) {
       fa[i] = *reinterpret_cast<const v4i*>(sb + b_row + i * 32 * kSK + off);
       fb[i] = *reinterpret_cast<const v4i*>(sa + a_row + i * 32 * kSK + off);
+    }
+  };
+  // Group k (0..2) of the fragment reads of sub-step u, in the order the
+  // next sub-step's first MFMA row consumes them (all four A fragments fb,
+  // then the B fragments fa): k = 0 reads fb[0..2], k = 1 fb[3], fa[0..1],
+  // k = 2 fa[2..3]. The last MFMA row of a sub-step issues no reads, so the
+  // reads have landed when the next sub-step starts.
+  auto read_group = [&](int slot_a, int slot_b, int u, int k, v4i (&fa)[4], v4i (&fb)[4]) {
+    const int off = lds_chunk(fr, 2 * u + fh) << 4;
+    const int8_t* sa = smem + slot_a * kSTile + a_row + off;
+    const int8_t* sb = smem + slot_b * kSTile + b_row + off;
+    auto rd = [](const int8_t* base, int i) { return *reinterpret_cast<const v4i*>(base + i * 32 * kSK); };
+    if (k == 0) {
+      fb[0] = rd(sa, 0); fb[1] = rd(sa, 1); fb[2] = rd(sa, 2);
+    } else if (k == 1) {
+      fb[3] = rd(sa, 3); fa[0] = rd(sb, 0); fa[1] = rd(sb, 1);
+    } else {
+      fa[2] = rd(sb, 2); fa[3] = rd(sb, 3);
     }
   };
   v16i acc[4][4];
@@ -704,23 +729,39 @@ void gemm_i8_persistent(GemmParams p) {
     // One stage: 64 MFMAs, 32 fragment reads and 16 DMA instructions.
     int stg = 0;   // the last stage's B slot: the epilogue's staging area
     int ks = 0;
+    // A sub-step in fixed order: each MFMA row of the current fragments is
+    // followed by one fragment pair of the next sub-step and one DMA
+    // instruction (sched_barrier keeps the compiler from regrouping them).
+    auto substep = [&](const v4i (&ca)[4], const v4i (&cb)[4], int ra, int rb, int u, v4i (&na)[4],
+                       v4i (&nb)[4], auto b_tag, auto h_tag, int dslot) {
+      constexpr int H = decltype(h_tag)::value;
+      mfma_row(0, ca, cb);
+      __builtin_amdgcn_sched_barrier(0);
+      read_group(ra, rb, u, 0, na, nb);
+      dma_one(b_tag, std::integral_constant<int, 4 * H>{}, dslot);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_row(1, ca, cb);
+      __builtin_amdgcn_sched_barrier(0);
+      read_group(ra, rb, u, 1, na, nb);
+      dma_one(b_tag, std::integral_constant<int, 4 * H + 1>{}, dslot);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_row(2, ca, cb);
+      __builtin_amdgcn_sched_barrier(0);
+      read_group(ra, rb, u, 2, na, nb);
+      dma_one(b_tag, std::integral_constant<int, 4 * H + 2>{}, dslot);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_row(3, ca, cb);
+      dma_one(b_tag, std::integral_constant<int, 4 * H + 3>{}, dslot);
+      __builtin_amdgcn_sched_barrier(0);
+    };
     do {  // nks >= 1
       const int cur_b = next_slot(cur_a);
       const int nxt_a = next_slot(cur_b), nxt_b = next_slot(nxt_a), fill = next_slot(nxt_b);
-      mfma16(fa0, fb0);
-      read_frags(cur_a, cur_b, 1, fa1, fb1);
-      issue_half(B_{}, H1{}, nxt_b);
-      interleave_dma();
-      mfma16(fa1, fb1);
-      read_frags(cur_a, cur_b, 2, fa0, fb0);
-      issue_half(A_{}, H0{}, fill);
-      interleave_dma();
-      mfma16(fa0, fb0);
-      read_frags(cur_a, cur_b, 3, fa1, fb1);
-      issue_half(A_{}, H1{}, fill);
-      interleave_dma();
-      // The first MFMAs of the last sub-step consume its fragments, so past
-      // them this wave is done reading the stage's slots.
+      substep(fa0, fb0, cur_a, cur_b, 1, fa1, fb1, B_{}, H1{}, nxt_b);
+      substep(fa1, fb1, cur_a, cur_b, 2, fa0, fb0, A_{}, H0{}, fill);
+      substep(fa0, fb0, cur_a, cur_b, 3, fa1, fb1, A_{}, H1{}, fill);
+      // The first MFMA row of the last sub-step consumes its fragments, so
+      // past it this wave is done reading the stage's slots.
       mfma_row(0, fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
       // The next stage (units 2g + 2, 2g + 3) landed - only unit 2g + 4,
@@ -728,11 +769,20 @@ void gemm_i8_persistent(GemmParams p) {
       // this stage returned;
       wait_vm_lgkm<8>();
       block_barrier();   // ... for every wave: both slots are released.
-      issue_half(B_{}, H0{}, cur_a);
-#pragma unroll
-      for (int nb = 1; nb < 4; ++nb) mfma_row(nb, fa1, fb1);
-      read_frags(nxt_a, nxt_b, 0, fa0, fb0);
-      interleave12_dma();
+      read_group(nxt_a, nxt_b, 0, 0, fa0, fb0);
+      dma_one(B_{}, std::integral_constant<int, 0>{}, cur_a);
+      mfma_row(1, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+      read_group(nxt_a, nxt_b, 0, 1, fa0, fb0);
+      dma_one(B_{}, std::integral_constant<int, 1>{}, cur_a);
+      mfma_row(2, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+      read_group(nxt_a, nxt_b, 0, 2, fa0, fb0);
+      dma_one(B_{}, std::integral_constant<int, 2>{}, cur_a);
+      mfma_row(3, fa1, fb1);
+      __builtin_amdgcn_sched_barrier(0);
+      dma_one(B_{}, std::integral_constant<int, 3>{}, cur_a);
+      __builtin_amdgcn_sched_barrier(0);
       stg = cur_b;
       cur_a = nxt_a;
     } while (++ks < nks);
