@@ -247,7 +247,7 @@ __device__ __forceinline__ int readout_col(int nw, int h, int lane) {
 // so the passes need only compiler ordering between the slice writes and
 // reads, and the next pass's writes may issue before this pass's reads
 // return.
-template <int EPI, int OUT, int FLAGS>
+template <int EPI, int OUT, int FLAGS, bool INTERIOR>
 __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[4][4],
                                                         const float (&wsc)[2][8], const float (&bsc)[2][8],
                                                         const float (&as)[4], const int (&lbl)[4], int mw, int nw,
@@ -264,14 +264,16 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     const int mb = pass >> 1, h = pass & 1;
     const int mrow = mw + mb * 32;
     const int ncol = nw + 64 * h + ocol;
-    const bool full_cols = p.vec16 && ncol + R::CPL <= p.n;
+    // INTERIOR: every row and column of the quadrant is inside the output
+    // and rows are 16-byte aligned, so no store needs a mask.
+    const bool full_cols = INTERIOR || (p.vec16 && ncol + R::CPL <= p.n);
     uint4 rres[R::ITERS];
     if constexpr (has_res) {
 #pragma unroll
       for (int it = 0; it < R::ITERS; ++it) {
         const int m = mrow + it * R::RPI + orow;
         const uint16_t* r = p.residual + (int64_t)m * p.ldr + ncol;
-        if (m < p.m && full_cols) {
+        if (INTERIOR || (m < p.m && full_cols)) {
           rres[it] = *reinterpret_cast<const uint4*>(r);
         } else {
           uint32_t w[4] = {0, 0, 0, 0};
@@ -307,6 +309,11 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
             v4i{acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2], acc[nb][mb][4 * g + 3]};
       }
     asm volatile("" ::: "memory");
+    // Row scales of the lane's read-out rows (from the lanes holding them in
+    // the MFMA layout), issued with the slice reads so one wait covers both.
+    float arow[R::ITERS];
+#pragma unroll
+    for (int it = 0; it < R::ITERS; ++it) arow[it] = EPI != kEpiInt32 ? __shfl(as[mb], it * R::RPI + orow, 64) : 0.0f;
     int c[R::ITERS][R::CPL];
 #pragma unroll
     for (int it = 0; it < R::ITERS; ++it) {
@@ -323,7 +330,7 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     for (int it = 0; it < R::ITERS; ++it) {
       const int row = it * R::RPI + orow;
       const int m = mrow + row;
-      const float a = EPI != kEpiInt32 ? __shfl(as[mb], row, 64) : 0.0f;
+      const float a = arow[it];
       uint32_t bits[R::CPL];
 #pragma unroll
       for (int j = 0; j < R::CPL; ++j)
@@ -339,13 +346,13 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
         }
       }
       char* o = reinterpret_cast<char*>(p.out) + (out_off + (int64_t)m * p.ldc + ncol) * R::ES;
-      if (m < p.m && full_cols) {
+      if (INTERIOR || (m < p.m && full_cols)) {
         if constexpr (R::ES == 2)
           *reinterpret_cast<uint4*>(o) = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
                                                     bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16));
         else
           *reinterpret_cast<uint4*>(o) = make_uint4(bits[0], bits[1], bits[2], bits[3]);
-      } else if (m < p.m) {
+      } else if (!INTERIOR && m < p.m) {
 #pragma unroll
         for (int j = 0; j < R::CPL; ++j) {
           if (ncol + j < p.n) {
@@ -798,8 +805,15 @@ void gemm_i8_persistent(GemmParams p) {
         bsc[h][j] = (FLAGS & kWithBias) == 0       ? 0.0f
                     : p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
                                            : __builtin_bit_cast(float, braw[h][j]);
-    store_quadrant32_passes<EPI, OUT, FLAGS>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,
-                                             smem + stg * kSTile + wave * 8192, (item % ksplit) * p.split_stride);
+    int8_t* const stage_w = smem + stg * kSTile + wave * 8192;
+    const int64_t out_off = (item % ksplit) * p.split_stride;
+    // Interior quadrants take a copy without store masks (not for the gate
+    // variants, whose registers a second copy would push into spills).
+    if ((FLAGS & kWithGate) == 0 && p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
+      store_quadrant32_passes<EPI, OUT, FLAGS, (FLAGS & kWithGate) == 0>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,
+                                                                        stage_w, out_off);
+    else
+      store_quadrant32_passes<EPI, OUT, FLAGS, false>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
     // The staging slot's next unit (2g + 6) is issued during the next
     // stage; a wave's DMA into a slot writes the same 8 KB it used for
     // staging, so its own staging reads returning is all that unit waits for.
