@@ -466,7 +466,9 @@ def run_dit_norm(args, torch, dev):
                unit='us', higher_is_better=False, dtype='f32', data='synthetic',
                config=dict(workload='dit_norm', m=m, k=k, mod_rows=shift.shape[0], segments=len(data['segments'])),
                roofline=dict(bound='hbm', achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit='GB/s',
-                             frac=round(gbs / PEAK_HBM_GBS, 4), traffic=None),
+                             frac=round(gbs / PEAK_HBM_GBS, 4), traffic=traffic_from_profiles('norm_quant'),
+                             kernel='norm_quant_kernel<1,3,3,3> (modulated RMSNorm + ConvRot256 + INT8, 16384x3072)',
+                             algorithmic=f'{nbytes:.4g} B per launch (x fp16 read, int8 codes + fp32 scales written)'),
                unfused_us=round(tu * 1e3, 2), fusion_speedup=round(tu / tf, 3))
     if not args.no_cpu_baseline:
         import oracle as o
