@@ -481,7 +481,42 @@ def run_dit_norm(args, torch, dev):
     return res
 
 
-WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_norm': run_dit_norm, 'copy': run_copy, 'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv,
+def run_dit_rms_rope(args, torch, dev):
+    """Per-head FP32 RMS norm + split-half RoPE of the DiT QKV output
+    (53504 tokens, 24 heads of 128, rotary prefix 96, fp16 in/out)."""
+    from w8a8 import kernels, workloads
+    data = workloads.dit_rms_rope()
+    m = data['packed'].shape[0]
+    heads, rot = data['heads'], data['rot_dim']
+    packed, freqs, gq, gk = (data[n].to(dev) for n in ('packed', 'freqs', 'q_gain', 'k_gain'))
+
+    def step():
+        return kernels.rms_rope(packed, freqs, gq, gk, heads=heads, rot_dim=rot, eps=1e-6)
+
+    t = timed(torch, step, args.steps, args.warmup)
+    width = heads * 128
+    nbytes = m * (2 * width * 2 + 2 * width * 2 + rot // 2 * 4 * 2)   # Q,K read + Q,K written + freqs
+    gbs = nbytes / (t * 1e-3) / 1e9
+    res = dict(metric='DiT packed-QKV RMS-RoPE 53504x24x128 us', value=round(t * 1e3, 2), unit='us',
+               higher_is_better=False, dtype='f32', data='synthetic',
+               config=dict(workload='dit_rms_rope', m=m, heads=heads, dim=128, rot_dim=rot),
+               roofline=dict(bound='hbm', achieved=round(gbs, 1), peak=PEAK_HBM_GBS, unit='GB/s',
+                             frac=round(gbs / PEAK_HBM_GBS, 4), traffic=traffic_from_profiles('rms_rope'),
+                             kernel='rms_rope_kernel<1,1,1> (53504 rows x 24 heads)',
+                             algorithmic=f'{nbytes:.4g} B per launch (Q,K fp16 read and written, fp16 freqs)'))
+    if not args.no_cpu_baseline:
+        import oracle as o
+        rows = min(args.cpu_rows // 4, m)      # the oracle's exact fma emulation is slow
+        p_np = data['packed'][:rows].numpy()
+        f_np = data['freqs'][:rows].float().numpy()
+        gq_np, gk_np = data['q_gain'].numpy(), data['k_gain'].numpy()
+        tc = _cpu_rows_timing(lambda: o.rms_rope(p_np, f_np, gq_np, gk_np, heads, rot, eps=1e-6)) * m / rows
+        res['cpu_baseline'] = dict(value=round(tc * 1e6, 1), unit='us', cores=1, kind='port',
+                                   sample=f'oracle rms_rope (numpy) on {rows} of {m} rows, scaled x{m / rows:g}')
+    return res
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy, 'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
 
 

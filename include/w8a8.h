@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 4
+#define W8A8_ABI_VERSION 5
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -181,6 +181,51 @@ typedef struct W8A8NormArgs {
 int w8a8_norm_quantize(const W8A8NormArgs* args);
 
 /*
+ * Per-head RMS normalization with FP32 statistics and gains, then split-half
+ * RoPE, of the Q and K parts of a packed QKV projection output.
+ * Replaces: patches/tilelang_fp32_rms_rope.py:6-66 (kernel, execute) and the
+ *           Kitchen rms_rope_split_half call of patches/tp_dit.py:296-309.
+ * packed: [rows, >= 2*heads*dim] of in_dtype (F16 or F32), row stride ldp;
+ *   Q heads in columns [0, heads*dim), K heads in [heads*dim, 2*heads*dim).
+ * freqs: [rows, rot_dim/2, 2, 2] of freq_dtype (F16 or F32), contiguous: for
+ *   pair p the 2x2 matrix F applied to (x[p], x[p + rot_dim/2]).
+ * q_gain, k_gain: [dim] fp32.
+ * Per head vector x (dim = 128), in fp32 (round to nearest even):
+ *   ss  = sum of x*x in a fixed order: the vector is 16 slices of 8 elements;
+ *         slice i adds its squares in order, then the 16 partials meet in an
+ *         xor butterfly (offsets 8, 4, 2, 1)
+ *   inv = 1 / sqrt(ss * fp32(1/dim) + eps)           (IEEE sqrt and division)
+ *   n   = (x * inv) * gain
+ *   d < rot_dim: out = fma(n[partner], F[p][s][1-s], n[d] * F[p][s][s]) with
+ *         p = d mod rot_dim/2, s = d div rot_dim/2, partner = the other half
+ *   d >= rot_dim: out = n[d]
+ * q_out, k_out: [rows, heads, dim] of out_dtype (F16 or F32), contiguous.
+ * Requirements: dim == 128, rot_dim even with 0 < rot_dim <= 128; packed,
+ *   freqs, gains and outputs 16-byte aligned, ldp * elem a multiple of 16.
+ */
+typedef struct W8A8RmsRopeArgs {
+  uint32_t struct_size;
+  int32_t in_dtype;
+  const void* packed;
+  int64_t ldp;
+  int64_t rows;
+  int32_t heads;
+  int32_t dim;
+  int32_t rot_dim;
+  int32_t freq_dtype;
+  const void* freqs;
+  const float* q_gain;
+  const float* k_gain;
+  float eps;
+  int32_t out_dtype;
+  void* q_out;
+  void* k_out;
+  void* stream;
+} W8A8RmsRopeArgs;
+
+int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
+
+/*
  * INT8 GEMM on gfx950 i8 MFMA with a fused epilogue.
  * Replaces: patches/parallel_int8.py:46-50 (int_mm),
  *           patches/optimized_tp.py:34-43 (native_int_mm),
@@ -289,7 +334,7 @@ int w8a8_dequantize(const W8A8DequantArgs* args);
 int w8a8_abi_version(void);
 
 /* sizeof of each argument struct, by index: 0 Quant, 1 Swiglu, 2 Gemm,
- * 3 Dequant, 4 Norm; -1 for an unknown index. Lets bindings verify their layout. */
+ * 3 Dequant, 4 Norm, 5 RmsRope; -1 for an unknown index. Lets bindings verify their layout. */
 int64_t w8a8_struct_size(int32_t which);
 
 /* Message describing the last error returned on the calling thread. */

@@ -22,6 +22,7 @@ static_assert(sizeof(W8A8SwigluArgs) == 96, "W8A8SwigluArgs layout");
 static_assert(sizeof(W8A8GemmArgs) == 184, "W8A8GemmArgs layout");
 static_assert(sizeof(W8A8DequantArgs) == 144, "W8A8DequantArgs layout");
 static_assert(sizeof(W8A8NormArgs) == 144, "W8A8NormArgs layout");
+static_assert(sizeof(W8A8RmsRopeArgs) == 104, "W8A8RmsRopeArgs layout");
 
 extern "C" int w8a8_abi_version(void) { return W8A8_ABI_VERSION; }
 
@@ -32,6 +33,7 @@ extern "C" int64_t w8a8_struct_size(int32_t which) {
     case 2: return (int64_t)sizeof(W8A8GemmArgs);
     case 3: return (int64_t)sizeof(W8A8DequantArgs);
     case 4: return (int64_t)sizeof(W8A8NormArgs);
+    case 5: return (int64_t)sizeof(W8A8RmsRopeArgs);
     default: return -1;
   }
 }

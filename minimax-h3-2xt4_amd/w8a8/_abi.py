@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -60,10 +60,17 @@ class NormArgs(ctypes.Structure):
                 ('round_rotated', _c.c_int32), ('q', _p), ('ldq', _c.c_int64), ('q_scale', _p), ('stream', _p)]
 
 
+class RmsRopeArgs(ctypes.Structure):
+    _fields_ = [('struct_size', _c.c_uint32), ('in_dtype', _c.c_int32), ('packed', _p), ('ldp', _c.c_int64),
+                ('rows', _c.c_int64), ('heads', _c.c_int32), ('dim', _c.c_int32), ('rot_dim', _c.c_int32),
+                ('freq_dtype', _c.c_int32), ('freqs', _p), ('q_gain', _p), ('k_gain', _p), ('eps', _c.c_float),
+                ('out_dtype', _c.c_int32), ('q_out', _p), ('k_out', _p), ('stream', _p)]
+
+
 # Argument structs in w8a8_struct_size() index order, with their entry points.
-STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs, NormArgs)
+STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs, NormArgs, RmsRopeArgs)
 STRUCT_ENTRY_POINTS = ('w8a8_quantize_rows', 'w8a8_swiglu_quantize', 'w8a8_gemm', 'w8a8_dequantize',
-                       'w8a8_norm_quantize')
+                       'w8a8_norm_quantize', 'w8a8_rms_rope')
 ENTRY_POINTS = STRUCT_ENTRY_POINTS + ('w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error',
                                       'w8a8_gemm_workspace_size')
 

@@ -146,6 +146,49 @@ def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, *, eps, q
     return out
 
 
+def rms_rope(packed, freqs, q_gain, k_gain, *, heads, rot_dim, eps, dim=128, out_dtype=torch.float16):
+    """Per-head FP32 RMS norm + split-half RoPE of packed Q and K.
+
+    packed: [rows, >= 2*heads*dim] fp16/fp32 (Q heads, then K heads; V may
+    follow); freqs: [rows, rot_dim/2, 2, 2] fp16/fp32 rotation matrices;
+    q_gain, k_gain: [dim]. Returns (q, k), each [rows, heads, dim] in out_dtype.
+    """
+    packed = _rows_2d(packed)
+    _device(packed, freqs, q_gain, k_gain)
+    if packed.dtype not in (torch.float16, torch.float32):
+        raise ValueError('packed QKV must be float16 or float32')
+    if freqs.dtype not in (torch.float16, torch.float32):
+        raise ValueError('frequencies must be float16 or float32')
+    if out_dtype not in (torch.float16, torch.float32):
+        raise ValueError('output must be float16 or float32')
+    rows = packed.shape[0]
+    if dim != 128 or packed.shape[1] < 2 * heads * dim:
+        raise ValueError('full 128-wide heads with Q and K in the packed row required')
+    if not (0 < rot_dim <= dim and rot_dim % 2 == 0):
+        raise ValueError('even rotary prefix required')
+    def aligned(t):
+        t = t.contiguous()
+        return t if t.data_ptr() % 16 == 0 else t.clone()
+    freqs = aligned(freqs.reshape(rows, rot_dim // 2, 2, 2))
+    if packed.stride(0) * packed.element_size() % 16 or packed.data_ptr() % 16:
+        packed = packed.contiguous()
+    gq = aligned(q_gain.to(torch.float32).reshape(-1))
+    gk = aligned(k_gain.to(torch.float32).reshape(-1))
+    if gq.numel() != dim or gk.numel() != dim:
+        raise ValueError(f'gains must have {dim} entries')
+    q = torch.empty((rows, heads, dim), dtype=out_dtype, device=packed.device)
+    k = torch.empty((rows, heads, dim), dtype=out_dtype, device=packed.device)
+    if rows == 0:
+        return q, k
+    args = _abi.RmsRopeArgs(in_dtype=_abi.DTYPE_CODE[packed.dtype], packed=packed.data_ptr(), ldp=packed.stride(0),
+                            rows=rows, heads=heads, dim=dim, rot_dim=rot_dim,
+                            freq_dtype=_abi.DTYPE_CODE[freqs.dtype], freqs=freqs.data_ptr(), q_gain=gq.data_ptr(),
+                            k_gain=gk.data_ptr(), eps=float(eps), out_dtype=_abi.DTYPE_CODE[out_dtype],
+                            q_out=q.data_ptr(), k_out=k.data_ptr(), stream=_abi.stream_of(packed))
+    _abi.call('w8a8_rms_rope', args)
+    return q, k
+
+
 def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_group_max=False):
     """Fused FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8 of x [M, 2W].
 

@@ -28,6 +28,9 @@ SHAPES = {
     'dit_half_shard': dict(seed=4, m=204336, hidden=3072, qkv=4608, ffn=4096, chunk=16384, outliers=8),
     # DiT residual stream -> norm2 with the AdaLN tables (9 modulation rows,
     # per-frame segments) -> FC1 input; eps after the 512^2 fold.
+    # The QKV output of the c2 projection (53504 tokens, 3 x 24 heads of 128),
+    # the H3 rotary prefix of 96 dims and fp16 rotation matrices.
+    'dit_rms_rope': dict(seed=6, m=53504, heads=24, rot_dim=96),
     'dit_norm': dict(seed=5, m=16384, hidden=3072, mod_rows=9, frames=16, eps=1e-6 / RESIDUAL_DIVISOR ** 2),
 }
 
@@ -114,6 +117,20 @@ def dit_norm(m=None, hidden=None, seed=None):
     bounds = [m * i // frames for i in range(frames + 1)]
     segments = [(bounds[i], bounds[i + 1], i % s['mod_rows']) for i in range(frames) if bounds[i] < bounds[i + 1]]
     return dict(x=x, weight=weight, shift=shift, scale=scale, segments=segments, eps=s['eps'])
+
+
+def dit_rms_rope(m=None, seed=None):
+    """Packed fp16 QKV rows, fp16 split-half rotation matrices, fp32 gains."""
+    s = SHAPES['dit_rms_rope']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m = m or s['m']
+    packed = (torch.randn((m, 3 * s['heads'] * 128), generator=g) * 2).half()
+    ang = torch.rand((m, s['rot_dim'] // 2), generator=g, dtype=torch.float64) * 6.283185307179586
+    c, sn = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack([torch.stack([c, -sn], -1), torch.stack([sn, c], -1)], -2).half()
+    q_gain = torch.rand(128, generator=g) + 0.5
+    k_gain = torch.rand(128, generator=g) + 0.5
+    return dict(packed=packed, freqs=freqs, q_gain=q_gain, k_gain=k_gain, heads=s['heads'], rot_dim=s['rot_dim'])
 
 
 def quantize_weight(w, device):

@@ -42,6 +42,12 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   (constant power-of-two rows give +-1 exactly; scale = -1 yields the shift
   table row exactly, which pins the label indexing), and a float64 bound
   against torch's own fp32 F.rms_norm on random rows.
+* ``head_sum_squares`` - exact integer totals; a hand-computed absorption
+  case that fixes the slice order and the descending butterfly offsets.
+* ``rms_rope``          - identity frequencies (F = I) reduce it to the
+  pinned norm times the gain; a quarter turn (F = [[0,-1],[1,0]]) swaps the
+  halves with a sign, exactly; scaling the input by a power of two leaves the
+  output unchanged; against a float64 torch restatement on random inputs.
 * ``norm_quantize``     - composition of the pinned norm with the pinned
   ``prepare_activation`` / ``convrot256`` + ``quantize_rows``.
 
@@ -56,5 +62,5 @@ from .w8a8_oracle import (  # noqa: F401
     dequantize_column, residual_add, to_bf16_bits, from_bf16_bits,
     cast_out, quantize_weight, column_linear, row_linear_fc2, ffn_block,
     fma_f32, gated_residual_add, rms_sum_squares, modulated_rms_norm,
-    norm_quantize,
+    norm_quantize, head_sum_squares, rms_rope,
 )

@@ -418,6 +418,72 @@ def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, eps=1e-6,
     return q, s, y
 
 
+ROPE_DIM = 128
+
+
+def head_sum_squares(x):
+    """Sum of squares of each 128-element head vector in this build's order.
+
+    The reference reduces with TileLang's T.reduce_sum
+    (patches/tilelang_fp32_rms_rope.py:22-28, squares via __fmul_rn), whose
+    order is the compiler's; this build fixes one: the vector is cut into 16
+    slices of 8 elements, slice i adds its squares in order to a partial
+    starting at +0, then the 16 partials meet in an xor butterfly (offsets 8,
+    4, 2, 1). x: [..., 128] fp32.
+    """
+    x = _f32(x)
+    sq = (x * x).astype(np.float32).reshape(*x.shape[:-1], 16, 8)
+    part = np.zeros(sq.shape[:-1], np.float32)
+    with np.errstate(over='ignore', invalid='ignore'):
+        for i in range(8):
+            part = part + sq[..., i]
+        lane = np.arange(16)
+        for off in (8, 4, 2, 1):
+            part = part + part[..., lane ^ off]
+    return part[..., 0].copy()
+
+
+def rms_rope(packed, freqs, q_gain, k_gain, heads, rot_dim, eps=1e-6, in_dtype='f16', out_dtype='f16'):
+    """Per-head FP32 RMS normalization and split-half RoPE of packed Q and K.
+
+    patches/tilelang_fp32_rms_rope.py:27-43: per head vector, qr = rsqrtf(ss *
+    fp32(1/dim) + eps); n = (x * qr) * gain; for d < rot_dim (pair p = d mod
+    half, side s = d div half, partner = the other half) the output is
+    __fmaf_rn(n[partner], F[p][s][1-s], n[d] * F[p][s][s]), else n[d]; each
+    step one fp32 rounding, then the cast to the output dtype. rsqrtf
+    (approximate) is replaced by a correctly rounded sqrt and division, and the
+    sum of squares follows ``head_sum_squares``.
+    packed: [rows, >= 2*heads*128] (Q heads, then K heads); freqs: [rows,
+    rot_dim/2, 2, 2]. Returns (q, k), each [rows, heads, 128].
+    """
+    x = _to_f32(packed, in_dtype)
+    rows = x.shape[0]
+    width = heads * ROPE_DIM
+    fr = _f32(np.asarray(freqs, np.float32)).reshape(rows, rot_dim // 2, 2, 2)
+    half = rot_dim // 2
+    outs = []
+    for part, gain in ((x[:, :width], q_gain), (x[:, width:2 * width], k_gain)):
+        v = part.reshape(rows, heads, ROPE_DIM)
+        ss = head_sum_squares(v)
+        with np.errstate(over='ignore', invalid='ignore', divide='ignore'):
+            mean = ss * F32(1.0 / ROPE_DIM)
+            inv = F32(1.0) / np.sqrt(mean + F32(eps))
+            n = (v * inv[..., None]) * _f32(gain).reshape(1, 1, ROPE_DIM)
+        n = n.astype(np.float32)
+        out = n.copy()
+        d = np.arange(rot_dim)
+        side = (d >= half).astype(np.int64)
+        pair = d - side * half
+        other = np.where(side == 1, d - half, d + half)
+        diag = fr[:, pair, side, side]              # [rows, rot_dim]
+        offd = fr[:, pair, side, 1 - side]
+        with np.errstate(over='ignore', invalid='ignore'):
+            a = (n[:, :, :rot_dim] * diag[:, None, :]).astype(np.float32)
+            out[:, :, :rot_dim] = fma_f32(n[:, :, other], np.broadcast_to(offd[:, None, :], a.shape), a)
+        outs.append(cast_out(out, out_dtype))
+    return outs[0], outs[1]
+
+
 def quantize_weight(w):
     """Symmetric per-output-channel INT8 weights with fp32 scales.
 

@@ -35,7 +35,7 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 184, 144, 144]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 184, 144, 144, 104]
 
 
 def _expect_invalid(name, args, fragment):
@@ -114,6 +114,21 @@ def test_norm_argument_checks():
     n = _abi.NormArgs(**{**base, 'q': None, 'q_scale': None, 'y': 8192, 'ldy': 272, 'cols': 272, 'ldx': 272,
                          'rows': 0})
     assert _abi.load().w8a8_norm_quantize(ctypes.byref(n)) == _abi.OK
+
+
+def test_rms_rope_argument_checks():
+    base = dict(struct_size=ctypes.sizeof(_abi.RmsRopeArgs), in_dtype=_abi.F16, packed=4096, ldp=3 * 4 * 128, rows=2,
+                heads=4, dim=128, rot_dim=96, freq_dtype=_abi.F16, freqs=8192, q_gain=12288, k_gain=16384,
+                eps=1e-6, out_dtype=_abi.F16, q_out=20480, k_out=24576)
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'dim': 64}), 'dim')
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'rot_dim': 95}), 'rot_dim')
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'rot_dim': 130}), 'rot_dim')
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'in_dtype': _abi.BF16}), 'in_dtype')
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'ldp': 4 * 128}), 'ldp')
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'q_out': 20482}), 'aligned')
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'freqs': None}), 'null')
+    n = _abi.RmsRopeArgs(**{**base, 'rows': 0})
+    assert _abi.load().w8a8_rms_rope(ctypes.byref(n)) == _abi.OK
 
 
 def test_empty_problems_return_ok_without_launch():

@@ -444,3 +444,71 @@ def test_norm_quantize_composition():
     # the rotated constant rows quantize like the rotation of a constant 0.25 row
     r = o.convrot256(np.full((1, 512), 0.25, np.float32))
     assert np.array_equal(q2[1], o.quantize_rows(r)[0][0])
+
+
+# ------------------------------------------------------------ RMS-RoPE
+def _rope_freqs(angles):
+    c, s = np.cos(angles), np.sin(angles)
+    return np.stack([np.stack([c, -s], -1), np.stack([s, c], -1)], -2).astype(np.float32)
+
+
+def test_head_sum_squares_exact_and_order():
+    rng = np.random.default_rng(21)
+    x = rng.integers(-20, 21, (6, 128)).astype(np.float32)
+    assert np.array_equal(o.head_sum_squares(x), (x.astype(np.int64) ** 2).sum(-1).astype(np.float32))
+    # Slice 0 holds 2^24 then seven squares of 1 (absorbed one at a time); slices
+    # 1..15 hold 8 each; offset 8 meets slice 8 first: 2^24 + 8 + 16 + 32 + 64.
+    x = np.ones((1, 128), np.float32)
+    x[0, 0] = 4096.0
+    assert o.head_sum_squares(x)[0] == np.float32(2 ** 24 + 120)   # exact sum: 2^24 + 127
+
+
+def test_rms_rope_identity_frequencies_are_the_norm():
+    rng = np.random.default_rng(22)
+    rows, heads, rot = 3, 2, 96
+    p = (rng.standard_normal((rows, 3 * heads * 128)) * 2).astype(np.float16)
+    gq = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    gk = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    f = _rope_freqs(np.zeros((rows, rot // 2)))
+    q, k = o.rms_rope(p, f, gq, gk, heads, rot, eps=1e-6, out_dtype='f32')
+    x = p.astype(np.float32)[:, :2 * heads * 128].reshape(rows, 2, heads, 128)
+    inv = np.float32(1) / np.sqrt(o.head_sum_squares(x) * np.float32(1 / 128) + np.float32(1e-6))
+    want_q = (x[:, 0] * inv[:, 0, :, None]) * gq
+    want_k = (x[:, 1] * inv[:, 1, :, None]) * gk
+    assert np.array_equal(q, want_q) and np.array_equal(k, want_k)
+
+
+def test_rms_rope_quarter_turn_swaps_halves():
+    rng = np.random.default_rng(23)
+    rows, heads, rot = 2, 2, 96
+    p = rng.standard_normal((rows, 3 * heads * 128)).astype(np.float16)
+    g = np.ones(128, np.float32)
+    f = _rope_freqs(np.full((rows, rot // 2), np.pi / 2))
+    f = np.round(f)                                   # exactly [[0, -1], [1, 0]]
+    base, _ = o.rms_rope(p, _rope_freqs(np.zeros((rows, rot // 2))), g, g, heads, rot, out_dtype='f32')
+    q, _ = o.rms_rope(p, f, g, g, heads, rot, out_dtype='f32')
+    h = rot // 2
+    assert np.array_equal(q[..., :h], -base[..., h:rot])
+    assert np.array_equal(q[..., h:rot], base[..., :h])
+    assert np.array_equal(q[..., rot:], base[..., rot:])
+
+
+def test_rms_rope_power_of_two_scale_invariance_and_float64():
+    import torch
+    rng = np.random.default_rng(24)
+    rows, heads, rot = 4, 3, 96
+    p = rng.standard_normal((rows, 3 * heads * 128)).astype(np.float32)
+    gq = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    gk = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    f = _rope_freqs(rng.uniform(0, 2 * np.pi, (rows, rot // 2)))
+    q, k = o.rms_rope(p, f, gq, gk, heads, rot, eps=0.0, in_dtype='f32', out_dtype='f32')
+    q2, k2 = o.rms_rope(p * np.float32(8), f, gq, gk, heads, rot, eps=0.0, in_dtype='f32', out_dtype='f32')
+    assert np.array_equal(q, q2) and np.array_equal(k, k2)
+    x = torch.from_numpy(p).double()[:, :heads * 128].reshape(rows, heads, 128)
+    n = torch.nn.functional.rms_norm(x, (128,), torch.from_numpy(gq).double(), 0.0)
+    ft = torch.from_numpy(f).double()
+    lo, hi = n[..., :rot // 2], n[..., rot // 2:rot]
+    out = n.clone()
+    out[..., :rot // 2] = ft[:, None, :, 0, 0] * lo + ft[:, None, :, 0, 1] * hi
+    out[..., rot // 2:rot] = ft[:, None, :, 1, 0] * lo + ft[:, None, :, 1, 1] * hi
+    assert np.max(np.abs(q - out.numpy())) < 4e-6 * np.max(np.abs(out.numpy()))
