@@ -115,6 +115,19 @@ class DiTFeedForwardINT8(nn.Module):
         self.fc1.operator_policy = policy
         self.fc2.operator_policy = policy
 
+    @classmethod
+    def from_projections(cls, fc1, fc2, policy=None):
+        """An FFN over existing FC1 / FC2 projection modules (e.g. a loaded
+        checkpoint block's ``fc1`` and ``fc2``)."""
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.fc1, self.fc2 = fc1, fc2
+        policy = policy or H3OperatorPolicy()
+        self.operator_policy = policy
+        self.fc1.operator_policy = policy
+        self.fc2.operator_policy = policy
+        return self
+
     def forward(self, h, residual, gate=None, segments=None):
         """residual <- residual + branch, or with the modulation ``gate`` table
         and ``segments`` the DiT gated update (tp_dit.py:356-362)."""
