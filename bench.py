@@ -147,6 +147,21 @@ def run_dit_ffn(args, torch, dev):
             v['frac'] = v['tops'] / PEAK_INT8_TOPS
         else:
             v['frac'] = v['gbs'] / PEAK_HBM_GBS
+    # The DiT route of FC2: the AdaLN gate table and per-frame row labels
+    # applied in the epilogue (fp32 FMA update), timed on its own.
+    from w8a8.h3_tensor_flow import labels_for
+    pq = kernels.swiglu_quantize(kernels.gemm(*kernels.quantize_rows(h, convrot=True, round_rotated=True)[:1], w1,
+                                              epilogue=kernels.EPI_COLUMN,
+                                              row_scale=kernels.quantize_rows(h, convrot=True)[1],
+                                              col_scale=ws1, out_dtype=torch.float16))
+    gate = torch.randn((9, hidden), generator=torch.Generator().manual_seed(11)).to(dev)
+    segs = [(m * i // 16, m * (i + 1) // 16, i % 9) for i in range(16)]
+    labels = labels_for(m, segs, 9, device=dev)
+    tg = timed(torch, lambda: kernels.gemm(pq['q'], w2, epilogue=kernels.EPI_ROW, row_scale=pq['scale'],
+                                           col_scale=ws2, out_dtype=torch.float16, residual=res, gate=gate,
+                                           gate_labels=labels), args.steps, args.warmup)
+    kernels_out['fc2_gemm_gated'] = dict(us=tg * 1e3, tops=ops_fc2 / (tg * 1e-3) / 1e12)
+    kernels_out['fc2_gemm_gated']['frac'] = kernels_out['fc2_gemm_gated']['tops'] / PEAK_INT8_TOPS
     fc1 = kernels_out['fc1_gemm']
     traffic = traffic_from_profiles('fc1_gemm')
     roofline = dict(bound='mfma', achieved=round(fc1['tops'], 1), peak=PEAK_INT8_TOPS, unit='TOPS',

@@ -72,6 +72,7 @@ static void fill_epilogue(GemmParams& p, const Args* a) {
   p.gate = a->gate;
   p.labels = a->gate_labels;
   p.ldg = a->ldg;
+  p.gvec = a->gate != nullptr && aligned16(a->gate) && a->ldg % 4 == 0;
   p.out = a->out;
   p.ldc = a->ldc;
   p.vec_out = aligned16(a->out) && a->ldc % 4 == 0;

@@ -294,8 +294,16 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       for (int it = 0; it < R::ITERS; ++it) {
         const int row = it * R::RPI + orow;
         const float* gr = p.gate + (int64_t)__shfl(lbl[mb], row, 64) * p.ldg;
+        if (p.gvec && full_cols) {
 #pragma unroll
-        for (int j = 0; j < R::CPL; ++j) gv[it][j] = gr[min(ncol + j, p.n - 1)];
+          for (int q = 0; q < R::CPL / 4; ++q) {
+            const float4 g4 = *reinterpret_cast<const float4*>(gr + ncol + 4 * q);
+            gv[it][4 * q] = g4.x; gv[it][4 * q + 1] = g4.y; gv[it][4 * q + 2] = g4.z; gv[it][4 * q + 3] = g4.w;
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < R::CPL; ++j) gv[it][j] = gr[min(ncol + j, p.n - 1)];
+        }
       }
     }
     // acc[nb][mb] group g holds columns 32 nb + 8 g + 4 fh + [0, 4) of row fr.
@@ -762,6 +770,9 @@ void gemm_i8_persistent(GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     };
     do {  // nks >= 1
+      // At a tile's last stage the next tile's first fragments are read
+      // after the epilogue, so they do not hold registers through it.
+      const bool last = ks + 1 == nks;
       const int cur_b = next_slot(cur_a);
       const int nxt_a = next_slot(cur_b), nxt_b = next_slot(nxt_a), fill = next_slot(nxt_b);
       substep(fa0, fb0, cur_a, cur_b, 1, fa1, fb1, B_{}, H1{}, nxt_b);
@@ -776,15 +787,15 @@ void gemm_i8_persistent(GemmParams p) {
       // this stage returned;
       wait_vm_lgkm<8>();
       block_barrier();   // ... for every wave: both slots are released.
-      read_group(nxt_a, nxt_b, 0, 0, fa0, fb0);
+      if (!last) read_group(nxt_a, nxt_b, 0, 0, fa0, fb0);
       dma_one(B_{}, std::integral_constant<int, 0>{}, cur_a);
       mfma_row(1, fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
-      read_group(nxt_a, nxt_b, 0, 1, fa0, fb0);
+      if (!last) read_group(nxt_a, nxt_b, 0, 1, fa0, fb0);
       dma_one(B_{}, std::integral_constant<int, 1>{}, cur_a);
       mfma_row(2, fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
-      read_group(nxt_a, nxt_b, 0, 2, fa0, fb0);
+      if (!last) read_group(nxt_a, nxt_b, 0, 2, fa0, fb0);
       dma_one(B_{}, std::integral_constant<int, 2>{}, cur_a);
       mfma_row(3, fa1, fb1);
       __builtin_amdgcn_sched_barrier(0);
@@ -818,6 +829,11 @@ void gemm_i8_persistent(GemmParams p) {
     // stage; a wave's DMA into a slot writes the same 8 KB it used for
     // staging, so its own staging reads returning is all that unit waits for.
     wait_lgkm();
+    // The next tile's first fragments (its stage 0 landed before the last
+    // barrier, in the slots cur_a and the one after).
+    read_group(cur_a, next_slot(cur_a), 0, 0, fa0, fb0);
+    read_group(cur_a, next_slot(cur_a), 0, 1, fa0, fb0);
+    read_group(cur_a, next_slot(cur_a), 0, 2, fa0, fb0);
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }

@@ -27,6 +27,7 @@ struct GemmParams {
   const float* gate;      // DiT gate table [R, ldg] (with residual), or null
   const int32_t* labels;  // row -> gate-table row
   int64_t ldg;
+  int gvec;               // gate rows allow float4 loads (16-byte base, ldg % 4 == 0)
   void* out;
   int64_t ldc;
   int vec_out;  // out rows allow 4-element vector stores (16-byte base, ldc % 4 == 0)
