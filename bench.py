@@ -531,7 +531,73 @@ def run_dit_rms_rope(args, torch, dev):
     return res
 
 
-WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy, 'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv,
+def run_dit_qkv_rope(args, torch, dev):
+    """DiT QKV projection with the RMS-RoPE epilogue (53504 tokens, 3072 ->
+    3 x 24 heads of 128, rotary prefix 96, fp16 rotation matrices), against
+    the same GEMM followed by the standalone RMS-RoPE kernel. The activation
+    is quantized once outside the timed region (both variants share it)."""
+    from w8a8 import kernels, workloads
+    data = workloads.dit_qkv_rope()
+    m, k = data['x'].shape
+    n = data['w'].shape[0]
+    heads, rot = data['heads'], data['rot_dim']
+    wq, ws = workloads.quantize_weight(data['w'], dev)
+    x = data['x'].to(dev)
+    freqs, gq, gk = (data[t].to(dev) for t in ('freqs', 'q_gain', 'k_gain'))
+    codes, a = kernels.quantize_rows(x, convrot=True)
+    rope = dict(heads=heads, rot_dim=rot, freqs=freqs, q_gain=gq, k_gain=gk, eps=1e-6)
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+
+    def plain():
+        return kernels.gemm(codes, wq, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=ws, out=out)
+
+    def rope_only():
+        return kernels.rms_rope(out, freqs, gq, gk, heads=heads, rot_dim=rot, eps=1e-6)
+
+    def fused():
+        return kernels.gemm(codes, wq, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=ws, out=out, rope=rope)
+
+    def unfused():
+        plain()
+        return rope_only()
+
+    tp = timed(torch, plain, args.steps, args.warmup)
+    tr = timed(torch, rope_only, args.steps, args.warmup)
+    tu = timed(torch, unfused, args.steps, args.warmup)
+    tf = timed(torch, fused, args.steps, args.warmup)
+    ops = 2.0 * m * n * k
+    tops = ops / (tf * 1e-3) / 1e12
+    res = dict(metric='DiT QKV 53504x3072->9216 + RMS-RoPE epilogue us', value=round(tf * 1e3, 1), unit='us',
+               higher_is_better=False, dtype='int8', data='synthetic',
+               config=dict(workload='dit_qkv_rope', m=m, k=k, n=n, heads=heads, rot_dim=rot),
+               roofline=dict(bound='mfma', achieved=round(tops, 1), peak=PEAK_INT8_TOPS, unit='TFLOP/s',
+                             frac=round(tops / PEAK_INT8_TOPS, 4), traffic=traffic_from_profiles('qkv_rope_gemm'),
+                             kernel='gemm_i8_persistent<2,1,8> (QKV GEMM with the RMS-RoPE epilogue)',
+                             algorithmic=f'{ops:.4g} int8 ops per launch'),
+               kernels=dict(fused_us=round(tf * 1e3, 1), gemm_us=round(tp * 1e3, 1),
+                            rms_rope_us=round(tr * 1e3, 1), unfused_us=round(tu * 1e3, 1),
+                            speedup=round(tu / tf, 3)))
+    if not args.no_cpu_baseline:
+        import oracle as o
+        rows = min(args.cpu_rows // 8, m)
+        xs, wqn, wsn = data['x'][:rows].numpy(), wq.cpu().numpy(), ws.cpu().numpy().reshape(-1)
+        wf = wqn.astype('float64')
+        f_np = data['freqs'][:rows].float().numpy()
+        gq_np, gk_np = data['q_gain'].numpy(), data['k_gain'].numpy()
+
+        def cpu():
+            packed = o.column_linear(xs, wqn, wsn, w_f64=wf)
+            return o.rms_rope(packed, f_np, gq_np, gk_np, heads, rot, eps=1e-6)
+
+        tc = _cpu_rows_timing(cpu) * m / rows
+        res['cpu_baseline'] = dict(value=round(tc * 1e6, 1), unit='us', cores=blas_threads(), kind='port',
+                                   sample=f'oracle column projection + rms_rope on {rows} of {m} rows, '
+                                          f'scaled x{m / rows:g}')
+    return res
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
+             'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv, 'dit_qkv_rope': run_dit_qkv_rope,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
 
 

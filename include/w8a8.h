@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 5
+#define W8A8_ABI_VERSION 6
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -255,10 +255,34 @@ int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
  *   the workspace and a second kernel adds them and runs the epilogue (the
  *   result is bit-identical to the unsplit GEMM). NULL / 0 never splits.
  *   Calls that share a workspace must not overlap.
+ * rope: optional RMS-RoPE epilogue (W8A8RopeEpilogue) for a packed QKV
+ *   projection: the Q and K heads of the output are normalized and rotated
+ *   as w8a8_rms_rope would on the stored fp16 output, in the same kernel, so
+ *   the QKV output makes no second HBM trip (replaces
+ *   patches/tilelang_fp32_rms_rope.py:6-66 after the QKV projection,
+ *   patches/tp_dit.py:288-301). Requires out_dtype F16, no bias, residual
+ *   or gate, (rot_dim / 2) % 8 == 0, m > 64, k % 128 == 0, 16-byte aligned
+ *   output rows, operands spanning < 4 GB; never splits K. Other requests return
+ *   W8A8_ERR_UNSUPPORTED (use w8a8_rms_rope on the output instead).
  * Requirements: k % 16 == 0; a, b 16-byte aligned; lda, ldb % 16 == 0;
  *   out element-aligned (rows are written with vector stores when out is
  *   16-byte aligned and ldc % 4 == 0).
  */
+/* The RMS-RoPE epilogue of w8a8_gemm (see W8A8GemmArgs.rope). Output
+ * columns [0, heads*128) are the Q heads and [heads*128, 2*heads*128) the K
+ * heads (the numerics of w8a8_rms_rope with dim 128); later columns (V) are
+ * stored unchanged. freqs: [m, rot_dim/2, 2, 2] of freq_dtype (F16 or F32);
+ * q_gain, k_gain: [128] fp32; all 16-byte aligned. */
+typedef struct W8A8RopeEpilogue {
+  int32_t heads;
+  int32_t rot_dim;
+  int32_t freq_dtype;
+  float eps;
+  const void* freqs;
+  const float* q_gain;
+  const float* k_gain;
+} W8A8RopeEpilogue;
+
 typedef struct W8A8GemmArgs {
   uint32_t struct_size;
   int32_t epilogue;
@@ -284,6 +308,7 @@ typedef struct W8A8GemmArgs {
   int64_t ldc;
   void* workspace;
   int64_t workspace_bytes;
+  const struct W8A8RopeEpilogue* rope;
   void* stream;
 } W8A8GemmArgs;
 

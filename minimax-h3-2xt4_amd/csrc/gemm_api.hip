@@ -115,6 +115,32 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
     p.vec16 = aligned16(a->out) && (a->ldc * es) % 16 == 0 &&
               (a->residual == nullptr || (aligned16(a->residual) && a->ldr % 8 == 0));
   }
+  if (a->rope) {
+    const W8A8RopeEpilogue* r = a->rope;
+    W8A8_REQUIRE(r->heads > 0 && 2 * (int64_t)r->heads * 128 <= a->n,
+                 "w8a8_gemm: rope needs heads > 0 and n >= 2 * heads * 128");
+    W8A8_REQUIRE(r->rot_dim > 0 && r->rot_dim <= 128 && r->rot_dim % 2 == 0, "w8a8_gemm: rope rot_dim %d invalid",
+                 r->rot_dim);
+    W8A8_REQUIRE(r->freq_dtype == W8A8_F16 || r->freq_dtype == W8A8_F32, "w8a8_gemm: rope freq_dtype not F16/F32");
+    W8A8_REQUIRE(r->freqs && r->q_gain && r->k_gain && aligned16(r->freqs) && aligned16(r->q_gain) &&
+                     aligned16(r->k_gain),
+                 "w8a8_gemm: rope freqs and gains must be non-null and 16-byte aligned");
+    if (a->epilogue == W8A8_EPI_INT32 || a->out_dtype != W8A8_F16 || a->bias || a->residual || a->gate ||
+        (r->rot_dim / 2) % 8 != 0 || a->m <= 64 || a->k % 128 != 0 || !p.vec16 ||
+        (a->m - 1) * a->lda + a->k >= (1LL << 32) || (a->n - 1) * a->ldb + a->k >= (1LL << 32)) {
+      set_error("w8a8_gemm: the rope epilogue needs F16 output without bias/residual/gate, (rot_dim/2) %% 8 == 0, "
+                "m > 64, k %% 128 == 0, 16-byte aligned output rows and operands under 4 GB");
+      return W8A8_ERR_UNSUPPORTED;
+    }
+    p.rope_heads = r->heads;
+    p.rope_rot = r->rot_dim;
+    p.rope_half = r->rot_dim / 2;
+    p.rope_f32 = r->freq_dtype == W8A8_F32;
+    p.rope_eps = r->eps;
+    p.rope_freqs = r->freqs;
+    p.rope_q_gain = r->q_gain;
+    p.rope_k_gain = r->k_gain;
+  }
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   int rc2;
   switch (a->epilogue) {

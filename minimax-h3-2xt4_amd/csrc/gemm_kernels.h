@@ -210,7 +210,7 @@ __device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xF | (
 
 // Compile-time epilogue options of the persistent kernel (each variant
 // carries only the loads it uses).
-enum EpilogueFlags { kWithBias = 1, kWithResidual = 2, kWithGate = 4 };
+enum EpilogueFlags { kWithBias = 1, kWithResidual = 2, kWithGate = 4, kWithRope = 8 };
 
 // Layout of the staged epilogue's read-out: a lane owns CPL consecutive
 // columns of a 64-column half of the quadrant (8 for 2-byte outputs, 4 for
@@ -339,37 +339,245 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       const int row = it * R::RPI + orow;
       const int m = mrow + row;
       const float a = arow[it];
-      uint32_t bits[R::CPL];
+      // words[i]: output elements 2 i, 2 i + 1 (2-byte outputs) or element i.
+      uint32_t words[4];
+      if constexpr (OUT == kF16) {
+        // FP16 pairs convert in one packed instruction; with a residual the
+        // rounded branch is widened again, added and rounded per pair.
 #pragma unroll
-      for (int j = 0; j < R::CPL; ++j)
-        bits[j] = out_bits<EPI, OUT>(c[it][j], a, wsc[h][j], bsc[h][j], has_bias);
-      if constexpr (has_res) {
-        const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
+        for (int i = 0; i < 4; ++i) {
+          float y0 = dequant1<EPI>(c[it][2 * i], a, wsc[h][2 * i]);
+          float y1 = dequant1<EPI>(c[it][2 * i + 1], a, wsc[h][2 * i + 1]);
+          if constexpr (has_bias) {
+            y0 = y0 + bsc[h][2 * i];
+            y1 = y1 + bsc[h][2 * i + 1];
+          }
+          words[i] = f2h2_of_f32(y0, y1);
+        }
+        if constexpr (has_res) {
+          const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
 #pragma unroll
-        for (int j = 0; j < R::CPL; ++j) {
-          const float res = h2f((uint16_t)(rw[j >> 1] >> (16 * (j & 1))));
-          const float branch = h2f((uint16_t)bits[j]);
-          if constexpr (has_gate) bits[j] = f2h_of_f32(__builtin_fmaf(branch, gv[it][j], res));
-          else bits[j] = f2h(res + branch);
+          for (int i = 0; i < 4; ++i) {
+            const float r0 = h2f((uint16_t)(rw[i] & 0xffffu)), r1 = h2f((uint16_t)(rw[i] >> 16));
+            const float b0 = h2f((uint16_t)(words[i] & 0xffffu)), b1 = h2f((uint16_t)(words[i] >> 16));
+            if constexpr (has_gate)
+              words[i] = f2h2_of_f32(__builtin_fmaf(b0, gv[it][2 * i], r0), __builtin_fmaf(b1, gv[it][2 * i + 1], r1));
+            else
+              words[i] = f2h2_of_f32(r0 + b0, r1 + b1);
+          }
+        }
+      } else {
+        uint32_t bits[R::CPL];
+#pragma unroll
+        for (int j = 0; j < R::CPL; ++j)
+          bits[j] = out_bits<EPI, OUT>(c[it][j], a, wsc[h][j], bsc[h][j], has_bias);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if constexpr (R::ES == 2) words[i] = bits[2 * i] | (bits[2 * i + 1] << 16);
+          else words[i] = bits[i];
         }
       }
       char* o = reinterpret_cast<char*>(p.out) + (out_off + (int64_t)m * p.ldc + ncol) * R::ES;
       if (INTERIOR || (m < p.m && full_cols)) {
-        if constexpr (R::ES == 2)
-          *reinterpret_cast<uint4*>(o) = make_uint4(bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16),
-                                                    bits[4] | (bits[5] << 16), bits[6] | (bits[7] << 16));
-        else
-          *reinterpret_cast<uint4*>(o) = make_uint4(bits[0], bits[1], bits[2], bits[3]);
+        *reinterpret_cast<uint4*>(o) = make_uint4(words[0], words[1], words[2], words[3]);
       } else if (!INTERIOR && m < p.m) {
 #pragma unroll
         for (int j = 0; j < R::CPL; ++j) {
           if (ncol + j < p.n) {
-            if constexpr (R::ES == 2) reinterpret_cast<uint16_t*>(o)[j] = (uint16_t)bits[j];
-            else reinterpret_cast<uint32_t*>(o)[j] = bits[j];
+            if constexpr (R::ES == 2) reinterpret_cast<uint16_t*>(o)[j] = (uint16_t)(words[j >> 1] >> (16 * (j & 1)));
+            else reinterpret_cast<uint32_t*>(o)[j] = words[j];
           }
         }
       }
     }
+  }
+}
+
+// Column scales (wsc[0]) and RMS gains (wsc[1]) of the columns a lane
+// handles in the RMS-RoPE epilogue: nw + 8 (lane % 16) + [0, 8). The gains
+// are Q's below heads * 128 columns, K's below 2 * heads * 128, and unused
+// in the V columns past them.
+template <int EPI>
+__device__ __forceinline__ void load_rope_scales(const GemmParams& p, int nw, int lane, float (&wsc)[2][8]) {
+  const int d0 = 8 * (lane & 15), width = p.rope_heads * 128;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) wsc[0][j] = p.col_scale[(int64_t)min(nw + d0 + j, p.n - 1) * p.col_stride];
+  if (nw < 2 * width) {
+    const float4* g = reinterpret_cast<const float4*>((nw < width ? p.rope_q_gain : p.rope_k_gain) + d0);
+    const float4 g0 = g[0], g1 = g[1];
+    wsc[1][0] = g0.x; wsc[1][1] = g0.y; wsc[1][2] = g0.z; wsc[1][3] = g0.w;
+    wsc[1][4] = g1.x; wsc[1][5] = g1.y; wsc[1][6] = g1.z; wsc[1][7] = g1.w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wsc[1][j] = 0.0f;
+  }
+}
+
+// Rotation matrix entries of the lane's eight elements d0 .. d0 + 7 of one
+// row: element d (pair p = d mod half, side s = d div half) is multiplied by
+// F[p][s][s] (diag) and its partner by F[p][s][1 - s] (offd). half % 8 == 0,
+// so the eight elements are on one side and use the consecutive pairs
+// p0 .. p0 + 7, a 16-byte aligned block of the row's table. (Four 16-byte
+// loads and selects beat eight 4-byte loads of just the side's words: the
+// epilogue is bound by the number of memory instructions.)
+template <int FQ>
+__device__ __forceinline__ void load_rope_freqs(const void* frow, int p0, int side, float (&diag)[8],
+                                                float (&offd)[8]) {
+  if constexpr (FQ == kF32) {
+    const float* f = reinterpret_cast<const float*>(frow) + 4 * p0 + 2 * side;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float2 v = *reinterpret_cast<const float2*>(f + 4 * i);   // F[p][s][0], F[p][s][1]
+      diag[i] = side ? v.y : v.x;
+      offd[i] = side ? v.x : v.y;
+    }
+  } else {
+    const uint4* f = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(frow) + 4 * p0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint4 u = f[k];   // pairs p0 + 2 k, p0 + 2 k + 1
+      const uint32_t w[2] = {side ? u.y : u.x, side ? u.w : u.z};
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const float lo = h2f((uint16_t)(w[q] & 0xffffu)), hi = h2f((uint16_t)(w[q] >> 16));
+        diag[2 * k + q] = side ? hi : lo;
+        offd[2 * k + q] = side ? lo : hi;
+      }
+    }
+  }
+}
+
+// RMS-RoPE epilogue of one 128x128 quadrant (FP16 output, no split) that is
+// one 128-column head of Q (nw < heads * 128) or of K (nw < 2 * heads *
+// 128); V quadrants take the plain staged epilogue. In 8 passes of 16 rows the
+// lanes holding those rows in the MFMA layout write their raw accumulators
+// to the wave's 8 KB LDS slice (16-byte chunks XOR-swizzled by row); lane
+// (rq, t) = (lane / 16, lane % 16) then reads columns 8 t .. 8 t + 7 of rows
+// 4 it + rq (it = 0..3), dequantizes and rounds them to FP16 exactly as the
+// plain GEMM output, and for a Q or K head continues as the standalone
+// RMS-RoPE kernel does on that FP16 output: the sum of squares of the row's
+// 128 values (each lane's eight in order, then an xor butterfly over the 16
+// lanes of the row, offsets 8, 4, 2, 1), 1 / sqrt(sum * 2^-7 + eps), the
+// gain, and the rotation with the partner element, read back from the
+// slice after the normalized values replace the accumulators there. Rows
+// past m are not stored (their rotation matrices are those of row m - 1).
+template <int EPI, int FQ>
+__device__ __forceinline__ void store_quadrant_rope(const GemmParams& p, v16i (&acc)[4][4], const float (&wsc)[2][8],
+                                                    const float (&as)[4], int mw, int nw, int lane, int8_t* stage) {
+  constexpr int RB = 512;   // 128 four-byte values per staged row
+  constexpr int FES = FQ == kF32 ? 4 : 2;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int rq = lane >> 4, t = lane & 15;
+  const int d0 = 8 * t, half = p.rope_half;
+  const bool rotated = d0 < p.rope_rot;
+  const int side0 = d0 >= half ? 1 : 0;
+  const int p0 = d0 - side0 * half;
+  const int other0 = side0 ? d0 - half : d0 + half;
+  const int ncol = nw + d0;
+  uint16_t* const out = reinterpret_cast<uint16_t*>(p.out);
+#pragma unroll
+  for (int pass = 0; pass < 8; ++pass) {   // unrolled: acc is indexed by pass
+    const int mb = pass >> 1, hh = pass & 1;
+    const int mrow = mw + mb * 32 + 16 * hh;
+    // acc[nb][mb] group g holds columns 32 nb + 8 g + 4 fh + [0, 4) of row fr.
+    if ((fr >> 4) == hh) {
+      const int r = fr & 15;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int chunk = 8 * nb + 2 * g + fh;
+          *reinterpret_cast<v4i*>(stage + r * RB + ((chunk ^ r) << 4)) =
+              v4i{acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2], acc[nb][mb][4 * g + 3]};
+        }
+    }
+    asm volatile("" ::: "memory");
+    float arow[4];
+    int c[4][8];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int r = 4 * it + rq;
+      arow[it] = __shfl(as[mb], 16 * hh + r, 64);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const v4i v = *reinterpret_cast<const v4i*>(stage + r * RB + (((2 * t + q) ^ r) << 4));
+        c[it][4 * q] = v[0]; c[it][4 * q + 1] = v[1]; c[it][4 * q + 2] = v[2]; c[it][4 * q + 3] = v[3];
+      }
+    }
+    asm volatile("" ::: "memory");  // the slice's next writes stay behind these reads
+    // y: the plain GEMM's FP16 outputs, widened. Sum of squares: y * y is
+    // exact in fp32, so fma(y, y, ss) rounds once, like ss + y * y.
+    float y[4][8], ss[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      ss[it] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = f2h2_of_f32(dequant1<EPI>(c[it][2 * i], arow[it], wsc[0][2 * i]),
+                                       dequant1<EPI>(c[it][2 * i + 1], arow[it], wsc[0][2 * i + 1]));
+        y[it][2 * i] = h2f((uint16_t)(w & 0xffffu));
+        y[it][2 * i + 1] = h2f((uint16_t)(w >> 16));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss[it] = __builtin_fmaf(y[it][j], y[it][j], ss[it]);
+#pragma unroll
+      for (int off = 8; off >= 1; off >>= 1) ss[it] = ss[it] + __shfl_xor(ss[it], off, 64);
+    }
+    // Each row's 1 / sqrt once: lane t of group rq takes row 4 (t % 4) + rq,
+    // then every lane fetches its four rows' values.
+    const int mine = t & 3;
+    const float ssm = mine == 0 ? ss[0] : mine == 1 ? ss[1] : mine == 2 ? ss[2] : ss[3];
+    const float invm = 1.0f / __builtin_sqrtf(ssm * 0.0078125f + p.rope_eps);
+    float nv[4][8];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const float inv = __shfl(invm, (lane & 48) | it, 64);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float s1 = y[it][j] * inv;
+        nv[it][j] = s1 * wsc[1][j];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int r = 4 * it + rq;
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        *reinterpret_cast<float4*>(stage + r * RB + (((2 * t + q) ^ r) << 4)) =
+            make_float4(nv[it][4 * q], nv[it][4 * q + 1], nv[it][4 * q + 2], nv[it][4 * q + 3]);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int r = 4 * it + rq;
+      const int m = mrow + r;
+      float o[8];
+      if (rotated) {
+        float part[8], diag[8], offd[8];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const float4 v = *reinterpret_cast<const float4*>(stage + r * RB + (((other0 / 4 + q) ^ r) << 4));
+          part[4 * q] = v.x; part[4 * q + 1] = v.y; part[4 * q + 2] = v.z; part[4 * q + 3] = v.w;
+        }
+        const char* frow = reinterpret_cast<const char*>(p.rope_freqs) + (int64_t)min(m, p.m - 1) * half * 4 * FES;
+        load_rope_freqs<FQ>(frow, p0, side0, diag, offd);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float a = nv[it][j] * diag[j];
+          o[j] = __builtin_fmaf(part[j], offd[j], a);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = nv[it][j];
+      }
+      if (m < p.m) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = f2h2_of_f32(o[2 * i], o[2 * i + 1]);
+        *reinterpret_cast<uint4*>(out + (int64_t)m * p.ldc + ncol) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    asm volatile("" ::: "memory");  // the next pass's slice writes stay behind these reads
   }
 }
 
@@ -735,7 +943,16 @@ void gemm_i8_persistent(GemmParams p) {
       as[mb] = EPI != kEpiInt32 ? p.row_scale[min(mw + mb * 32 + fr, p.m - 1)] : 0.0f;
       if constexpr ((FLAGS & kWithGate) != 0) lbl[mb] = p.labels[min(mw + mb * 32 + fr, p.m - 1)];
     }
-    load_readout_scales<EPI, OUT, (FLAGS & kWithBias) != 0>(p, nw, lane, wsc, braw);
+    if constexpr ((FLAGS & kWithRope) != 0) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) braw[h][j] = 0;
+      if (nw < 2 * p.rope_heads * 128) load_rope_scales<EPI>(p, nw, lane, wsc);
+      else load_readout_scales<EPI, OUT, false>(p, nw, lane, wsc, braw);
+    } else {
+      load_readout_scales<EPI, OUT, (FLAGS & kWithBias) != 0>(p, nw, lane, wsc, braw);
+    }
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -820,7 +1037,18 @@ void gemm_i8_persistent(GemmParams p) {
     const int64_t out_off = (item % ksplit) * p.split_stride;
     // Interior quadrants take a copy without store masks (not for the gate
     // variants, whose registers a second copy would push into spills).
-    if ((FLAGS & kWithGate) == 0 && p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
+    if constexpr ((FLAGS & kWithRope) != 0) {
+      if (nw >= 2 * p.rope_heads * 128) {   // V columns
+        if (p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
+          store_quadrant32_passes<EPI, OUT, 0, true>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
+        else
+          store_quadrant32_passes<EPI, OUT, 0, false>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
+      } else if (p.rope_f32) {
+        store_quadrant_rope<EPI, kF32>(p, acc, wsc, as, mw, nw, lane, stage_w);
+      } else {
+        store_quadrant_rope<EPI, kF16>(p, acc, wsc, as, mw, nw, lane, stage_w);
+      }
+    } else if ((FLAGS & kWithGate) == 0 && p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
       store_quadrant32_passes<EPI, OUT, FLAGS, (FLAGS & kWithGate) == 0>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,
                                                                         stage_w, out_off);
     else
@@ -1054,7 +1282,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
   int rc = current_device(dev);
   if (rc != W8A8_OK) return rc;
   int64_t ws_need = 0;
-  const int ksplit = p.ws ? gemm_ksplit(p.m, p.n, p.k, dev, &ws_need) : 1;
+  const int ksplit = p.ws && !p.rope_heads ? gemm_ksplit(p.m, p.n, p.k, dev, &ws_need) : 1;
   if (ksplit > 1 && p.ws_bytes >= ws_need) {
     GemmParams q = p;
     q.out = p.ws;
@@ -1078,6 +1306,8 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     return p.bias_dtype ? launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s)
                         : launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
   } else {
+    // The host admits the RMS-RoPE epilogue only without bias, residual or gate.
+    if (p.rope_heads) return launch_persistent<EPI, OUT, kWithRope>(p, tiles, dev, s);
     switch ((p.bias_dtype ? kWithBias : 0) | (p.residual ? kWithResidual : 0) | (p.gate ? kWithGate : 0)) {
       case 0: return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
       case kWithBias: return launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s);

@@ -28,6 +28,13 @@ struct GemmParams {
   const int32_t* labels;  // row -> gate-table row
   int64_t ldg;
   int gvec;               // gate rows allow float4 loads (16-byte base, ldg % 4 == 0)
+  // RMS-RoPE epilogue (rope_heads > 0): output columns [0, 2 * rope_heads *
+  // 128) are Q then K heads, normalized and rotated after the fp16 rounding.
+  int rope_heads, rope_half, rope_rot, rope_f32;
+  float rope_eps;
+  const void* rope_freqs;
+  const float* rope_q_gain;
+  const float* rope_k_gain;
   void* out;
   int64_t ldc;
   int vec_out;  // out rows allow 4-element vector stores (16-byte base, ldc % 4 == 0)

@@ -38,6 +38,16 @@ __device__ __forceinline__ uint16_t f2h_of_f32(float f) {
   __asm__("" : "+v"(f));
   return f2h(f);
 }
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+// Two fp32 -> fp16 conversions (round to nearest even) in one packed
+// instruction, a in the low half; like f2h_of_f32, each operand first exists
+// as a rounded fp32 value.
+__device__ __forceinline__ uint32_t f2h2_of_f32(float a, float b) {
+  __asm__("" : "+v"(a));
+  __asm__("" : "+v"(b));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2h));
+}
 __device__ __forceinline__ float bf2f(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }

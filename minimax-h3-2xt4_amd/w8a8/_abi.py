@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -34,6 +34,11 @@ class SwigluArgs(ctypes.Structure):
                 ('group_max', _p), ('q', _p), ('ldq', _c.c_int64), ('scale', _p), ('stream', _p)]
 
 
+class RopeEpilogue(ctypes.Structure):
+    _fields_ = [('heads', _c.c_int32), ('rot_dim', _c.c_int32), ('freq_dtype', _c.c_int32), ('eps', _c.c_float),
+                ('freqs', _p), ('q_gain', _p), ('k_gain', _p)]
+
+
 class GemmArgs(ctypes.Structure):
     _fields_ = [('struct_size', _c.c_uint32), ('epilogue', _c.c_int32), ('a', _p), ('lda', _c.c_int64),
                 ('b', _p), ('ldb', _c.c_int64), ('m', _c.c_int64), ('n', _c.c_int64), ('k', _c.c_int64),
@@ -41,7 +46,7 @@ class GemmArgs(ctypes.Structure):
                 ('bias_dtype', _c.c_int32), ('out_dtype', _c.c_int32), ('residual', _p),
                 ('ldr', _c.c_int64), ('gate', _p), ('gate_labels', _p), ('ldg', _c.c_int64), ('out', _p),
                 ('ldc', _c.c_int64), ('workspace', _p),
-                ('workspace_bytes', _c.c_int64), ('stream', _p)]
+                ('workspace_bytes', _c.c_int64), ('rope', ctypes.POINTER(RopeEpilogue)), ('stream', _p)]
 
 
 class DequantArgs(ctypes.Structure):

@@ -5,6 +5,8 @@ work is queued on the current stream of the tensors' device. Every wrapper
 checks device, dtype, shape and layout first and raises ValueError on a
 contract violation; a failing library call raises W8A8Error.
 """
+import ctypes
+
 import torch
 
 from . import _abi
@@ -171,7 +173,7 @@ def rms_rope(packed, freqs, q_gain, k_gain, *, heads, rot_dim, eps, dim=128, out
         return t if t.data_ptr() % 16 == 0 else t.clone()
     freqs = aligned(freqs.reshape(rows, rot_dim // 2, 2, 2))
     if packed.stride(0) * packed.element_size() % 16 or packed.data_ptr() % 16:
-        packed = packed.contiguous()
+        packed = packed[:, :2 * heads * dim].contiguous()   # Q and K only: 16-byte rows
     gq = aligned(q_gain.to(torch.float32).reshape(-1))
     gk = aligned(k_gain.to(torch.float32).reshape(-1))
     if gq.numel() != dim or gk.numel() != dim:
@@ -296,6 +298,31 @@ def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dty
 _WORKSPACE_BYTES = {}
 
 
+def _aligned16(t):
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _rope_epilogue(rope, m, device):
+    """RopeEpilogue struct of a gemm() rope dict, and the tensors it points to."""
+    heads, rot_dim = int(rope['heads']), int(rope['rot_dim'])
+    freqs = rope['freqs']
+    if freqs.dtype not in (torch.float16, torch.float32):
+        raise ValueError('frequencies must be float16 or float32')
+    if not (0 < rot_dim <= 128 and rot_dim % 2 == 0) or freqs.numel() != m * rot_dim * 2:
+        raise ValueError('rope needs an even rot_dim <= 128 and freqs [M, rot_dim/2, 2, 2]')
+    freqs = _aligned16(freqs.reshape(m, rot_dim // 2, 2, 2))
+    gq = _aligned16(rope['q_gain'].to(torch.float32).reshape(-1))
+    gk = _aligned16(rope['k_gain'].to(torch.float32).reshape(-1))
+    _device(freqs, gq, gk)
+    if freqs.device != device or gq.numel() != 128 or gk.numel() != 128:
+        raise ValueError('rope tensors must be on the operands\' device, with 128-entry gains')
+    args = _abi.RopeEpilogue(heads=heads, rot_dim=rot_dim, freq_dtype=_abi.DTYPE_CODE[freqs.dtype],
+                             eps=float(rope.get('eps', 1e-6)), freqs=freqs.data_ptr(), q_gain=gq.data_ptr(),
+                             k_gain=gk.data_ptr())
+    return args, (freqs, gq, gk)
+
+
 def gemm_workspace_bytes(m, n, k, device):
     """Split-K workspace bytes libw8a8 uses for an m x n x k GEMM on device
     (0 when the shape does not split); cached per shape and device."""
@@ -307,7 +334,7 @@ def gemm_workspace_bytes(m, n, k, device):
 
 
 def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=None, residual=None,
-         out_dtype=torch.float16, out=None, workspace=None, gate=None, gate_labels=None):
+         out_dtype=torch.float16, out=None, workspace=None, gate=None, gate_labels=None, rope=None):
     """C = q @ weight.T on i8 MFMA with a fused epilogue.
 
     q int8 [M, K], weight int8 [N, K]. epilogue EPI_INT32 -> int32 [M, N];
@@ -319,6 +346,12 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
     workspace: optional uint8 device tensor for split K; by default one of
     gemm_workspace_bytes() is allocated when the shape splits K (grids that
     would leave CUs idle). An empty tensor disables the split.
+    rope: RMS-RoPE epilogue of a packed QKV projection, a dict with 'heads',
+    'rot_dim', 'freqs' ([M, rot_dim/2, 2, 2] fp16/fp32), 'q_gain', 'k_gain'
+    ([128]) and 'eps': the first 2 * heads * 128 output columns (Q heads,
+    then K heads) are stored normalized and rotated, bit-identical to
+    rms_rope() of the plain FP16 output; needs FP16 output without bias,
+    residual or gate (K is never split).
     """
     q = _rows_2d(q)
     if weight.ndim != 2:
@@ -338,6 +371,11 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
                                        q.device, gate, gate_labels)
     if m == 0 or n == 0:
         return out
+    rope_args = None
+    if rope is not None:
+        rope_args, rope_keep = _rope_epilogue(rope, m, q.device)
+        keep = (keep, rope_keep)
+        workspace = torch.empty(0, dtype=torch.uint8, device=q.device)
     if workspace is None:
         nbytes = gemm_workspace_bytes(m, n, k, q.device)
         workspace = torch.empty(nbytes, dtype=torch.uint8, device=q.device) if nbytes else None
@@ -347,7 +385,8 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
     ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr else 0
     args = _abi.GemmArgs(epilogue=epilogue, a=q.data_ptr(), lda=q.stride(0), b=weight.data_ptr(),
                          ldb=weight.stride(0), m=m, n=n, k=k, out=out.data_ptr(), ldc=out.stride(0),
-                         workspace=ws_ptr, workspace_bytes=ws_bytes, stream=_abi.stream_of(q), **fields)
+                         workspace=ws_ptr, workspace_bytes=ws_bytes, stream=_abi.stream_of(q),
+                         rope=ctypes.pointer(rope_args) if rope_args is not None else None, **fields)
     _abi.call('w8a8_gemm', args)
     del keep, workspace
     return out

@@ -32,3 +32,41 @@ def execute(packed, freqs, q_gain, k_gain, *, heads=28, dim=128, epsilon=1e-6, o
     rot_dim = freqs.shape[-3] * 2
     return kernels.rms_rope(packed, freqs.reshape(packed.shape[0], rot_dim // 2, 2, 2), q_gain, k_gain,
                             heads=heads, rot_dim=rot_dim, eps=float(epsilon), dim=dim, out_dtype=out_dtype)
+
+
+def fused_qkv(x, weight, weight_scale, freqs, q_gain, k_gain, *, heads=28, dim=128, epsilon=1e-6, prepared=None,
+              convrot=True):
+    """The QKV projection followed by execute(), in one GEMM.
+
+    patches/tp_dit.py:286-300 (qkv_proj, the split into q, k, v, then
+    execute on the packed output) with the RMS-RoPE applied in the GEMM's
+    epilogue to the FP16 values the projection would have stored, so the
+    packed Q and K never make the round trip through HBM. x: [S, K] fp16
+    activation (or prepared = (codes, row_scale), the ConvRot256 INT8
+    activation of the fused modulated norm); weight int8 [3 * heads * dim, K]
+    with its per-channel scale; freqs (1, S, 1, half, 2, 2). Returns (q, k,
+    v), each a [S, heads, dim] view of the packed FP16 output; q and k equal
+    execute(qkv_proj(x), ...) bit for bit, v equals the projection's V.
+    """
+    if dim != 128:
+        raise ValueError('full 128-wide heads required')
+    if prepared is None:
+        codes, row_scale = kernels.quantize_rows(x.reshape(-1, x.shape[-1]), convrot=bool(convrot),
+                                                 round_rotated=True)
+    else:
+        codes, row_scale = prepared
+    rows = codes.shape[0]
+    if weight.ndim != 2 or weight.shape[0] != 3 * heads * dim:
+        raise ValueError('packed QKV weight of 3 * heads * dim rows required')
+    if not (freqs.ndim == 6 and tuple(freqs.shape[:3]) == (1, rows, 1) and tuple(freqs.shape[-2:]) == (2, 2)
+            and 0 < freqs.shape[-3] * 2 <= dim):
+        raise ValueError('Packed QKV/frequency layout required')
+    rot_dim = freqs.shape[-3] * 2
+    weight = weight.to(device=codes.device).contiguous()
+    scale = weight_scale.to(device=codes.device, dtype=torch.float32).reshape(-1)
+    rope = {'heads': heads, 'rot_dim': rot_dim, 'freqs': freqs.reshape(rows, rot_dim // 2, 2, 2),
+            'q_gain': q_gain, 'k_gain': k_gain, 'eps': float(epsilon)}
+    qkv = kernels.gemm(codes, weight, epilogue=kernels.EPI_COLUMN, row_scale=row_scale, col_scale=scale,
+                       out_dtype=torch.float16, rope=rope)
+    q, k, v = qkv.split(heads * dim, dim=-1)
+    return q.view(rows, heads, dim), k.view(rows, heads, dim), v.view(rows, heads, dim)

@@ -31,6 +31,9 @@ SHAPES = {
     # The QKV output of the c2 projection (53504 tokens, 3 x 24 heads of 128),
     # the H3 rotary prefix of 96 dims and fp16 rotation matrices.
     'dit_rms_rope': dict(seed=6, m=53504, heads=24, rot_dim=96),
+    # The c2 QKV projection (53504 tokens, 3072 -> 3 x 24 heads of 128, no
+    # bias) with the RMS-RoPE of its Q and K heads fused into the epilogue.
+    'dit_qkv_rope': dict(seed=7, m=53504, k=3072, heads=24, rot_dim=96, outliers=3),
     'dit_norm': dict(seed=5, m=16384, hidden=3072, mod_rows=9, frames=16, eps=1e-6 / RESIDUAL_DIVISOR ** 2),
 }
 
@@ -131,6 +134,21 @@ def dit_rms_rope(m=None, seed=None):
     q_gain = torch.rand(128, generator=g) + 0.5
     k_gain = torch.rand(128, generator=g) + 0.5
     return dict(packed=packed, freqs=freqs, q_gain=q_gain, k_gain=k_gain, heads=s['heads'], rot_dim=s['rot_dim'])
+
+
+def dit_qkv_rope(m=None, seed=None):
+    """fp16 activation, QKV weights [3 * heads * 128, k], fp16 rotation matrices, fp32 gains."""
+    s = SHAPES['dit_qkv_rope']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m = m or s['m']
+    x = activations(g, m, s['k'], s['outliers'])
+    w = weights(g, 3 * s['heads'] * 128, s['k'])
+    ang = torch.rand((m, s['rot_dim'] // 2), generator=g, dtype=torch.float64) * 6.283185307179586
+    c, sn = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack([torch.stack([c, -sn], -1), torch.stack([sn, c], -1)], -2).half()
+    q_gain = torch.rand(128, generator=g) + 0.5
+    k_gain = torch.rand(128, generator=g) + 0.5
+    return dict(x=x, w=w, freqs=freqs, q_gain=q_gain, k_gain=k_gain, heads=s['heads'], rot_dim=s['rot_dim'])
 
 
 def quantize_weight(w, device):

@@ -35,7 +35,8 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 184, 144, 144, 104]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 192, 144, 144, 104]
+    assert ctypes.sizeof(_abi.RopeEpilogue) == 40   # static_assert'ed in the library too
 
 
 def _expect_invalid(name, args, fragment):
@@ -76,6 +77,36 @@ def test_gemm_argument_checks():
     _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'k': 1 << 20, 'lda': 1 << 20, 'ldb': 1 << 20}),
                     'overflow')
     _expect_invalid('w8a8_gemm', _abi.GemmArgs(**{**base, 'a': 4100}), 'aligned')
+
+
+def test_gemm_rope_epilogue_checks():
+    lib = _abi.load()
+    rope = _abi.RopeEpilogue(heads=2, rot_dim=96, freq_dtype=_abi.F16, eps=1e-6, freqs=4096, q_gain=8192,
+                             k_gain=12288)
+    base = dict(struct_size=ctypes.sizeof(_abi.GemmArgs), epilogue=_abi.EPI_COLUMN, a=4096, lda=128, b=8192,
+                ldb=128, m=256, n=3 * 2 * 128, k=128, row_scale=64, col_scale=128, col_scale_stride=1,
+                out=16384, ldc=3 * 2 * 128, out_dtype=_abi.F16)
+
+    def call(rope_fields=None, **gemm_fields):
+        r = _abi.RopeEpilogue.from_buffer_copy(rope)
+        for key, value in (rope_fields or {}).items():
+            setattr(r, key, value)
+        args = _abi.GemmArgs(**{**base, **gemm_fields}, rope=ctypes.pointer(r))
+        return lib.w8a8_gemm(ctypes.byref(args)), lib.w8a8_last_error().decode()
+
+    rc, msg = call({'heads': 4})
+    assert rc == _abi.ERR_INVALID and 'heads' in msg
+    rc, msg = call({'rot_dim': 95})
+    assert rc == _abi.ERR_INVALID and 'rot_dim' in msg
+    rc, msg = call({'freq_dtype': _abi.BF16})
+    assert rc == _abi.ERR_INVALID and 'freq_dtype' in msg
+    rc, msg = call({'q_gain': 8200})
+    assert rc == _abi.ERR_INVALID and 'aligned' in msg
+    for rope_fields, gemm_fields in (({'rot_dim': 20}, {}), ({}, {'m': 64}), ({}, {'bias': 64, 'bias_dtype': _abi.F32}),
+                                     ({}, {'out_dtype': _abi.F32}), ({}, {'ldc': 3 * 2 * 128 + 4}),
+                                     ({}, {'k': 64, 'lda': 64, 'ldb': 64})):
+        rc, msg = call(rope_fields, **gemm_fields)
+        assert rc == _abi.ERR_UNSUPPORTED and 'rope epilogue' in msg, (rope_fields, gemm_fields, msg)
 
 
 def test_swiglu_argument_checks():
