@@ -596,7 +596,58 @@ def run_dit_qkv_rope(args, torch, dev):
     return res
 
 
-WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
+def run_dit_attention(args, torch, dev):
+    """INT8 attention of one DiT rank (53504 tokens, 24 heads of 128, fp16 in
+    and out): the preparation (key statistics, INT8 codes, V transposed) and
+    the attention kernel, timed separately. value = the attention kernel's
+    INT8 ops (4 N^2 D per head: Q.K^T and P.V) per second."""
+    from w8a8 import kernels, workloads
+    data = workloads.dit_attention()
+    q, k, v = (data[n].to(dev) for n in ('q', 'k', 'v'))
+    b, h, n, d = q.shape
+    state = {}
+
+    def prep():
+        state['p'] = kernels.attention_prepare(q, k, v)
+
+    prep()
+    out = torch.empty_like(q)
+
+    def attn():
+        return kernels.attention(state['p'], out_dtype=torch.float16, out=out)
+
+    tp = timed(torch, prep, args.steps, args.warmup)
+    ta = timed(torch, attn, args.steps, args.warmup)
+    ops = 4.0 * n * n * d * b * h
+    tops = ops / (ta * 1e-3) / 1e12
+    res = dict(metric='DiT INT8 attention 53504 tokens x 24 heads TOPS', value=round(tops, 1), unit='TOPS',
+               higher_is_better=True, dtype='int8', data='synthetic',
+               config=dict(workload='dit_attention', tokens=n, heads=h, head_dim=d),
+               ms_per_step=round(ta + tp, 3),
+               roofline=dict(bound='mfma', achieved=round(tops, 1), peak=PEAK_INT8_TOPS, unit='TFLOP/s',
+                             frac=round(tops / PEAK_INT8_TOPS, 4), traffic=None,
+                             kernel='attention_kernel<1> (128 queries x 64-key blocks per workgroup)',
+                             algorithmic=f'{ops:.4g} int8 ops per launch (4 N^2 D H)'),
+               kernels=dict(prepare_us=round(tp * 1e3, 1), attention_us=round(ta * 1e3, 1)))
+    if not args.no_cpu_baseline:
+        import numpy as np
+        import oracle as o
+        from oracle import int8_attention as oa
+        rows = 32
+        qn, kn, vn = (data[t][:, :1].float().numpy() for t in ('q', 'k', 'v'))
+
+        def cpu():
+            pr = oa.prepare(qn[:, :, :rows], kn, vn)
+            return oa.attention(pr)
+
+        tc = _cpu_rows_timing(cpu, reps=1) * (n / rows) * h
+        res['cpu_baseline'] = dict(value=round(ops / tc / 1e12, 6), unit='TOPS', cores=blas_threads(), kind='port',
+                                   sample=f'oracle prepare + attention for {rows} queries of 1 head against all '
+                                          f'{n} keys, scaled x{n / rows * h:g}')
+    return res
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_attention': run_dit_attention, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
              'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv, 'dit_qkv_rope': run_dit_qkv_rope,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
 

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 6
+#define W8A8_ABI_VERSION 7
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -226,6 +226,76 @@ typedef struct W8A8RmsRopeArgs {
 int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
 
 /*
+ * INT8 attention for 128-wide heads, in two calls like the reference's
+ * prepared Kitchen route (patches/h3_operator_policy.py:173-209:
+ * ck.prequantize_int8_attention, then ck.int8_attention_from_prequantized;
+ * patches/kitchen_attention.py:227-238 int8_attention; the native launcher
+ * patches/kitchen_attention_native/attention.cu:20-101 h3_attention, whose
+ * vendored kernel is not part of the reference). The numerics are this
+ * library's own SageAttention-style scheme; they match the reference's only
+ * approximately:
+ *   prepare: k is centred per channel (mean over the keys; softmax-invariant);
+ *     q rows get per-token scales (stored multiplied by sm_scale * log2(e)),
+ *     k one scale per 64-key block, v one scale per channel; INT8 codes
+ *     sat(rne(x / s)) with s = max(amax * fp32(1/127), 1e-30). v is written
+ *     transposed: vt8[c][64 j + 32 u + p] holds key 64 j + 32 u + 8 g + 4 h + i
+ *     of channel c for p = 16 h + 4 g + i.
+ *   attention: per query and 64-key block, S = q8.k8 (int32), fp32 online
+ *     softmax in the exp2 domain with the hardware exp2, probabilities
+ *     rounded to integers 0..127, P.v8 in int32, output
+ *     (acc * vs[c]) / sum of probabilities.
+ * q, k, v: [b, h, nq|nk, d] contiguous; d == 128.
+ */
+typedef struct W8A8AttnPrepareArgs {
+  uint32_t struct_size;
+  int32_t in_dtype;        /* W8A8_F16 or W8A8_F32 */
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t b;
+  int64_t h;
+  int64_t nq;
+  int64_t nk;
+  int32_t d;
+  float sm_scale;          /* > 0; the reference's default is 1/sqrt(d) */
+  int8_t* q8;              /* [b, h, nq, d] */
+  float* qs;               /* [b, h, nq] */
+  int8_t* k8;              /* [b, h, nkp, d], nkp = 64 * ceil(nk / 64) */
+  float* ks;               /* [b, h, nkp / 64] */
+  int8_t* vt8;             /* [b, h, d, nkp] */
+  float* vs;               /* [b, h, d] */
+  void* workspace;         /* w8a8_attention_workspace_size(b, h, nk) bytes */
+  int64_t workspace_bytes;
+  void* stream;
+} W8A8AttnPrepareArgs;
+
+int w8a8_attention_prepare(const W8A8AttnPrepareArgs* args);
+
+/* Scratch bytes w8a8_attention_prepare needs (key statistics). */
+int64_t w8a8_attention_workspace_size(int64_t b, int64_t h, int64_t nk);
+
+typedef struct W8A8AttentionArgs {
+  uint32_t struct_size;
+  int32_t out_dtype;       /* W8A8_F16 or W8A8_F32 */
+  const int8_t* q8;
+  const float* qs;
+  const int8_t* k8;
+  const float* ks;
+  const int8_t* vt8;
+  const float* vs;
+  int64_t b;
+  int64_t h;
+  int64_t nq;
+  int64_t nk;
+  int32_t d;
+  int32_t reserved;
+  void* out;               /* [b, h, nq, d] of out_dtype */
+  void* stream;
+} W8A8AttentionArgs;
+
+int w8a8_attention(const W8A8AttentionArgs* args);
+
+/*
  * INT8 GEMM on gfx950 i8 MFMA with a fused epilogue.
  * Replaces: patches/parallel_int8.py:46-50 (int_mm),
  *           patches/optimized_tp.py:34-43 (native_int_mm),
@@ -359,7 +429,8 @@ int w8a8_dequantize(const W8A8DequantArgs* args);
 int w8a8_abi_version(void);
 
 /* sizeof of each argument struct, by index: 0 Quant, 1 Swiglu, 2 Gemm,
- * 3 Dequant, 4 Norm, 5 RmsRope; -1 for an unknown index. Lets bindings verify their layout. */
+ * 3 Dequant, 4 Norm, 5 RmsRope, 6 AttnPrepare, 7 Attention; -1 for an
+ * unknown index. Lets bindings verify their layout. */
 int64_t w8a8_struct_size(int32_t which);
 
 /* Message describing the last error returned on the calling thread. */

@@ -24,6 +24,8 @@ static_assert(sizeof(W8A8RopeEpilogue) == 40, "W8A8RopeEpilogue layout");
 static_assert(sizeof(W8A8DequantArgs) == 144, "W8A8DequantArgs layout");
 static_assert(sizeof(W8A8NormArgs) == 144, "W8A8NormArgs layout");
 static_assert(sizeof(W8A8RmsRopeArgs) == 104, "W8A8RmsRopeArgs layout");
+static_assert(sizeof(W8A8AttnPrepareArgs) == 144, "W8A8AttnPrepareArgs layout");
+static_assert(sizeof(W8A8AttentionArgs) == 112, "W8A8AttentionArgs layout");
 
 extern "C" int w8a8_abi_version(void) { return W8A8_ABI_VERSION; }
 
@@ -35,6 +37,8 @@ extern "C" int64_t w8a8_struct_size(int32_t which) {
     case 3: return (int64_t)sizeof(W8A8DequantArgs);
     case 4: return (int64_t)sizeof(W8A8NormArgs);
     case 5: return (int64_t)sizeof(W8A8RmsRopeArgs);
+    case 6: return (int64_t)sizeof(W8A8AttnPrepareArgs);
+    case 7: return (int64_t)sizeof(W8A8AttentionArgs);
     default: return -1;
   }
 }

@@ -1,0 +1,487 @@
+// INT8 attention for 128-wide heads: the preparation of the INT8 operands
+// (key centering, per-token Q scales, per-64-key K scales, per-channel V
+// scales, V transposed) and the attention kernel (S = Q.K^T on INT8 MFMA,
+// exp2-domain online softmax in fp32, probabilities quantized to 0..127 for
+// an INT8 MFMA P.V product, with the denominator as the sum of the same
+// integer probabilities). The exponentials use the hardware exp2
+// (v_exp_f32).
+//
+// Layout of the attention kernel: a workgroup of four wavefronts takes 128
+// queries of one (batch, head); a wavefront owns 32 of them. Keys come in
+// blocks of 64 through a two-stage LDS ring (K tile 64 x 128 bytes, V^T tile
+// 128 x 64 bytes). The score tile is computed transposed, S^T = K.Q^T, so a
+// lane holds one query (lane % 32) and 16 of every 32 keys: the softmax
+// statistics of a query need one exchange with the lane 32 away, and the
+// quantized probabilities are already the B operand of O^T = V^T.P^T. Its K
+// positions follow the order in which the score layout hands out the keys,
+// so the preparation writes V^T with the same order inside each 32-key
+// group (position 16 h + 4 g + i holds key 8 g + 4 h + i).
+#include "w8a8_device.h"
+#include "w8a8_host.h"
+
+#include <type_traits>
+
+namespace w8a8 {
+
+constexpr int kAttnD = 128;       // head dimension
+constexpr int kAttnBK = 64;       // keys per block
+constexpr int kAttnChunk = 256;   // tokens per partial of the key statistics
+constexpr int kAttnWaveQ = 32;    // queries per wavefront
+constexpr int kAttnBQ = 128;      // queries per workgroup
+constexpr float kLog2e = 0x1.715476p+0f;    // fp32(log2(e))
+constexpr float kLog2_127 = 0x1.bf469cp+2f; // fp32(log2(127))
+constexpr float kRneMagic = 12582912.0f;    // 1.5 * 2^23
+
+struct AttnPrepParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  int nq, nk, nkp, nblk, chunks;
+  float c0;   // fp32(sm_scale * log2(e))
+  int8_t* q8;
+  float* qs;
+  int8_t* k8;
+  float* ks;
+  int8_t* vt8;
+  float* vs;
+  float* part_sum;
+  float* part_max;
+  float* kmean;
+};
+
+template <int DT>
+__device__ __forceinline__ float ld1(const void* base, int64_t i) {
+  if constexpr (DT == kF32) return reinterpret_cast<const float*>(base)[i];
+  else return h2f(reinterpret_cast<const uint16_t*>(base)[i]);
+}
+
+// Partial statistics of 256 keys of one (batch, head): the fp32 sum of k
+// (sequential from +0) and the absmax of v, per channel (thread = channel).
+template <int DT>
+__global__ __launch_bounds__(128) void attn_stats_kernel(AttnPrepParams p) {
+  const int d = threadIdx.x, chunk = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int t0 = chunk * kAttnChunk, t1 = min(t0 + kAttnChunk, p.nk);
+  const int64_t base = bh * (int64_t)p.nk * kAttnD + d;
+  float s = 0.0f, m = 0.0f;
+  for (int t = t0; t < t1; ++t) {
+    s = s + ld1<DT>(p.k, base + (int64_t)t * kAttnD);
+    m = fmaxf(m, fabsf(ld1<DT>(p.v, base + (int64_t)t * kAttnD)));
+  }
+  const int64_t o = (bh * p.chunks + chunk) * kAttnD + d;
+  p.part_sum[o] = s;
+  p.part_max[o] = m;
+}
+
+// Key mean (the partials added in chunk order, then one division by Nk) and
+// the per-channel V scale.
+__global__ __launch_bounds__(128) void attn_finalize_kernel(AttnPrepParams p) {
+  const int d = threadIdx.x;
+  const int64_t bh = blockIdx.x;
+  float s = 0.0f, m = 0.0f;
+  for (int c = 0; c < p.chunks; ++c) {
+    const int64_t o = (bh * p.chunks + c) * kAttnD + d;
+    s = s + p.part_sum[o];
+    m = fmaxf(m, p.part_max[o]);
+  }
+  p.kmean[bh * kAttnD + d] = s / (float)p.nk;
+  p.vs[bh * kAttnD + d] = row_scale_of(m);
+}
+
+// 32 consecutive channels [32 part, 32 part + 32) of token t (16-byte loads).
+template <int DT>
+__device__ __forceinline__ void load32(const void* base, int64_t off, float (&x)[32]) {
+  float a[16], b[16];
+  if constexpr (DT == kF32) {
+    load16<kF32>(reinterpret_cast<const float*>(base) + off, a);
+    load16<kF32>(reinterpret_cast<const float*>(base) + off + 16, b);
+  } else {
+    load16<kF16>(reinterpret_cast<const uint16_t*>(base) + off, a);
+    load16<kF16>(reinterpret_cast<const uint16_t*>(base) + off + 16, b);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    x[i] = a[i];
+    x[16 + i] = b[i];
+  }
+}
+
+__device__ __forceinline__ void store32_i8(int8_t* dst, const int (&q)[32]) {
+  uint4 w[2];
+  uint32_t* u = reinterpret_cast<uint32_t*>(w);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) u[i] = pack4(q[4 * i], q[4 * i + 1], q[4 * i + 2], q[4 * i + 3]);
+  reinterpret_cast<uint4*>(dst)[0] = w[0];
+  reinterpret_cast<uint4*>(dst)[1] = w[1];
+}
+
+// Block blk of 64 tokens of one (batch, head): thread (token tid / 4, part
+// tid % 4) handles 32 channels. Q rows get their own scale; K rows are
+// centred and share one scale per block; V is quantized with the channel
+// scales and written transposed (through LDS) in the permuted key order.
+template <int DT>
+__global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
+  __shared__ __attribute__((aligned(16))) int8_t vtile[kAttnBK * kAttnD];
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x, tl = tid >> 2, part = tid & 3;
+  const int blk = blockIdx.x;
+  const int64_t bh = blockIdx.y;
+  const int t = blk * kAttnBK + tl;
+  const int c0 = 32 * part;
+  if (blk * kAttnBK < p.nq) {   // workgroup-uniform
+    const bool valid = t < p.nq;
+    float x[32];
+    if (valid) load32<DT>(p.q, (bh * p.nq + t) * kAttnD + c0, x);
+    else
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    const float s = row_scale_of(amax), rcp = 1.0f / s;
+    int q[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) q[i] = quant1(x[i], s, rcp);
+    if (valid) {
+      store32_i8(p.q8 + (bh * p.nq + t) * kAttnD + c0, q);
+      if (part == 0) p.qs[bh * p.nq + t] = s * p.c0;
+    }
+  }
+  if (blk < p.nblk) {   // workgroup-uniform
+    const bool valid = t < p.nk;
+    const float* mean = p.kmean + bh * kAttnD + c0;
+    float x[32];
+    if (valid) {
+      load32<DT>(p.k, (bh * p.nk + t) * kAttnD + c0, x);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = x[i] - mean[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) wmax[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float s = row_scale_of(amax), rcp = 1.0f / s;
+    int q[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) q[i] = quant1(x[i], s, rcp);
+    store32_i8(p.k8 + (bh * p.nkp + t) * kAttnD + c0, q);
+    if (tid == 0) p.ks[bh * p.nblk + blk] = s;
+    // V: channel scales, then the tile goes through LDS to be transposed.
+    const float* vsc = p.vs + bh * kAttnD + c0;
+    if (valid) load32<DT>(p.v, (bh * p.nk + t) * kAttnD + c0, x);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float sv = vsc[i];
+      q[i] = valid ? quant1(x[i], sv, 1.0f / sv) : 0;
+    }
+    store32_i8(vtile + tl * kAttnD + c0, q);
+    __syncthreads();
+    // Thread (channel ch, 32-key group gq) writes 32 bytes of V^T row ch.
+    const int ch = tid >> 1, gq = tid & 1;
+    int vb[32];
+#pragma unroll
+    for (int pos = 0; pos < 32; ++pos) {
+      const int key = 8 * ((pos >> 2) & 3) + 4 * (pos >> 4) + (pos & 3);
+      vb[pos] = vtile[(32 * gq + key) * kAttnD + ch];
+    }
+    store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * gq, vb);
+  }
+}
+
+struct AttnParams {
+  const int8_t* q8;
+  const float* qs;
+  const int8_t* k8;
+  const float* ks;
+  const int8_t* vt8;
+  const float* vs;
+  void* out;
+  int nq, nk, nkp, nblk;
+};
+
+template <int OUT>
+__global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
+  // Three-stage ring of [0: K tile, 64 keys x 128 bytes; 1: V^T tile, 128
+  // channels x 64 bytes]. Iteration j reads K of block j + 1 (its scores are
+  // issued before block j's softmax, so the MFMAs run under it) and V of
+  // block j, and fills the stage of block j + 2.
+  __shared__ __attribute__((aligned(16))) int8_t lds[3][2][kAttnBK * kAttnD];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 31, hh = lane >> 5;
+  const int64_t bh = blockIdx.y;
+  const int q0 = blockIdx.x * kAttnBQ + wave * kAttnWaveQ;
+  const int qrow = min(q0 + fr, p.nq - 1);
+  const int8_t* k8 = p.k8 + bh * (int64_t)p.nkp * kAttnD;
+  const int8_t* vt8 = p.vt8 + bh * (int64_t)kAttnD * p.nkp;
+  // Q fragments (B operand of S^T = K.Q^T): query fr, channels 32 ds + 16 hh + [0, 16).
+  v4i qf[4];
+  {
+    const int8_t* qp = p.q8 + (bh * p.nq + qrow) * kAttnD + 16 * hh;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + 32 * ds);
+  }
+  const float qscale = p.qs[bh * p.nq + qrow];
+  // Thread tid moves 16-byte chunks tid and tid + 256 of both tiles: K row
+  // r = idx / 8, chunk idx % 8 (stored at chunk ^ ((r >> 1) & 7)); V^T row
+  // idx / 4, chunk idx % 4 (stored at chunk ^ ((row >> 2) & 3)). The
+  // swizzles keep the fragment reads (32 rows, one chunk column) free of
+  // bank conflicts.
+  auto load_tiles = [&](int j, v4i (&kr)[2], v4i (&vr)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = tid + 256 * u;
+      kr[u] = *reinterpret_cast<const v4i*>(k8 + (int64_t)(kAttnBK * j + (idx >> 3)) * kAttnD + 16 * (idx & 7));
+      vr[u] = *reinterpret_cast<const v4i*>(vt8 + (int64_t)(idx >> 2) * p.nkp + kAttnBK * j + 16 * (idx & 3));
+    }
+  };
+  auto store_tiles = [&](int st, const v4i (&kr)[2], const v4i (&vr)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int idx = tid + 256 * u;
+      const int r = idx >> 3, c = idx & 7, ch = idx >> 2, s = idx & 3;
+      *reinterpret_cast<v4i*>(lds[st][0] + r * kAttnD + ((c ^ ((r >> 1) & 7)) << 4)) = kr[u];
+      *reinterpret_cast<v4i*>(lds[st][1] + ch * kAttnBK + ((s ^ ((ch >> 2) & 3)) << 4)) = vr[u];
+    }
+  };
+  // S^T of the block in stage st: sacc[t][4 g + i] is the score of key
+  // 32 t + 8 g + 4 hh + i of the block for query fr.
+  auto scores = [&](int st, v16i (&sacc)[2]) {
+    sacc[0] = v16i{};
+    sacc[1] = v16i{};
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) {
+        const int r = 32 * t + fr, ck = 2 * ds + hh;
+        const v4i kf = *reinterpret_cast<const v4i*>(lds[st][0] + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
+        sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
+      }
+  };
+  v4i kr[2], vr[2];
+  load_tiles(0, kr, vr);
+  store_tiles(0, kr, vr);
+  if (p.nblk > 1) {
+    load_tiles(1, kr, vr);
+    store_tiles(1, kr, vr);
+  }
+  __syncthreads();
+  v16i sc[2];
+  scores(0, sc);
+  float m = -__builtin_inff();
+  // Output and denominator: fp32 parts plus integer parts accumulated since
+  // the last change of the running maximum.
+  float of[4][16], lf = 0.0f;
+  v16i oi[4];
+  int li = 0;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    oi[ct] = v16i{};
+#pragma unroll
+    for (int x = 0; x < 16; ++x) of[ct][x] = 0.0f;
+  }
+  const float* ksc = p.ks + bh * p.nblk;
+  // Softmax of one block: quantized probabilities (packed as the B operand
+  // of the P.V product), their integer sum and the new maximum. TAIL masks
+  // the keys past nk (last block only).
+  auto softmax = [&](auto tail_tag, int j, const v16i (&s)[2], uint32_t (&pw)[2][4], int& psum, float& mnew,
+                     float& alpha) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    int sv[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        sv[t][x] = s[t][x];
+        if constexpr (TAIL) {
+          if (kAttnBK * j + 32 * t + 8 * (x >> 2) + 4 * hh + (x & 3) >= p.nk) sv[t][x] = INT32_MIN;
+        }
+      }
+    int mx = sv[0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) mx = max(mx, sv[t][x]);
+    mx = max(mx, __shfl_xor(mx, 32, 64));
+    const float c = qscale * ksc[j];
+    mnew = fmaxf(m, (float)mx * c);
+    alpha = __builtin_amdgcn_exp2f(m - mnew);
+    // log2(127) - mnew, lowered by |mnew| 2^-22 so that the largest
+    // exponent cannot pass log2(127) by more than a few ulps (P <= 127).
+    const float nm = (kLog2_127 - mnew) - fabsf(mnew) * 0x1p-22f;
+    psum = 0;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        int b4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float qv = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sv[t][4 * g + i], c, nm));
+          // rne(qv) for 0 <= qv < 2^22: the low bits of qv + 1.5 * 2^23.
+          b4[i] = __builtin_bit_cast(int, qv + kRneMagic);
+          if constexpr (TAIL) {
+            if (sv[t][4 * g + i] == INT32_MIN) b4[i] = 0;
+          }
+        }
+        pw[t][g] = pack4(b4[0], b4[1], b4[2], b4[3]);
+        psum = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, psum, false);
+      }
+  };
+  for (int j = 0; j < p.nblk; ++j) {
+    const int st = j % 3;
+    const bool has1 = j + 1 < p.nblk, has2 = j + 2 < p.nblk;
+    if (has2) load_tiles(j + 2, kr, vr);
+    v16i sn[2];
+    if (has1) scores(st == 2 ? 0 : st + 1, sn);
+    uint32_t pw[2][4];
+    int psum;
+    float mnew, alpha;
+    if (kAttnBK * (j + 1) > p.nk) softmax(std::true_type{}, j, sc, pw, psum, mnew, alpha);
+    else softmax(std::false_type{}, j, sc, pw, psum, mnew, alpha);
+    // A new maximum for any query of the wavefront folds the integer parts
+    // into the fp32 ones with the rescale.
+    if (__any(alpha != 1.0f)) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          of[ct][x] = (of[ct][x] + (float)oi[ct][x]) * alpha;
+          oi[ct][x] = 0;
+        }
+      lf = (lf + (float)li) * alpha;
+      li = 0;
+    }
+    li += psum;
+    m = mnew;
+    // O^T += V^T.P^T (channels 32 ct + rows of the MFMA layout x queries).
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const v4i pf = {(int)pw[t][0], (int)pw[t][1], (int)pw[t][2], (int)pw[t][3]};
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int r = 32 * ct + fr, ck = 2 * t + hh;
+        const v4i vf = *reinterpret_cast<const v4i*>(lds[st][1] + r * kAttnBK + ((ck ^ ((r >> 2) & 3)) << 4));
+        oi[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, oi[ct], 0, 0, 0);
+      }
+    }
+    if (has2) store_tiles(st == 0 ? 2 : st - 1, kr, vr);
+    __syncthreads();
+    if (has1) {
+      sc[0] = sn[0];
+      sc[1] = sn[1];
+    }
+  }
+  lf = lf + (float)li;
+  const float l = lf + __shfl_xor(lf, 32, 64);
+  if (q0 + fr >= p.nq) return;
+  const int64_t orow = (bh * p.nq + q0 + fr) * kAttnD;
+  const float* vsc = p.vs + bh * kAttnD;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = 32 * ct + 8 * g + 4 * hh;
+      const float4 s4 = *reinterpret_cast<const float4*>(vsc + c0);
+      const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float o = of[ct][4 * g + i] + (float)oi[ct][4 * g + i];
+        y[i] = (o * sv[i]) / l;
+      }
+      if constexpr (OUT == kF32) {
+        *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + c0) = make_float4(y[0], y[1], y[2], y[3]);
+      } else {
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + orow + c0) =
+            make_uint2(f2h2_of_f32(y[0], y[1]), f2h2_of_f32(y[2], y[3]));
+      }
+    }
+}
+
+static int64_t attn_chunks(int64_t nk) { return (nk + kAttnChunk - 1) / kAttnChunk; }
+
+}  // namespace w8a8
+
+extern "C" int64_t w8a8_attention_workspace_size(int64_t b, int64_t h, int64_t nk) {
+  using namespace w8a8;
+  if (b <= 0 || h <= 0 || nk <= 0) return 0;
+  return b * h * (2 * attn_chunks(nk) + 1) * kAttnD * (int64_t)sizeof(float);
+}
+
+extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_attention_prepare: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8AttnPrepareArgs), "w8a8_attention_prepare: struct_size %u != %zu",
+               a->struct_size, sizeof(W8A8AttnPrepareArgs));
+  W8A8_REQUIRE(a->in_dtype == W8A8_F16 || a->in_dtype == W8A8_F32, "w8a8_attention_prepare: in_dtype not F16/F32");
+  W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention_prepare: head dimension %d != 128", a->d);
+  W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention_prepare: empty problem");
+  W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536,
+               "w8a8_attention_prepare: sizes out of range");
+  W8A8_REQUIRE(a->q && a->k && a->v && a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->workspace,
+               "w8a8_attention_prepare: null buffer");
+  W8A8_REQUIRE(aligned16(a->q) && aligned16(a->k) && aligned16(a->v) && aligned16(a->q8) && aligned16(a->k8) &&
+                   aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->workspace),
+               "w8a8_attention_prepare: tensors must be 16-byte aligned");
+  W8A8_REQUIRE(a->workspace_bytes >= w8a8_attention_workspace_size(a->b, a->h, a->nk),
+               "w8a8_attention_prepare: workspace below w8a8_attention_workspace_size()");
+  W8A8_REQUIRE(a->sm_scale > 0.0f, "w8a8_attention_prepare: sm_scale must be positive");
+  AttnPrepParams p;
+  p.q = a->q; p.k = a->k; p.v = a->v;
+  p.nq = (int)a->nq; p.nk = (int)a->nk;
+  p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);
+  p.nkp = p.nblk * kAttnBK;
+  p.chunks = (int)attn_chunks(a->nk);
+  p.c0 = a->sm_scale * kLog2e;
+  p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs;
+  const int64_t bh = a->b * a->h;
+  float* ws = reinterpret_cast<float*>(a->workspace);
+  p.part_sum = ws;
+  p.part_max = ws + bh * p.chunks * kAttnD;
+  p.kmean = ws + 2 * bh * p.chunks * kAttnD;
+  hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
+  const int qblocks = (p.nq + kAttnBK - 1) / kAttnBK;
+  const dim3 gstat((unsigned)p.chunks, (unsigned)bh), gq((unsigned)max(qblocks, p.nblk), (unsigned)bh);
+  if (a->in_dtype == W8A8_F16) {
+    hipLaunchKernelGGL(attn_stats_kernel<kF16>, gstat, dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_finalize_kernel, dim3((unsigned)bh), dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_quant_kernel<kF16>, gq, dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL(attn_stats_kernel<kF32>, gstat, dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_finalize_kernel, dim3((unsigned)bh), dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_quant_kernel<kF32>, gq, dim3(256), 0, s, p);
+  }
+  return launch_status("w8a8_attention_prepare");
+}
+
+extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_attention: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8AttentionArgs), "w8a8_attention: struct_size %u != %zu",
+               a->struct_size, sizeof(W8A8AttentionArgs));
+  W8A8_REQUIRE(a->out_dtype == W8A8_F16 || a->out_dtype == W8A8_F32, "w8a8_attention: out_dtype not F16/F32");
+  W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention: head dimension %d != 128", a->d);
+  W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention: empty problem");
+  W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536, "w8a8_attention: sizes out of range");
+  W8A8_REQUIRE(a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->out, "w8a8_attention: null buffer");
+  W8A8_REQUIRE(aligned16(a->q8) && aligned16(a->k8) && aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->out),
+               "w8a8_attention: tensors must be 16-byte aligned");
+  AttnParams p;
+  p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs; p.out = a->out;
+  p.nq = (int)a->nq; p.nk = (int)a->nk;
+  p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);
+  p.nkp = p.nblk * kAttnBK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
+  const dim3 grid((unsigned)((p.nq + kAttnBQ - 1) / kAttnBQ), (unsigned)(a->b * a->h));
+  if (a->out_dtype == W8A8_F32) hipLaunchKernelGGL(attention_kernel<kF32>, grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL(attention_kernel<kF16>, grid, dim3(256), 0, s, p);
+  return launch_status("w8a8_attention");
+}

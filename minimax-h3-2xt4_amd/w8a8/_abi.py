@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -72,12 +72,25 @@ class RmsRopeArgs(ctypes.Structure):
                 ('out_dtype', _c.c_int32), ('q_out', _p), ('k_out', _p), ('stream', _p)]
 
 
+class AttnPrepareArgs(ctypes.Structure):
+    _fields_ = [('struct_size', _c.c_uint32), ('in_dtype', _c.c_int32), ('q', _p), ('k', _p), ('v', _p),
+                ('b', _c.c_int64), ('h', _c.c_int64), ('nq', _c.c_int64), ('nk', _c.c_int64), ('d', _c.c_int32),
+                ('sm_scale', _c.c_float), ('q8', _p), ('qs', _p), ('k8', _p), ('ks', _p), ('vt8', _p), ('vs', _p),
+                ('workspace', _p), ('workspace_bytes', _c.c_int64), ('stream', _p)]
+
+
+class AttentionArgs(ctypes.Structure):
+    _fields_ = [('struct_size', _c.c_uint32), ('out_dtype', _c.c_int32), ('q8', _p), ('qs', _p), ('k8', _p),
+                ('ks', _p), ('vt8', _p), ('vs', _p), ('b', _c.c_int64), ('h', _c.c_int64), ('nq', _c.c_int64),
+                ('nk', _c.c_int64), ('d', _c.c_int32), ('reserved', _c.c_int32), ('out', _p), ('stream', _p)]
+
+
 # Argument structs in w8a8_struct_size() index order, with their entry points.
-STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs, NormArgs, RmsRopeArgs)
+STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs, NormArgs, RmsRopeArgs, AttnPrepareArgs, AttentionArgs)
 STRUCT_ENTRY_POINTS = ('w8a8_quantize_rows', 'w8a8_swiglu_quantize', 'w8a8_gemm', 'w8a8_dequantize',
-                       'w8a8_norm_quantize', 'w8a8_rms_rope')
+                       'w8a8_norm_quantize', 'w8a8_rms_rope', 'w8a8_attention_prepare', 'w8a8_attention')
 ENTRY_POINTS = STRUCT_ENTRY_POINTS + ('w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error',
-                                      'w8a8_gemm_workspace_size')
+                                      'w8a8_gemm_workspace_size', 'w8a8_attention_workspace_size')
 
 _LIB = None
 
@@ -106,6 +119,8 @@ def load(path=None):
     lib.w8a8_last_error.restype = _c.c_char_p
     lib.w8a8_gemm_workspace_size.restype = _c.c_int64
     lib.w8a8_gemm_workspace_size.argtypes = [_c.c_int64, _c.c_int64, _c.c_int64]
+    lib.w8a8_attention_workspace_size.restype = _c.c_int64
+    lib.w8a8_attention_workspace_size.argtypes = [_c.c_int64, _c.c_int64, _c.c_int64]
     for name, st in zip(STRUCT_ENTRY_POINTS, STRUCTS):
         fn = getattr(lib, name)
         fn.restype = _c.c_int

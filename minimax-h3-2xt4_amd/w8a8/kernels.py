@@ -411,3 +411,64 @@ def dequantize(acc, row_scale, col_scale, *, epilogue=EPI_ROW, out_dtype=torch.f
     _abi.call('w8a8_dequantize', args)
     del keep
     return out
+
+
+ATTN_BLOCK_K = 64
+
+
+def attention_prepare(q, k, v, *, sm_scale=None):
+    """INT8 operands of the attention for q [B, H, Nq, 128], k, v [B, H, Nk,
+    128] (fp16 or fp32, contiguous after this call). Returns a dict with q8,
+    qs, k8, ks, vt8, vs (device tensors) and the shape."""
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError('q, k, v must be [batch, heads, tokens, dim]')
+    _device(q, k, v)
+    b, h, nq, d = q.shape
+    if k.shape != v.shape or k.shape[:2] != (b, h) or k.shape[3] != d:
+        raise ValueError('q, k, v must share batch, heads and dim; k and v their shape')
+    if d != 128:
+        raise ValueError('INT8 attention supports 128-wide heads')
+    if q.dtype not in (torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError('q, k, v must all be float16 or all float32')
+    nk = k.shape[2]
+    if nq == 0 or nk == 0 or b * h == 0:
+        raise ValueError('empty attention')
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    scale = float(d ** -0.5 if sm_scale is None else sm_scale)
+    nkp = -(-nk // ATTN_BLOCK_K) * ATTN_BLOCK_K
+    dev = q.device
+    prep = dict(q8=torch.empty((b, h, nq, d), dtype=torch.int8, device=dev),
+                qs=torch.empty((b, h, nq), dtype=torch.float32, device=dev),
+                k8=torch.empty((b, h, nkp, d), dtype=torch.int8, device=dev),
+                ks=torch.empty((b, h, nkp // ATTN_BLOCK_K), dtype=torch.float32, device=dev),
+                vt8=torch.empty((b, h, d, nkp), dtype=torch.int8, device=dev),
+                vs=torch.empty((b, h, d), dtype=torch.float32, device=dev),
+                shape=(b, h, nq, nk, d))
+    with torch.cuda.device(dev):
+        nbytes = int(_abi.load().w8a8_attention_workspace_size(b, h, nk))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    args = _abi.AttnPrepareArgs(in_dtype=_abi.DTYPE_CODE[q.dtype], q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
+                                b=b, h=h, nq=nq, nk=nk, d=d, sm_scale=scale,
+                                q8=prep['q8'].data_ptr(), qs=prep['qs'].data_ptr(), k8=prep['k8'].data_ptr(),
+                                ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(), vs=prep['vs'].data_ptr(),
+                                workspace=ws.data_ptr(), workspace_bytes=nbytes, stream=_abi.stream_of(q))
+    _abi.call('w8a8_attention_prepare', args)
+    return prep
+
+
+def attention(prep, *, out_dtype=torch.float16, out=None):
+    """Attention output [B, H, Nq, 128] from attention_prepare()'s operands."""
+    b, h, nq, nk, d = prep['shape']
+    if out_dtype not in (torch.float16, torch.float32):
+        raise ValueError('output must be float16 or float32')
+    q8 = prep['q8']
+    if out is None:
+        out = torch.empty((b, h, nq, d), dtype=out_dtype, device=q8.device)
+    elif out.shape != (b, h, nq, d) or out.dtype != out_dtype or not out.is_contiguous():
+        raise ValueError('out must be a contiguous [B, H, Nq, D] tensor of out_dtype')
+    args = _abi.AttentionArgs(out_dtype=_abi.DTYPE_CODE[out_dtype], q8=q8.data_ptr(), qs=prep['qs'].data_ptr(),
+                              k8=prep['k8'].data_ptr(), ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(),
+                              vs=prep['vs'].data_ptr(), b=b, h=h, nq=nq, nk=nk, d=d, out=out.data_ptr(),
+                              stream=_abi.stream_of(q8))
+    _abi.call('w8a8_attention', args)
+    return out

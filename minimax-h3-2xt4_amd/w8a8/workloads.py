@@ -34,6 +34,8 @@ SHAPES = {
     # The c2 QKV projection (53504 tokens, 3072 -> 3 x 24 heads of 128, no
     # bias) with the RMS-RoPE of its Q and K heads fused into the epilogue.
     'dit_qkv_rope': dict(seed=7, m=53504, k=3072, heads=24, rot_dim=96, outliers=3),
+    # Attention of one DiT rank at the c2 token count: 24 heads of 128.
+    'dit_attention': dict(seed=8, m=53504, heads=24),
     'dit_norm': dict(seed=5, m=16384, hidden=3072, mod_rows=9, frames=16, eps=1e-6 / RESIDUAL_DIVISOR ** 2),
 }
 
@@ -149,6 +151,15 @@ def dit_qkv_rope(m=None, seed=None):
     q_gain = torch.rand(128, generator=g) + 0.5
     k_gain = torch.rand(128, generator=g) + 0.5
     return dict(x=x, w=w, freqs=freqs, q_gain=q_gain, k_gain=k_gain, heads=s['heads'], rot_dim=s['rot_dim'])
+
+
+def dit_attention(m=None, seed=None):
+    """q, k, v [1, heads, m, 128] fp16 ~ N(0, 1) (the RMS-normalized Q/K scale)."""
+    s = SHAPES['dit_attention']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m = m or s['m']
+    shape = (1, s['heads'], m, 128)
+    return {n: torch.randn(shape, generator=g, dtype=torch.float32).half() for n in ('q', 'k', 'v')}
 
 
 def quantize_weight(w, device):

@@ -50,6 +50,13 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   output unchanged; against a float64 torch restatement on random inputs.
 * ``norm_quantize``     - composition of the pinned norm with the pinned
   ``prepare_activation`` / ``convrot256`` + ``quantize_rows``.
+* ``int8_attention``    - (module) the permutation of the transposed V
+  layout; an exact chunked key mean on integer data; absmax elements mapping
+  to +-127 and the folded softmax scale; identical keys give the mean of the
+  quantized values, one dominant key gives its value row; random inputs
+  within cosine 0.999 of float64 softmax attention, which a wrong softmax
+  scale fails. Bit parity with the reference's vendored Kitchen kernel is
+  unpinned (its source is not part of the reference).
 
 Functions that only an import of the absent third-party comfy-kitchen 0.2.37
 could pin bit for bit (its GEMM-based rotation summation order) are noted

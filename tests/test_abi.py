@@ -35,7 +35,7 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 192, 144, 144, 104]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 192, 144, 144, 104, 144, 112]
     assert ctypes.sizeof(_abi.RopeEpilogue) == 40   # static_assert'ed in the library too
 
 

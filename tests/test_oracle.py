@@ -512,3 +512,54 @@ def test_rms_rope_power_of_two_scale_invariance_and_float64():
     out[..., :rot // 2] = ft[:, None, :, 0, 0] * lo + ft[:, None, :, 0, 1] * hi
     out[..., rot // 2:rot] = ft[:, None, :, 1, 0] * lo + ft[:, None, :, 1, 1] * hi
     assert np.max(np.abs(q - out.numpy())) < 4e-6 * np.max(np.abs(out.numpy()))
+
+
+# ------------------------------------------------------------ INT8 attention
+from oracle import int8_attention as oa  # noqa: E402
+
+
+def test_attention_oracle_layout_and_prepare_pins():
+    perm = oa.perm32()
+    assert sorted(perm.tolist()) == list(range(32))
+    assert perm[:8].tolist() == [0, 1, 2, 3, 8, 9, 10, 11] and perm[16:20].tolist() == [4, 5, 6, 7]
+    # integer keys: the chunked fp32 mean is exact
+    k = np.arange(2 * 300 * 128, dtype=np.float32).reshape(1, 2, 300, 128) % 7 - 3
+    assert np.array_equal(oa.key_mean(k), k.astype(np.float64).mean(2).astype(np.float32))
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, 1, 5, 128)).astype(np.float32)
+    v = rng.standard_normal((1, 1, 300, 128)).astype(np.float32)
+    pr = oa.prepare(q, k[:, :1], v)
+    # each query row's absmax element maps to +-127; qs carries sm_scale * log2(e)
+    assert np.all(np.abs(pr['q8']).max(-1) == 127)
+    s = np.abs(q).max(-1) * np.float32(1 / 127)
+    assert np.allclose(pr['qs'], s * np.float32(128 ** -0.5 * 1.4426950408889634), rtol=1e-6)
+    # centred keys, one scale per 64-key block, zero padding past nk
+    assert pr['k8'].shape == (1, 1, 320, 128) and not pr['k8'][:, :, 300:].any()
+    assert pr['ks'].shape == (1, 1, 5)
+    # V^T holds key perm(p) of each 32-key group at position p
+    assert np.array_equal(pr['vt8'][0, 0, :, 32 + 5], pr['v8'][0, 0, 32 + perm[5], :])
+
+
+def test_attention_oracle_against_closed_forms():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal((1, 2, 40, 128)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 150, 128)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 150, 128)).astype(np.float32)
+    out = oa.attention(oa.prepare(q, k, v)).astype(np.float64)
+    exact = oa.reference_attention(q, k, v)
+    cos = (out * exact).sum() / np.sqrt((out * out).sum() * (exact * exact).sum())
+    assert cos > 0.999
+    # identical keys: every probability is 127, the output is the mean of the quantized values
+    ku = np.repeat(rng.standard_normal((1, 1, 1, 128)).astype(np.float32), 100, axis=2)
+    pr = oa.prepare(q[:, :1], ku, v[:, :1, :100])
+    mean_v = (pr['v8'][:, :, :100].astype(np.float64) * pr['vs'][:, :, None, :]).mean(2)
+    assert np.abs(oa.attention(pr) - mean_v[:, :, None, :]).max() <= 1e-6 * np.abs(mean_v).max()
+    # one dominant key: the output is that key's quantized value row
+    kd = rng.standard_normal((1, 1, 70, 128)).astype(np.float32) * 0.01
+    kd[0, 0, 33] = q[0, 0, 0] * 30
+    pr = oa.prepare(q[:, :1, :1], kd, v[:, :1, :70])
+    row = pr['v8'][0, 0, 33].astype(np.float64) * pr['vs'][0, 0]
+    assert np.abs(oa.attention(pr)[0, 0, 0] - row).max() <= 1e-6 * np.abs(row).max()
+    # a wrong softmax scale fails the comparison with exact attention
+    wrong = oa.attention(oa.prepare(q, k, v, sm_scale=np.float32(2 * 128 ** -0.5))).astype(np.float64)
+    assert (wrong * exact).sum() / np.sqrt((wrong * wrong).sum() * (exact * exact).sum()) < 0.99
