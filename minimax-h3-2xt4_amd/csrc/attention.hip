@@ -196,6 +196,16 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
   }
 }
 
+// Direct global -> LDS load (global_load_lds_dwordx4): lane i's 16 bytes
+// land at l + 16 i (l wave-uniform).
+__device__ __forceinline__ void lds_dma16(const int8_t* g, int8_t* l) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)l, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(0) (loads, including the LDS DMA, have landed).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 struct AttnParams {
   const int8_t* q8;
   const float* qs;
@@ -229,26 +239,20 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + 32 * ds);
   }
   const float qscale = p.qs[bh * p.nq + qrow];
-  // Thread tid moves 16-byte chunks tid and tid + 256 of both tiles: K row
-  // r = idx / 8, chunk idx % 8 (stored at chunk ^ ((r >> 1) & 7)); V^T row
-  // idx / 4, chunk idx % 4 (stored at chunk ^ ((row >> 2) & 3)). The
-  // swizzles keep the fragment reads (32 rows, one chunk column) free of
-  // bank conflicts.
-  auto load_tiles = [&](int j, v4i (&kr)[2], v4i (&vr)[2]) {
+  // Tiles are DMA'd global -> LDS, each wave filling 2 KB of each: K rows
+  // are 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7),
+  // V^T rows 64 bytes with chunk c at c ^ ((row >> 2) & 3) (the fragment
+  // reads, 32 rows of one chunk column, are then free of bank conflicts). A
+  // DMA lane writes the next 16 bytes of its instruction's kilobyte, so it
+  // loads the chunk that lands on its physical position.
+  auto dma_tiles = [&](int j, int st) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int idx = tid + 256 * u;
-      kr[u] = *reinterpret_cast<const v4i*>(k8 + (int64_t)(kAttnBK * j + (idx >> 3)) * kAttnD + 16 * (idx & 7));
-      vr[u] = *reinterpret_cast<const v4i*>(vt8 + (int64_t)(idx >> 2) * p.nkp + kAttnBK * j + 16 * (idx & 3));
-    }
-  };
-  auto store_tiles = [&](int st, const v4i (&kr)[2], const v4i (&vr)[2]) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int idx = tid + 256 * u;
-      const int r = idx >> 3, c = idx & 7, ch = idx >> 2, s = idx & 3;
-      *reinterpret_cast<v4i*>(lds[st][0] + r * kAttnD + ((c ^ ((r >> 1) & 7)) << 4)) = kr[u];
-      *reinterpret_cast<v4i*>(lds[st][1] + ch * kAttnBK + ((s ^ ((ch >> 2) & 3)) << 4)) = vr[u];
+      const int kb = 2 * wave + u;
+      const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
+      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, lds[st][0] + kb * 1024);
+      const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
+      lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, lds[st][1] + kb * 1024);
     }
   };
   // S^T of the block in stage st: sacc[t][4 g + i] is the score of key
@@ -265,16 +269,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
         sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
       }
   };
-  v4i kr[2], vr[2];
-  load_tiles(0, kr, vr);
-  store_tiles(0, kr, vr);
-  if (p.nblk > 1) {
-    load_tiles(1, kr, vr);
-    store_tiles(1, kr, vr);
-  }
+  dma_tiles(0, 0);
+  if (p.nblk > 1) dma_tiles(1, 1);
+  wait_vmem();
   __syncthreads();
-  v16i sc[2];
-  scores(0, sc);
+  v16i sa[2], sb[2];
+  scores(0, sa);
   float m = -__builtin_inff();
   // Output and denominator: fp32 parts plus integer parts accumulated since
   // the last change of the running maximum.
@@ -335,17 +335,17 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
         psum = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, psum, false);
       }
   };
-  for (int j = 0; j < p.nblk; ++j) {
-    const int st = j % 3;
+  // Block j from stage st (its scores in cur); the scores of block j + 1
+  // (stage st1) go to nxt, block j + 2 is DMA'd into stage st2.
+  auto step = [&](int j, int st, int st1, int st2, const v16i (&cur)[2], v16i (&nxt)[2]) {
     const bool has1 = j + 1 < p.nblk, has2 = j + 2 < p.nblk;
-    if (has2) load_tiles(j + 2, kr, vr);
-    v16i sn[2];
-    if (has1) scores(st == 2 ? 0 : st + 1, sn);
+    if (has2) dma_tiles(j + 2, st2);
+    if (has1) scores(st1, nxt);
     uint32_t pw[2][4];
     int psum;
     float mnew, alpha;
-    if (kAttnBK * (j + 1) > p.nk) softmax(std::true_type{}, j, sc, pw, psum, mnew, alpha);
-    else softmax(std::false_type{}, j, sc, pw, psum, mnew, alpha);
+    if (kAttnBK * (j + 1) > p.nk) softmax(std::true_type{}, j, cur, pw, psum, mnew, alpha);
+    else softmax(std::false_type{}, j, cur, pw, psum, mnew, alpha);
     // A new maximum for any query of the wavefront folds the integer parts
     // into the fp32 ones with the rescale.
     if (__any(alpha != 1.0f)) {
@@ -372,13 +372,20 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
         oi[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, oi[ct], 0, 0, 0);
       }
     }
-    if (has2) store_tiles(st == 0 ? 2 : st - 1, kr, vr);
+    // Block j + 2 landed, and every wave is done with stages st (V) and
+    // st1 (K) of this step before they are refilled.
+    wait_vmem();
     __syncthreads();
-    if (has1) {
-      sc[0] = sn[0];
-      sc[1] = sn[1];
-    }
+  };
+  int st = 0;
+  int j = 0;
+  for (; j + 1 < p.nblk; j += 2) {   // two steps per trip: the score buffers swap without copies
+    const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+    step(j, st, s1, s2, sa, sb);
+    step(j + 1, s1, s2, st, sb, sa);
+    st = s2;
   }
+  if (j < p.nblk) step(j, st, st == 2 ? 0 : st + 1, st == 0 ? 2 : st - 1, sa, sb);
   lf = lf + (float)li;
   const float l = lf + __shfl_xor(lf, 32, 64);
   if (q0 + fr >= p.nq) return;
