@@ -240,10 +240,11 @@ int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
  *     sat(rne(x / s)) with s = max(amax * fp32(1/127), 1e-30). v is written
  *     transposed: vt8[c][64 j + 32 u + p] holds key 64 j + 32 u + 8 g + 4 h + i
  *     of channel c for p = 16 h + 4 g + i.
- *   attention: per query and 64-key block, S = q8.k8 (int32), fp32 online
- *     softmax in the exp2 domain with the hardware exp2, probabilities
- *     rounded to integers 0..127, P.v8 in int32, output
- *     (acc * vs[c]) / sum of probabilities.
+ *   attention: S = q8.k8 (int32); m = the query's largest logit
+ *     fp32(max(S) * qs * ks[block]); probabilities
+ *     P = rne(exp2(fma(S, qs * ks, log2(127) - m - |m| 2^-22))) in 0..127
+ *     (hardware exp2); P.v8 and sum(P) exact in int32 (nk <= 131072);
+ *     output fp32(fp32(f32(acc) * vs[c]) / f32(sum P)).
  * q, k, v: [b, h, nq|nk, d] contiguous; d == 128.
  */
 typedef struct W8A8AttnPrepareArgs {

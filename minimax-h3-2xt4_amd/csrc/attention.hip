@@ -1,10 +1,11 @@
 // INT8 attention for 128-wide heads: the preparation of the INT8 operands
 // (key centering, per-token Q scales, per-64-key K scales, per-channel V
-// scales, V transposed) and the attention kernel (S = Q.K^T on INT8 MFMA,
-// exp2-domain online softmax in fp32, probabilities quantized to 0..127 for
-// an INT8 MFMA P.V product, with the denominator as the sum of the same
-// integer probabilities). The exponentials use the hardware exp2
-// (v_exp_f32).
+// scales, V transposed) and the attention kernel (S = Q.K^T on INT8 MFMA;
+// a first pass finds each query's largest logit, the second quantizes the
+// exp2-domain probabilities against it to integers 0..127 for an INT8 MFMA
+// P.V product, the denominator being the sum of the same integers, so the
+// whole accumulation is exact in int32). The exponentials use the hardware
+// exp2 (v_exp_f32).
 //
 // Layout of the attention kernel: a workgroup of four wavefronts takes 128
 // queries of one (batch, head); a wavefront owns 32 of them. Keys come in
@@ -220,9 +221,11 @@ struct AttnParams {
 template <int OUT>
 __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   // Three-stage ring of [0: K tile, 64 keys x 128 bytes; 1: V^T tile, 128
-  // channels x 64 bytes]. Iteration j reads K of block j + 1 (its scores are
-  // issued before block j's softmax, so the MFMAs run under it) and V of
-  // block j, and fills the stage of block j + 2.
+  // channels x 64 bytes]. Two passes over the keys: the first finds each
+  // query's largest logit (K tiles only), the second quantizes the
+  // probabilities against it and accumulates P.V and sum(P) in int32. In
+  // both, step j issues the scores of block j + 1 before working on block j
+  // (the MFMAs run under the VALU work) and DMAs block j + 2.
   __shared__ __attribute__((aligned(16))) int8_t lds[3][2][kAttnBK * kAttnD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hh = lane >> 5;
@@ -239,20 +242,23 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + 32 * ds);
   }
   const float qscale = p.qs[bh * p.nq + qrow];
+  const float* ksc = p.ks + bh * p.nblk;
   // Tiles are DMA'd global -> LDS, each wave filling 2 KB of each: K rows
   // are 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7),
   // V^T rows 64 bytes with chunk c at c ^ ((row >> 2) & 3) (the fragment
   // reads, 32 rows of one chunk column, are then free of bank conflicts). A
   // DMA lane writes the next 16 bytes of its instruction's kilobyte, so it
   // loads the chunk that lands on its physical position.
-  auto dma_tiles = [&](int j, int st) {
+  auto dma_tiles = [&](auto with_v, int j, int st) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int kb = 2 * wave + u;
       const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
       lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, lds[st][0] + kb * 1024);
-      const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
-      lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, lds[st][1] + kb * 1024);
+      if constexpr (decltype(with_v)::value) {
+        const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
+        lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, lds[st][1] + kb * 1024);
+      }
     }
   };
   // S^T of the block in stage st: sacc[t][4 g + i] is the score of key
@@ -269,54 +275,70 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
         sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
       }
   };
-  dma_tiles(0, 0);
-  if (p.nblk > 1) dma_tiles(1, 1);
-  wait_vmem();
-  __syncthreads();
-  v16i sa[2], sb[2];
-  scores(0, sa);
-  float m = -__builtin_inff();
-  // Output and denominator: fp32 parts plus integer parts accumulated since
-  // the last change of the running maximum.
-  float of[4][16], lf = 0.0f;
+  // Keys of the last block past nk.
+  auto masked = [&](int j, int t, int x) { return kAttnBK * j + 32 * t + 8 * (x >> 2) + 4 * hh + (x & 3) >= p.nk; };
+  // One pass over the blocks: prologue (blocks 0 and 1 in stages 0 and 1,
+  // scores of block 0), then work(j, st, cur) per block with the score
+  // buffers swapping without copies.
+  auto run_pass = [&](auto with_v, auto work) {
+    dma_tiles(with_v, 0, 0);
+    if (p.nblk > 1) dma_tiles(with_v, 1, 1);
+    wait_vmem();
+    __syncthreads();
+    v16i sa[2], sb[2];
+    scores(0, sa);
+    auto step = [&](int j, int st, int st1, int st2, const v16i (&cur)[2], v16i (&nxt)[2]) {
+      if (j + 2 < p.nblk) dma_tiles(with_v, j + 2, st2);
+      if (j + 1 < p.nblk) scores(st1, nxt);
+      work(j, st, cur);
+      // Block j + 2 landed, and every wave is done with the stages this
+      // step read before they are refilled.
+      wait_vmem();
+      __syncthreads();
+    };
+    int st = 0, j = 0;
+    for (; j + 1 < p.nblk; j += 2) {
+      const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+      step(j, st, s1, s2, sa, sb);
+      step(j + 1, s1, s2, st, sb, sa);
+      st = s2;
+    }
+    if (j < p.nblk) step(j, st, st == 2 ? 0 : st + 1, st == 0 ? 2 : st - 1, sa, sb);
+  };
+
+  // Pass 1: the largest logit of the query, max over blocks of
+  // fp32(max(S) * c_j) (the lane's half of the keys, then the other half).
+  float ml = -__builtin_inff();
+  run_pass(std::false_type{}, [&](int j, int, const v16i (&s)[2]) {
+    int mx = INT32_MIN;
+    if (kAttnBK * (j + 1) > p.nk) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) mx = masked(j, t, x) ? mx : max(mx, s[t][x]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) mx = max(mx, s[t][x]);
+    }
+    if (mx != INT32_MIN) ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
+  });
+  const float m = fmaxf(ml, __shfl_xor(ml, 32, 64));
+  // log2(127) - m, lowered by |m| 2^-22 so that the largest exponent cannot
+  // pass log2(127) by more than a few ulps (P <= 127).
+  const float nm = (kLog2_127 - m) - fabsf(m) * 0x1p-22f;
+
+  // Pass 2: P = rne(exp2(fma(S, c_j, nm))) in 0..127, O^T += V^T.P^T and
+  // sum(P), exact in int32.
   v16i oi[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) oi[ct] = v16i{};
   int li = 0;
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    oi[ct] = v16i{};
-#pragma unroll
-    for (int x = 0; x < 16; ++x) of[ct][x] = 0.0f;
-  }
-  const float* ksc = p.ks + bh * p.nblk;
-  // Softmax of one block: quantized probabilities (packed as the B operand
-  // of the P.V product), their integer sum and the new maximum. TAIL masks
-  // the keys past nk (last block only).
-  auto softmax = [&](auto tail_tag, int j, const v16i (&s)[2], uint32_t (&pw)[2][4], int& psum, float& mnew,
-                     float& alpha) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
-    int sv[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        sv[t][x] = s[t][x];
-        if constexpr (TAIL) {
-          if (kAttnBK * j + 32 * t + 8 * (x >> 2) + 4 * hh + (x & 3) >= p.nk) sv[t][x] = INT32_MIN;
-        }
-      }
-    int mx = sv[0][0];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int x = 0; x < 16; ++x) mx = max(mx, sv[t][x]);
-    mx = max(mx, __shfl_xor(mx, 32, 64));
+  run_pass(std::true_type{}, [&](int j, int st, const v16i (&s)[2]) {
     const float c = qscale * ksc[j];
-    mnew = fmaxf(m, (float)mx * c);
-    alpha = __builtin_amdgcn_exp2f(m - mnew);
-    // log2(127) - mnew, lowered by |mnew| 2^-22 so that the largest
-    // exponent cannot pass log2(127) by more than a few ulps (P <= 127).
-    const float nm = (kLog2_127 - mnew) - fabsf(mnew) * 0x1p-22f;
-    psum = 0;
+    const bool tail = kAttnBK * (j + 1) > p.nk;
+    uint32_t pw[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -324,44 +346,17 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
         int b4[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float qv = __builtin_amdgcn_exp2f(__builtin_fmaf((float)sv[t][4 * g + i], c, nm));
+          const float qv = __builtin_amdgcn_exp2f(__builtin_fmaf((float)s[t][4 * g + i], c, nm));
           // rne(qv) for 0 <= qv < 2^22: the low bits of qv + 1.5 * 2^23.
           b4[i] = __builtin_bit_cast(int, qv + kRneMagic);
-          if constexpr (TAIL) {
-            if (sv[t][4 * g + i] == INT32_MIN) b4[i] = 0;
-          }
+        }
+        if (tail) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) b4[i] = masked(j, t, 4 * g + i) ? 0 : b4[i];
         }
         pw[t][g] = pack4(b4[0], b4[1], b4[2], b4[3]);
-        psum = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, psum, false);
+        li = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, li, false);
       }
-  };
-  // Block j from stage st (its scores in cur); the scores of block j + 1
-  // (stage st1) go to nxt, block j + 2 is DMA'd into stage st2.
-  auto step = [&](int j, int st, int st1, int st2, const v16i (&cur)[2], v16i (&nxt)[2]) {
-    const bool has1 = j + 1 < p.nblk, has2 = j + 2 < p.nblk;
-    if (has2) dma_tiles(j + 2, st2);
-    if (has1) scores(st1, nxt);
-    uint32_t pw[2][4];
-    int psum;
-    float mnew, alpha;
-    if (kAttnBK * (j + 1) > p.nk) softmax(std::true_type{}, j, cur, pw, psum, mnew, alpha);
-    else softmax(std::false_type{}, j, cur, pw, psum, mnew, alpha);
-    // A new maximum for any query of the wavefront folds the integer parts
-    // into the fp32 ones with the rescale.
-    if (__any(alpha != 1.0f)) {
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-          of[ct][x] = (of[ct][x] + (float)oi[ct][x]) * alpha;
-          oi[ct][x] = 0;
-        }
-      lf = (lf + (float)li) * alpha;
-      li = 0;
-    }
-    li += psum;
-    m = mnew;
-    // O^T += V^T.P^T (channels 32 ct + rows of the MFMA layout x queries).
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const v4i pf = {(int)pw[t][0], (int)pw[t][1], (int)pw[t][2], (int)pw[t][3]};
@@ -372,22 +367,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
         oi[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, oi[ct], 0, 0, 0);
       }
     }
-    // Block j + 2 landed, and every wave is done with stages st (V) and
-    // st1 (K) of this step before they are refilled.
-    wait_vmem();
-    __syncthreads();
-  };
-  int st = 0;
-  int j = 0;
-  for (; j + 1 < p.nblk; j += 2) {   // two steps per trip: the score buffers swap without copies
-    const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
-    step(j, st, s1, s2, sa, sb);
-    step(j + 1, s1, s2, st, sb, sa);
-    st = s2;
-  }
-  if (j < p.nblk) step(j, st, st == 2 ? 0 : st + 1, st == 0 ? 2 : st - 1, sa, sb);
-  lf = lf + (float)li;
-  const float l = lf + __shfl_xor(lf, 32, 64);
+  });
+  const float l = (float)(li + __shfl_xor(li, 32, 64));
   if (q0 + fr >= p.nq) return;
   const int64_t orow = (bh * p.nq + q0 + fr) * kAttnD;
   const float* vsc = p.vs + bh * kAttnD;
@@ -400,10 +381,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
       const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
       float y[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float o = of[ct][4 * g + i] + (float)oi[ct][4 * g + i];
-        y[i] = (o * sv[i]) / l;
-      }
+      for (int i = 0; i < 4; ++i) y[i] = ((float)oi[ct][4 * g + i] * sv[i]) / l;
       if constexpr (OUT == kF32) {
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + c0) = make_float4(y[0], y[1], y[2], y[3]);
       } else {
@@ -478,6 +456,10 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention: head dimension %d != 128", a->d);
   W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention: empty problem");
   W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536, "w8a8_attention: sizes out of range");
+  if (a->nk > (1 << 17)) {   // the int32 P.V sums hold nk * 127 * 127
+    set_error("w8a8_attention: at most 131072 keys (exact int32 accumulation)");
+    return W8A8_ERR_UNSUPPORTED;
+  }
   W8A8_REQUIRE(a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->out, "w8a8_attention: null buffer");
   W8A8_REQUIRE(aligned16(a->q8) && aligned16(a->k8) && aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->out),
                "w8a8_attention: tensors must be 16-byte aligned");

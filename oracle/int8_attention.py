@@ -27,19 +27,15 @@ prepare (exact, checked bit for bit):
     values), k8 = sat(rne(kc / s)); keys past Nk are zero.
   * V: one scale per channel (amax over all tokens), v8 = sat(rne(v / s)).
 
-attention (fp32, checked within a tolerance: the GPU's exp2 is the hardware
-approximation):
-  per query, over 64-key blocks in order, with running max m (-inf):
-    S = q8 . k8 (int32, exact), c = fp32(qs * ks[block]),
-    m_new = max(m, fp32(max(S) * c)), alpha = exp2(m - m_new),
-    nm = fp32(fp32(log2(127) - m_new) - fp32(|m_new| * 2^-22)),
-    p = exp2(fma(S, c, nm)), P = rne(p) (integers 0..127; the 2^-22 margin
-    keeps the largest exponent within a few ulps of log2(127)),
-    the integer accumulators of P.v8 and of sum(P) (one per half of the
-    keys, the lanes' split) are folded into fp32 ones
-    (O = (O + f32(acc)) * alpha) whenever any query of the 32-query group
-    has alpha != 1;
-  out = fp32(fp32(O * vs) / l), l the sum of both halves' denominators.
+attention (checked within a tolerance: the GPU's exp2 is the hardware
+approximation), per query:
+    S = q8 . k8 (int32, exact) and c_j = fp32(qs * ks[j]) for key block j;
+    m = max over blocks of fp32(max(S_j) * c_j), the largest logit;
+    nm = fp32(fp32(log2(127) - m) - fp32(|m| * 2^-22));
+    P = rne(exp2(fma(S, c_j, nm))), integers 0..127 (the 2^-22 margin keeps
+    the largest exponent within a few ulps of log2(127)), 0 past Nk;
+    acc = P . v8 and l = sum(P), exact integers;
+    out = fp32(fp32(f32(acc) * vs) / f32(l)).
 """
 import numpy as np
 
@@ -50,7 +46,6 @@ LOG2E = F32(1.4426950408889634)
 L127 = F32(np.log2(127.0))
 BLOCK_K = 64
 CHUNK = 256
-WAVE_Q = 32
 
 
 def _f32(x):
@@ -116,7 +111,7 @@ def prepare(q, k, v, sm_scale=None):
 
 
 def attention(prep, out_dtype='f32'):
-    """Blockwise INT8 attention from prepared operands (module docstring).
+    """INT8 attention from prepared operands (module docstring).
     Returns [B, H, Nq, D] in out_dtype ('f32' or 'f16')."""
     q8 = prep['q8'].astype(np.int64)
     k8 = prep['k8'].astype(np.int64)
@@ -125,50 +120,25 @@ def attention(prep, out_dtype='f32'):
     b, h, nq, d = q8.shape
     nkp = k8.shape[2]
     nblk = nkp // BLOCK_K
+    valid = np.arange(nkp) < nk
     out = np.zeros((b, h, nq, d), F32)
-    nqp = -(-nq // WAVE_Q) * WAVE_Q
-    rows = np.minimum(np.arange(nqp), nq - 1)     # padded queries repeat the last one
-    # per-half key order of the running denominators (the lane's 16 keys per 32-key tile)
-    half_keys = [np.array([8 * g + 4 * hh + i for g in range(4) for i in range(4)]) for hh in (0, 1)]
     for bi in range(b):
         for hi in range(h):
-            qq = q8[bi, hi, rows]                           # [nqp, d]
-            qsc = qs[bi, hi, rows]
-            m = np.full(nqp, -np.inf, F32)
-            lf = np.zeros((2, nqp), F32)
-            li = np.zeros((2, nqp), np.int64)
-            of = np.zeros((nqp, d), F32)
-            oi = np.zeros((nqp, d), np.int64)
-            for j in range(nblk):
-                kb = k8[bi, hi, j * BLOCK_K:(j + 1) * BLOCK_K]
-                s = qq @ kb.T                                # [nqp, 64] exact
-                valid = np.arange(j * BLOCK_K, (j + 1) * BLOCK_K) < nk
-                c = (qsc * ks[bi, hi, j]).astype(F32)
-                mx = np.where(valid[None, :], s, np.iinfo(np.int64).min).max(1)
-                with np.errstate(over='ignore', invalid='ignore'):
-                    mblk = (mx.astype(F32) * c).astype(F32)
-                    mnew = np.maximum(m, mblk)
-                    alpha = np.exp2((m - mnew).astype(F32)).astype(F32)
-                    nm = ((L127 - mnew).astype(F32) - (np.abs(mnew) * F32(2.0 ** -22)).astype(F32)).astype(F32)
-                    e = (s.astype(np.float64) * c[:, None].astype(np.float64) + nm[:, None]).astype(F32)
-                    p = np.exp2(e).astype(F32)
-                pi = np.where(valid[None, :], np.rint(p), 0).astype(np.int64)
-                groups = alpha.reshape(-1, WAVE_Q)
-                flush = np.repeat((groups != 1).any(1), WAVE_Q)
-                of = np.where(flush[:, None], ((of + oi.astype(F32)) * alpha[:, None]).astype(F32), of)
-                oi = np.where(flush[:, None], 0, oi)
-                lf = np.where(flush[None, :], ((lf + li.astype(F32)) * alpha[None, :]).astype(F32), lf)
-                li = np.where(flush[None, :], 0, li)
-                for hh in (0, 1):
-                    cols = np.concatenate([half_keys[hh], 32 + half_keys[hh]])
-                    li[hh] = li[hh] + pi[:, cols].sum(1)
-                oi = oi + pi @ v8[bi, hi, j * BLOCK_K:(j + 1) * BLOCK_K]
-                m = mnew
-            of = (of + oi.astype(F32)).astype(F32)
-            lfin = (lf + li.astype(F32)).astype(F32)
-            l = (lfin[0] + lfin[1]).astype(F32)
-            res = ((of * vs[bi, hi][None, :]).astype(F32) / l[:, None]).astype(F32)
-            out[bi, hi] = res[:nq]
+            s = q8[bi, hi] @ k8[bi, hi].T                                  # [nq, nkp] exact
+            c = (qs[bi, hi][:, None] * ks[bi, hi][None, :]).astype(F32)   # [nq, nblk]
+            cfull = np.repeat(c, BLOCK_K, axis=1)
+            smask = np.where(valid[None, :], s, np.iinfo(np.int64).min)
+            mblk = smask.reshape(nq, nblk, BLOCK_K).max(-1)
+            with np.errstate(over='ignore', invalid='ignore'):
+                mj = np.where(mblk > np.iinfo(np.int64).min, (mblk.astype(F32) * c).astype(F32), -np.inf)
+                m = mj.max(1).astype(F32)
+                nm = ((L127 - m).astype(F32) - (np.abs(m) * F32(2.0 ** -22)).astype(F32)).astype(F32)
+                e = (s.astype(np.float64) * cfull.astype(np.float64) + nm[:, None]).astype(F32)
+                p = np.exp2(e).astype(F32)
+            pi = np.where(valid[None, :], np.rint(p), 0).astype(np.int64)
+            acc = pi @ v8[bi, hi]
+            l = pi.sum(1).astype(F32)
+            out[bi, hi] = ((acc.astype(F32) * vs[bi, hi][None, :]).astype(F32) / l[:, None]).astype(F32)
     if out_dtype == 'f16':
         return out.astype(np.float16)
     return out
