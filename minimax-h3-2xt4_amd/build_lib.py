@@ -39,6 +39,11 @@ HIPCC_FLAGS = [
 INST_VARIANTS = [(0, 4), (1, 1), (1, 2), (1, 3), (2, 1), (2, 2), (2, 3)]
 
 
+# Per-file options. attention.hip: MFMA results in VGPRs (its scores feed
+# VALU work every block; in AGPRs each block would copy them over).
+FILE_FLAGS = {'attention.hip': ['-mllvm', '-amdgpu-mfma-vgpr-form']}
+
+
 def hipcc():
     path = shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
     if not Path(path).exists():
@@ -55,7 +60,7 @@ def _units():
                 units.append((src, f'{src.stem}_{epi}_{out}.o',
                               [f'-DW8A8_INST_EPI={epi}', f'-DW8A8_INST_OUT={out}']))
         else:
-            units.append((src, src.stem + '.o', []))
+            units.append((src, src.stem + '.o', FILE_FLAGS.get(src.name, [])))
     return units
 
 
