@@ -109,6 +109,28 @@ def test_gemm_rope_epilogue_checks():
         assert rc == _abi.ERR_UNSUPPORTED and 'rope epilogue' in msg, (rope_fields, gemm_fields, msg)
 
 
+def test_attention_argument_checks():
+    lib = _abi.load()
+    assert lib.w8a8_attention_workspace_size(1, 2, 300) == 2 * (2 * 2 + 1) * 128 * 4
+    assert lib.w8a8_attention_workspace_size(0, 2, 300) == 0
+    base = dict(struct_size=ctypes.sizeof(_abi.AttnPrepareArgs), in_dtype=_abi.F16, q=4096, k=8192, v=12288, b=1,
+                h=2, nq=100, nk=300, d=128, sm_scale=0.088, q8=16384, qs=20480, k8=24576, ks=28672, vt8=32768,
+                vs=36864, workspace=40960, workspace_bytes=1 << 20)
+    _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'd': 64}), 'head dimension')
+    _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'in_dtype': _abi.BF16}), 'in_dtype')
+    _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'workspace_bytes': 64}), 'workspace')
+    _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'k': 8200}), 'aligned')
+    _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'sm_scale': 0.0}), 'sm_scale')
+    _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'nk': 0}), 'empty')
+    att = dict(struct_size=ctypes.sizeof(_abi.AttentionArgs), out_dtype=_abi.F16, q8=4096, qs=8192, k8=12288,
+               ks=16384, vt8=20480, vs=24576, b=1, h=2, nq=100, nk=300, d=128, out=28672)
+    _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out_dtype': _abi.I32}), 'out_dtype')
+    _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out': None}), 'null')
+    big = _abi.AttentionArgs(**{**att, 'nk': (1 << 17) + 1})
+    assert lib.w8a8_attention(ctypes.byref(big)) == _abi.ERR_UNSUPPORTED
+    assert '131072' in lib.w8a8_last_error().decode()
+
+
 def test_swiglu_argument_checks():
     base = dict(struct_size=ctypes.sizeof(_abi.SwigluArgs), x_dtype=_abi.F16, x=4096, ldx=512, rows=2,
                 width=256, q=8192, ldq=256, scale=16384)
