@@ -31,7 +31,6 @@ constexpr int kAttnWaveQ = 32;    // queries per wavefront
 constexpr int kAttnBQ = 128;      // queries per workgroup
 constexpr float kLog2e = 0x1.715476p+0f;    // fp32(log2(e))
 constexpr float kLog2_127 = 0x1.bf469cp+2f; // fp32(log2(127))
-constexpr float kRneMagic = 12582912.0f;    // 1.5 * 2^23
 
 struct AttnPrepParams {
   const void* q;
@@ -343,18 +342,18 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        int b4[4];
+        float qv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float qv = __builtin_amdgcn_exp2f(__builtin_fmaf((float)s[t][4 * g + i], c, nm));
-          // rne(qv) for 0 <= qv < 2^22: the low bits of qv + 1.5 * 2^23.
-          b4[i] = __builtin_bit_cast(int, qv + kRneMagic);
-        }
+        for (int i = 0; i < 4; ++i) qv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)s[t][4 * g + i], c, nm));
         if (tail) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) b4[i] = masked(j, t, 4 * g + i) ? 0 : b4[i];
+          for (int i = 0; i < 4; ++i) qv[i] = masked(j, t, 4 * g + i) ? 0.0f : qv[i];
         }
-        pw[t][g] = pack4(b4[0], b4[1], b4[2], b4[3]);
+        // v_cvt_pk_u8_f32 rounds to nearest even and packs the byte.
+        uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(qv[0], 0, 0u);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(qv[1], 1, w);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(qv[2], 2, w);
+        pw[t][g] = __builtin_amdgcn_cvt_pk_u8_f32(qv[3], 3, w);
         li = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, li, false);
       }
 #pragma unroll
