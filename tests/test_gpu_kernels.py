@@ -20,7 +20,9 @@ pytestmark = pytest.mark.gpu
 GEMM_SHAPES = [(1, 16, 16), (13, 48, 64), (64, 64, 128), (256, 256, 64), (300, 520, 192), (257, 260, 80),
                (1000, 1100, 3072), (4096, 3072, 3072),
                # weight-streaming (M <= 64) shapes: text-encoder up/down, ragged N
-               (1, 14336, 4096), (64, 4096, 14336), (37, 1000, 1024), (5, 520, 192), (65, 4096, 512)]
+               (1, 14336, 4096), (64, 4096, 14336), (37, 1000, 1024), (5, 520, 192), (65, 4096, 512),
+               # 64 weight rows per workgroup (M 49..64, N >= 12288), ragged last workgroup
+               (64, 14336, 4096), (50, 12352, 256)]
 
 
 @pytest.mark.parametrize('m,n,k', GEMM_SHAPES)
