@@ -7,10 +7,10 @@
 // whole accumulation is exact in int32). The exponentials use the hardware
 // exp2 (v_exp_f32).
 //
-// Layout of the attention kernel: a workgroup of four wavefronts takes 128
-// queries of one (batch, head); a wavefront owns 32 of them. Keys come in
-// blocks of 64 through a two-stage LDS ring (K tile 64 x 128 bytes, V^T tile
-// 128 x 64 bytes). The score tile is computed transposed, S^T = K.Q^T, so a
+// Layout of the attention kernel: a workgroup of eight wavefronts (two per
+// SIMD) takes 256 queries of one (batch, head); a wavefront owns 32. Keys come in
+// blocks of 64 through a three-stage LDS ring (K tile 64 x 128 bytes, V^T
+// tile 128 x 64 bytes). The score tile is computed transposed, S^T = K.Q^T, so a
 // lane holds one query (lane % 32) and 16 of every 32 keys: the softmax
 // statistics of a query need one exchange with the lane 32 away, and the
 // quantized probabilities are already the B operand of O^T = V^T.P^T. Its K
@@ -28,7 +28,9 @@ constexpr int kAttnD = 128;       // head dimension
 constexpr int kAttnBK = 64;       // keys per block
 constexpr int kAttnChunk = 256;   // tokens per partial of the key statistics
 constexpr int kAttnWaveQ = 32;    // queries per wavefront
-constexpr int kAttnBQ = 128;      // queries per workgroup
+constexpr int kAttnWaves = 8;     // wavefronts per workgroup
+constexpr int kAttnBQ = kAttnWaves * kAttnWaveQ;   // queries per workgroup
+constexpr int kAttnDma = 8 / kAttnWaves;           // 1 KB DMA instructions per wave and tile
 constexpr float kLog2e = 0x1.715476p+0f;    // fp32(log2(e))
 constexpr float kLog2_127 = 0x1.bf469cp+2f; // fp32(log2(127))
 
@@ -218,7 +220,7 @@ struct AttnParams {
 };
 
 template <int OUT>
-__global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p) {
   // Three-stage ring of [0: K tile, 64 keys x 128 bytes; 1: V^T tile, 128
   // channels x 64 bytes]. Two passes over the keys: the first finds each
   // query's largest logit (K tiles only), the second quantizes the
@@ -250,8 +252,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   // loads the chunk that lands on its physical position.
   auto dma_tiles = [&](auto with_v, int j, int st) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int kb = 2 * wave + u;
+    for (int u = 0; u < kAttnDma; ++u) {
+      const int kb = kAttnDma * wave + u;
       const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
       lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, lds[st][0] + kb * 1024);
       if constexpr (decltype(with_v)::value) {
@@ -469,7 +471,7 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   p.nkp = p.nblk * kAttnBK;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   const dim3 grid((unsigned)((p.nq + kAttnBQ - 1) / kAttnBQ), (unsigned)(a->b * a->h));
-  if (a->out_dtype == W8A8_F32) hipLaunchKernelGGL(attention_kernel<kF32>, grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL(attention_kernel<kF16>, grid, dim3(256), 0, s, p);
+  if (a->out_dtype == W8A8_F32) hipLaunchKernelGGL(attention_kernel<kF32>, grid, dim3(64 * kAttnWaves), 0, s, p);
+  else hipLaunchKernelGGL(attention_kernel<kF16>, grid, dim3(64 * kAttnWaves), 0, s, p);
   return launch_status("w8a8_attention");
 }
