@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 7
+#define W8A8_ABI_VERSION 8
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -342,13 +342,21 @@ int w8a8_attention(const W8A8AttentionArgs* args);
 /* The RMS-RoPE epilogue of w8a8_gemm (see W8A8GemmArgs.rope). Output
  * columns [0, heads*128) are the Q heads and [heads*128, 2*heads*128) the K
  * heads (the numerics of w8a8_rms_rope with dim 128); later columns (V) are
- * stored unchanged. freqs: [m, rot_dim/2, 2, 2] of freq_dtype (F16 or F32);
+ * stored unchanged. freqs of freq_dtype (F16 or F32), in freq_layout
+ *   W8A8_ROPE_MATRICES: [m, rot_dim/2, 2, 2], F[p][s][t] (the reference's);
+ *   W8A8_ROPE_PAIRS: [m, 2, rot_dim/2, 2], entry [s][p] = (F[p][s][s],
+ *     F[p][s][1-s]) - the same values ordered so a lane's eight rotations
+ *     are one contiguous run (built once per forward, see the package's
+ *     rms_rope.pack_freqs);
  * q_gain, k_gain: [128] fp32; all 16-byte aligned. */
+enum { W8A8_ROPE_MATRICES = 0, W8A8_ROPE_PAIRS = 1 };
 typedef struct W8A8RopeEpilogue {
   int32_t heads;
   int32_t rot_dim;
   int32_t freq_dtype;
   float eps;
+  int32_t freq_layout;     /* W8A8_ROPE_MATRICES or W8A8_ROPE_PAIRS */
+  int32_t reserved;
   const void* freqs;
   const float* q_gain;
   const float* k_gain;

@@ -20,7 +20,7 @@ void set_error(const char* fmt, ...) {
 static_assert(sizeof(W8A8QuantArgs) == 88, "W8A8QuantArgs layout");
 static_assert(sizeof(W8A8SwigluArgs) == 96, "W8A8SwigluArgs layout");
 static_assert(sizeof(W8A8GemmArgs) == 192, "W8A8GemmArgs layout");
-static_assert(sizeof(W8A8RopeEpilogue) == 40, "W8A8RopeEpilogue layout");
+static_assert(sizeof(W8A8RopeEpilogue) == 48, "W8A8RopeEpilogue layout");
 static_assert(sizeof(W8A8DequantArgs) == 144, "W8A8DequantArgs layout");
 static_assert(sizeof(W8A8NormArgs) == 144, "W8A8NormArgs layout");
 static_assert(sizeof(W8A8RmsRopeArgs) == 104, "W8A8RmsRopeArgs layout");

@@ -122,6 +122,8 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
     W8A8_REQUIRE(r->rot_dim > 0 && r->rot_dim <= 128 && r->rot_dim % 2 == 0, "w8a8_gemm: rope rot_dim %d invalid",
                  r->rot_dim);
     W8A8_REQUIRE(r->freq_dtype == W8A8_F16 || r->freq_dtype == W8A8_F32, "w8a8_gemm: rope freq_dtype not F16/F32");
+    W8A8_REQUIRE(r->freq_layout == W8A8_ROPE_MATRICES || r->freq_layout == W8A8_ROPE_PAIRS,
+                 "w8a8_gemm: rope freq_layout %d unknown", r->freq_layout);
     W8A8_REQUIRE(r->freqs && r->q_gain && r->k_gain && aligned16(r->freqs) && aligned16(r->q_gain) &&
                      aligned16(r->k_gain),
                  "w8a8_gemm: rope freqs and gains must be non-null and 16-byte aligned");
@@ -136,6 +138,7 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
     p.rope_rot = r->rot_dim;
     p.rope_half = r->rot_dim / 2;
     p.rope_f32 = r->freq_dtype == W8A8_F32;
+    p.rope_pairs = r->freq_layout == W8A8_ROPE_PAIRS;
     p.rope_eps = r->eps;
     p.rope_freqs = r->freqs;
     p.rope_q_gain = r->q_gain;

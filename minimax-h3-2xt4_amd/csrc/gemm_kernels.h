@@ -420,10 +420,35 @@ __device__ __forceinline__ void load_rope_scales(const GemmParams& p, int nw, in
 // p0 .. p0 + 7, a 16-byte aligned block of the row's table. (Four 16-byte
 // loads and selects beat eight 4-byte loads of just the side's words: the
 // epilogue is bound by the number of memory instructions.)
-template <int FQ>
-__device__ __forceinline__ void load_rope_freqs(const void* frow, int p0, int side, float (&diag)[8],
+// PAIRS: the table row holds, per side s and pair p, (F[p][s][s],
+// F[p][s][1 - s]), so the lane's sixteen values are one contiguous run
+// (two 16-byte loads for fp16, no selects).
+template <int FQ, bool PAIRS>
+__device__ __forceinline__ void load_rope_freqs(const void* frow, int p0, int side, int half, float (&diag)[8],
                                                 float (&offd)[8]) {
-  if constexpr (FQ == kF32) {
+  if constexpr (PAIRS) {
+    const int first = 2 * (side * half + p0);
+    if constexpr (FQ == kF32) {
+      const float4* f = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(frow) + first);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float4 v = f[k];
+        diag[2 * k] = v.x; offd[2 * k] = v.y; diag[2 * k + 1] = v.z; offd[2 * k + 1] = v.w;
+      }
+    } else {
+      const uint4* f = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(frow) + first);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint4 u = f[k];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          diag[4 * k + q] = h2f((uint16_t)(w[q] & 0xffffu));
+          offd[4 * k + q] = h2f((uint16_t)(w[q] >> 16));
+        }
+      }
+    }
+  } else if constexpr (FQ == kF32) {
     const float* f = reinterpret_cast<const float*>(frow) + 4 * p0 + 2 * side;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -461,7 +486,7 @@ __device__ __forceinline__ void load_rope_freqs(const void* frow, int p0, int si
 // gain, and the rotation with the partner element, read back from the
 // slice after the normalized values replace the accumulators there. Rows
 // past m are not stored (their rotation matrices are those of row m - 1).
-template <int EPI, int FQ>
+template <int EPI, int FQ, bool PAIRS>
 __device__ __forceinline__ void store_quadrant_rope(const GemmParams& p, v16i (&acc)[4][4], const float (&wsc)[2][8],
                                                     const float (&as)[4], int mw, int nw, int lane, int8_t* stage) {
   constexpr int RB = 512;   // 128 four-byte values per staged row
@@ -560,7 +585,7 @@ __device__ __forceinline__ void store_quadrant_rope(const GemmParams& p, v16i (&
           part[4 * q] = v.x; part[4 * q + 1] = v.y; part[4 * q + 2] = v.z; part[4 * q + 3] = v.w;
         }
         const char* frow = reinterpret_cast<const char*>(p.rope_freqs) + (int64_t)min(m, p.m - 1) * half * 4 * FES;
-        load_rope_freqs<FQ>(frow, p0, side0, diag, offd);
+        load_rope_freqs<FQ, PAIRS>(frow, p0, side0, half, diag, offd);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const float a = nv[it][j] * diag[j];
@@ -1043,10 +1068,13 @@ void gemm_i8_persistent(GemmParams p) {
           store_quadrant32_passes<EPI, OUT, 0, true>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
         else
           store_quadrant32_passes<EPI, OUT, 0, false>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
+      } else if (p.rope_pairs) {
+        if (p.rope_f32) store_quadrant_rope<EPI, kF32, true>(p, acc, wsc, as, mw, nw, lane, stage_w);
+        else store_quadrant_rope<EPI, kF16, true>(p, acc, wsc, as, mw, nw, lane, stage_w);
       } else if (p.rope_f32) {
-        store_quadrant_rope<EPI, kF32>(p, acc, wsc, as, mw, nw, lane, stage_w);
+        store_quadrant_rope<EPI, kF32, false>(p, acc, wsc, as, mw, nw, lane, stage_w);
       } else {
-        store_quadrant_rope<EPI, kF16>(p, acc, wsc, as, mw, nw, lane, stage_w);
+        store_quadrant_rope<EPI, kF16, false>(p, acc, wsc, as, mw, nw, lane, stage_w);
       }
     } else if ((FLAGS & kWithGate) == 0 && p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
       store_quadrant32_passes<EPI, OUT, FLAGS, (FLAGS & kWithGate) == 0>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,

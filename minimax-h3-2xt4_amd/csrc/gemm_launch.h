@@ -30,7 +30,7 @@ struct GemmParams {
   int gvec;               // gate rows allow float4 loads (16-byte base, ldg % 4 == 0)
   // RMS-RoPE epilogue (rope_heads > 0): output columns [0, 2 * rope_heads *
   // 128) are Q then K heads, normalized and rotated after the fp16 rounding.
-  int rope_heads, rope_half, rope_rot, rope_f32;
+  int rope_heads, rope_half, rope_rot, rope_f32, rope_pairs;
   float rope_eps;
   const void* rope_freqs;
   const float* rope_q_gain;

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -36,7 +36,7 @@ class SwigluArgs(ctypes.Structure):
 
 class RopeEpilogue(ctypes.Structure):
     _fields_ = [('heads', _c.c_int32), ('rot_dim', _c.c_int32), ('freq_dtype', _c.c_int32), ('eps', _c.c_float),
-                ('freqs', _p), ('q_gain', _p), ('k_gain', _p)]
+                ('freq_layout', _c.c_int32), ('reserved', _c.c_int32), ('freqs', _p), ('q_gain', _p), ('k_gain', _p)]
 
 
 class GemmArgs(ctypes.Structure):

@@ -311,15 +311,16 @@ def _rope_epilogue(rope, m, device):
         raise ValueError('frequencies must be float16 or float32')
     if not (0 < rot_dim <= 128 and rot_dim % 2 == 0) or freqs.numel() != m * rot_dim * 2:
         raise ValueError('rope needs an even rot_dim <= 128 and freqs [M, rot_dim/2, 2, 2]')
-    freqs = _aligned16(freqs.reshape(m, rot_dim // 2, 2, 2))
+    pairs = bool(rope.get('pairs', False))
+    freqs = _aligned16(freqs.reshape((m, 2, rot_dim // 2, 2) if pairs else (m, rot_dim // 2, 2, 2)))
     gq = _aligned16(rope['q_gain'].to(torch.float32).reshape(-1))
     gk = _aligned16(rope['k_gain'].to(torch.float32).reshape(-1))
     _device(freqs, gq, gk)
     if freqs.device != device or gq.numel() != 128 or gk.numel() != 128:
         raise ValueError('rope tensors must be on the operands\' device, with 128-entry gains')
     args = _abi.RopeEpilogue(heads=heads, rot_dim=rot_dim, freq_dtype=_abi.DTYPE_CODE[freqs.dtype],
-                             eps=float(rope.get('eps', 1e-6)), freqs=freqs.data_ptr(), q_gain=gq.data_ptr(),
-                             k_gain=gk.data_ptr())
+                             eps=float(rope.get('eps', 1e-6)), freq_layout=1 if pairs else 0, freqs=freqs.data_ptr(),
+                             q_gain=gq.data_ptr(), k_gain=gk.data_ptr())
     return args, (freqs, gq, gk)
 
 
@@ -347,11 +348,13 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
     gemm_workspace_bytes() is allocated when the shape splits K (grids that
     would leave CUs idle). An empty tensor disables the split.
     rope: RMS-RoPE epilogue of a packed QKV projection, a dict with 'heads',
-    'rot_dim', 'freqs' ([M, rot_dim/2, 2, 2] fp16/fp32), 'q_gain', 'k_gain'
-    ([128]) and 'eps': the first 2 * heads * 128 output columns (Q heads,
-    then K heads) are stored normalized and rotated, bit-identical to
-    rms_rope() of the plain FP16 output; needs FP16 output without bias,
-    residual or gate (K is never split).
+    'rot_dim', 'freqs' ([M, rot_dim/2, 2, 2] fp16/fp32 rotation matrices, or
+    with 'pairs': True the [M, 2, rot_dim/2, 2] layout of
+    rms_rope.pack_freqs), 'q_gain', 'k_gain' ([128]) and 'eps': the first
+    2 * heads * 128 output columns (Q heads, then K heads) are stored
+    normalized and rotated, bit-identical to rms_rope() of the plain FP16
+    output; needs FP16 output without bias, residual or gate (K is never
+    split).
     """
     q = _rows_2d(q)
     if weight.ndim != 2:

@@ -34,8 +34,20 @@ def execute(packed, freqs, q_gain, k_gain, *, heads=28, dim=128, epsilon=1e-6, o
                             heads=heads, rot_dim=rot_dim, eps=float(epsilon), dim=dim, out_dtype=out_dtype)
 
 
+def pack_freqs(freqs):
+    """The rotation matrices (1, S, 1, half, 2, 2) or [S, half, 2, 2] reordered
+    for the QKV epilogue: [S, 2, half, 2] with entry [s][p] = (F[p][s][s],
+    F[p][s][1 - s]) - the values a lane of side s needs, contiguous. A layout
+    change only (no arithmetic); the DiT computes the matrices once per
+    forward, so this runs once for all its blocks."""
+    f = freqs.reshape(-1, freqs.shape[-3], 2, 2)
+    side0 = torch.stack([f[:, :, 0, 0], f[:, :, 0, 1]], -1)
+    side1 = torch.stack([f[:, :, 1, 1], f[:, :, 1, 0]], -1)
+    return torch.stack([side0, side1], 1).contiguous()
+
+
 def fused_qkv(x, weight, weight_scale, freqs, q_gain, k_gain, *, heads=28, dim=128, epsilon=1e-6, prepared=None,
-              convrot=True):
+              convrot=True, freqs_pairs=None):
     """The QKV projection followed by execute(), in one GEMM.
 
     patches/tp_dit.py:286-300 (qkv_proj, the split into q, k, v, then
@@ -44,9 +56,10 @@ def fused_qkv(x, weight, weight_scale, freqs, q_gain, k_gain, *, heads=28, dim=1
     packed Q and K never make the round trip through HBM. x: [S, K] fp16
     activation (or prepared = (codes, row_scale), the ConvRot256 INT8
     activation of the fused modulated norm); weight int8 [3 * heads * dim, K]
-    with its per-channel scale; freqs (1, S, 1, half, 2, 2). Returns (q, k,
-    v), each a [S, heads, dim] view of the packed FP16 output; q and k equal
-    execute(qkv_proj(x), ...) bit for bit, v equals the projection's V.
+    with its per-channel scale; freqs (1, S, 1, half, 2, 2); freqs_pairs, when
+    given, is pack_freqs(freqs) (the faster layout for the epilogue). Returns
+    (q, k, v), each a [S, heads, dim] view of the packed FP16 output; q and k
+    equal execute(qkv_proj(x), ...) bit for bit, v equals the projection's V.
     """
     if dim != 128:
         raise ValueError('full 128-wide heads required')
@@ -66,6 +79,10 @@ def fused_qkv(x, weight, weight_scale, freqs, q_gain, k_gain, *, heads=28, dim=1
     scale = weight_scale.to(device=codes.device, dtype=torch.float32).reshape(-1)
     rope = {'heads': heads, 'rot_dim': rot_dim, 'freqs': freqs.reshape(rows, rot_dim // 2, 2, 2),
             'q_gain': q_gain, 'k_gain': k_gain, 'eps': float(epsilon)}
+    if freqs_pairs is not None:
+        if freqs_pairs.shape != (rows, 2, rot_dim // 2, 2):
+            raise ValueError('freqs_pairs must be pack_freqs(freqs)')
+        rope.update(freqs=freqs_pairs, pairs=True)
     qkv = kernels.gemm(codes, weight, epilogue=kernels.EPI_COLUMN, row_scale=row_scale, col_scale=scale,
                        out_dtype=torch.float16, rope=rope)
     q, k, v = qkv.split(heads * dim, dim=-1)

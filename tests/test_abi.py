@@ -36,7 +36,7 @@ def test_version_and_struct_sizes():
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
     assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 192, 144, 144, 104, 144, 112]
-    assert ctypes.sizeof(_abi.RopeEpilogue) == 40   # static_assert'ed in the library too
+    assert ctypes.sizeof(_abi.RopeEpilogue) == 48   # static_assert'ed in the library too
 
 
 def _expect_invalid(name, args, fragment):
@@ -102,6 +102,8 @@ def test_gemm_rope_epilogue_checks():
     assert rc == _abi.ERR_INVALID and 'freq_dtype' in msg
     rc, msg = call({'q_gain': 8200})
     assert rc == _abi.ERR_INVALID and 'aligned' in msg
+    rc, msg = call({'freq_layout': 2})
+    assert rc == _abi.ERR_INVALID and 'freq_layout' in msg
     for rope_fields, gemm_fields in (({'rot_dim': 20}, {}), ({}, {'m': 64}), ({}, {'bias': 64, 'bias_dtype': _abi.F32}),
                                      ({}, {'out_dtype': _abi.F32}), ({}, {'ldc': 3 * 2 * 128 + 4}),
                                      ({}, {'k': 64, 'lda': 64, 'ldb': 64})):

@@ -168,3 +168,24 @@ def test_gemm_rope_epilogue_full_dit_shape(gpu):
     got = np_of(fused[rows.to(gpu)])
     assert_bits_equal(got[:, :width].reshape(-1, heads, 128), wq_, 'full-shape q rows')
     assert_bits_equal(got[:, width:2 * width].reshape(-1, heads, 128), wk_, 'full-shape k rows')
+
+
+@pytest.mark.parametrize('fq_dt', [torch.float16, torch.float32])
+def test_gemm_rope_paired_frequency_layout(gpu, fq_dt):
+    g = torch.Generator().manual_seed(23)
+    m, heads, k, rot = 301, 3, 256, 96
+    n = 3 * heads * 128
+    x, codes, a, wq, ws, f, gq, gk = _qkv_case(g, gpu, m, n, k, fq_dt, rot)
+    rope = {'heads': heads, 'rot_dim': rot, 'freqs': f, 'q_gain': gq, 'k_gain': gk, 'eps': 1e-6}
+    plain = kernels.gemm(codes, wq, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=ws, rope=rope)
+    packed = rms_rope.pack_freqs(f)
+    assert packed.shape == (m, 2, rot // 2, 2)
+    fr = f.reshape(m, rot // 2, 2, 2)
+    assert torch.equal(packed[:, 1, :, 0], fr[:, :, 1, 1]) and torch.equal(packed[:, 1, :, 1], fr[:, :, 1, 0])
+    paired = kernels.gemm(codes, wq, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=ws,
+                          rope=dict(rope, freqs=packed, pairs=True))
+    assert torch.equal(paired.view(torch.int16), plain.view(torch.int16))
+    freqs6 = f.reshape(1, m, 1, rot // 2, 2, 2)
+    q1, k1, v1 = rms_rope.fused_qkv(x, wq, ws, freqs6, gq, gk, heads=heads)
+    q2, k2, v2 = rms_rope.fused_qkv(x, wq, ws, freqs6, gq, gk, heads=heads, freqs_pairs=packed)
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, v2)
