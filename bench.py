@@ -447,7 +447,7 @@ def run_dit_half_shard(args, torch, dev):
             hc = h[r0:r0 + chunk]
             dit_column_linear.column_linear(hc, wqkv, sqkv)   # consumed by attention (not part of this path)
             y1 = dit_column_linear.column_linear(hc, w1, s1)
-            out[r0:r0 + chunk] = swiglu_quant.row_linear(y1, w2, s2)
+            swiglu_quant.row_linear(y1, w2, s2, out=out[r0:r0 + chunk])   # FP32 partial in place
     t = timed(torch, step, max(1, args.steps // 10), 1)
     ops = 2.0 * m * hidden * (s['qkv'] + 2 * s['ffn'] + s['ffn'])
     return dict(metric='DiT half-shard projections M=204336 (QKV, FC1, FC2 fp32 partial) TOPS',

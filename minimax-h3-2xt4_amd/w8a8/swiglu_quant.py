@@ -46,7 +46,7 @@ def supported(x, weight, weight_scale, world_size, groupsize):
 
 
 def row_linear(x, weight, weight_scale, comm=None, *, mode='fused_stored', scaled_transport=False,
-               finish_fn=None, consume_input=False, p0_b=False, residual=None, gate=None, gate_labels=None):
+               finish_fn=None, consume_input=False, p0_b=False, residual=None, gate=None, gate_labels=None, out=None):
     """FC2 row projection; patches/tilelang_swiglu_quant.py:108-128 on one GPU.
 
     Without a residual it returns FP32 (C * a) * w, as the reference does
@@ -57,18 +57,22 @@ def row_linear(x, weight, weight_scale, comm=None, *, mode='fused_stored', scale
     update fp16(fma(fp16(branch), gate[label], residual)) of the reference's
     fused row_gate_kernel (patches/tilelang_dit_fusion.py:56-77). The scaled FP16
     transport is a two-rank codec; on one GPU the INT32 accumulator is exact
-    and ``scaled_transport`` changes nothing.
+    and ``scaled_transport`` changes nothing. ``out`` (an extension of the
+    reference's signature): a [M, N] tensor of the result dtype to write into,
+    e.g. a row range of a larger buffer, instead of a new tensor.
     """
     if finish_fn is not None:
         raise ValueError('finish_fn belongs to the two-rank transport; pass residual= for the fused add')
     shape = x.shape
     q, scale = prepare(x, comm, mode, consume_input=consume_input, p0_b=p0_b)
     del x
+    if out is not None:
+        out = out.reshape(-1, weight.shape[0])
     if residual is None:
         out = kernels.gemm(q, weight, epilogue=kernels.EPI_ROW, row_scale=scale, col_scale=weight_scale,
-                           out_dtype=torch.float32)
+                           out_dtype=torch.float32, out=out)
     else:
         out = kernels.gemm(q, weight, epilogue=kernels.EPI_ROW, row_scale=scale, col_scale=weight_scale,
                            out_dtype=torch.float16, residual=residual.reshape(-1, weight.shape[0]),
-                           gate=gate, gate_labels=gate_labels)
+                           gate=gate, gate_labels=gate_labels, out=out)
     return out.reshape(*shape[:-1], weight.shape[0])

@@ -234,3 +234,16 @@ def test_gemm_w8a8_linear_full_size(gpu):
     acc = kernels.gemm(q, wq)
     assert_bits_equal(np_of(acc), o.int_mm(oq, np_of(wq)), 'c0 int32')
     assert_bits_equal(np_of(y), o.dequantize_row(np_of(acc), oa, np_of(ws), 'f16', np_of(data['bias'])), 'c0 out')
+
+
+def test_row_linear_writes_into_a_row_range(gpu):
+    g = torch.Generator().manual_seed(41)
+    x = (torch.randn((70, 2 * 512), generator=g) * 0.5).half().to(gpu)
+    w = torch.randn((256, 512), generator=g) * 0.02
+    wq, ws = _wq(w, gpu)
+    full = torch.full((100, 256), float('nan'), device=gpu)
+    got = swiglu_quant.row_linear(x, wq, ws, out=full[20:90])
+    want = swiglu_quant.row_linear(x, wq, ws)
+    assert got.data_ptr() == full[20:90].data_ptr()
+    assert torch.equal(full[20:90], want)
+    assert torch.isnan(full[:20]).all() and torch.isnan(full[90:]).all()
