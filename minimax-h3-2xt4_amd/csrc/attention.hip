@@ -262,9 +262,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       }
     }
   };
-  // S^T of the block in stage st: sacc[t][4 g + i] is the score of key
+  // S^T of the K tile at kt: sacc[t][4 g + i] is the score of key
   // 32 t + 8 g + 4 hh + i of the block for query fr.
-  auto scores = [&](int st, v16i (&sacc)[2]) {
+  auto scores_at = [&](const int8_t* kt, v16i (&sacc)[2]) {
     sacc[0] = v16i{};
     sacc[1] = v16i{};
 #pragma unroll
@@ -272,9 +272,19 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) {
         const int r = 32 * t + fr, ck = 2 * ds + hh;
-        const v4i kf = *reinterpret_cast<const v4i*>(lds[st][0] + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
+        const v4i kf = *reinterpret_cast<const v4i*>(kt + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
         sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
       }
+  };
+  auto scores = [&](int st, v16i (&sacc)[2]) { scores_at(lds[st][0], sacc); };
+  // K tile of block j DMA'd to dst (the layout of dma_tiles).
+  auto dma_k = [&](int j, int8_t* dst) {
+#pragma unroll
+    for (int u = 0; u < kAttnDma; ++u) {
+      const int kb = kAttnDma * wave + u;
+      const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
+      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, dst + kb * 1024);
+    }
   };
   // Keys of the last block past nk.
   auto masked = [&](int j, int t, int x) { return kAttnBK * j + 32 * t + 8 * (x >> 2) + 4 * hh + (x & 3) >= p.nk; };
@@ -309,22 +319,58 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 
   // Pass 1: the largest logit of the query, max over blocks of
   // fp32(max(S) * c_j) (the lane's half of the keys, then the other half).
+  // It takes two key blocks per step (K only: block 2u in the K half of a
+  // stage, block 2u + 1 in its V half), halving the barriers.
   float ml = -__builtin_inff();
-  run_pass(std::false_type{}, [&](int j, int, const v16i (&s)[2]) {
-    int mx = INT32_MIN;
-    if (kAttnBK * (j + 1) > p.nk) {
+  {
+    auto block_max = [&](int j, const v16i (&s)[2]) {
+      int mx = INT32_MIN;
+      if (kAttnBK * (j + 1) > p.nk) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int x = 0; x < 16; ++x) mx = masked(j, t, x) ? mx : max(mx, s[t][x]);
-    } else {
+          for (int x = 0; x < 16; ++x) mx = masked(j, t, x) ? mx : max(mx, s[t][x]);
+      } else {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int x = 0; x < 16; ++x) mx = max(mx, s[t][x]);
+          for (int x = 0; x < 16; ++x) mx = max(mx, s[t][x]);
+      }
+      if (mx != INT32_MIN) ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
+    };
+    const int npairs = (p.nblk + 1) / 2;
+    auto dma_pair = [&](int u, int st) {
+      dma_k(2 * u, lds[st][0]);
+      if (2 * u + 1 < p.nblk) dma_k(2 * u + 1, lds[st][1]);
+    };
+    auto pair_scores = [&](int u, int st, v16i (&s0)[2], v16i (&s1)[2]) {
+      scores_at(lds[st][0], s0);
+      if (2 * u + 1 < p.nblk) scores_at(lds[st][1], s1);
+    };
+    dma_pair(0, 0);
+    if (npairs > 1) dma_pair(1, 1);
+    wait_vmem();
+    __syncthreads();
+    v16i a0[2], a1[2], b0[2], b1[2];
+    pair_scores(0, 0, a0, a1);
+    auto step = [&](int u, int st1, int st2, const v16i (&c0)[2], const v16i (&c1)[2], v16i (&n0)[2],
+                    v16i (&n1)[2]) {
+      if (u + 2 < npairs) dma_pair(u + 2, st2);
+      if (u + 1 < npairs) pair_scores(u + 1, st1, n0, n1);
+      block_max(2 * u, c0);
+      if (2 * u + 1 < p.nblk) block_max(2 * u + 1, c1);
+      wait_vmem();
+      __syncthreads();
+    };
+    int st = 0, u = 0;
+    for (; u + 1 < npairs; u += 2) {
+      const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+      step(u, s1, s2, a0, a1, b0, b1);
+      step(u + 1, s2, st, b0, b1, a0, a1);
+      st = s2;
     }
-    if (mx != INT32_MIN) ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
-  });
+    if (u < npairs) step(u, st == 2 ? 0 : st + 1, st == 0 ? 2 : st - 1, a0, a1, b0, b1);
+  }
   const float m = fmaxf(ml, __shfl_xor(ml, 32, 64));
   // log2(127) - m, lowered by |m| 2^-22 so that the largest exponent cannot
   // pass log2(127) by more than a few ulps (P <= 127).
