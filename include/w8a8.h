@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 8
+#define W8A8_ABI_VERSION 9
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -245,7 +245,11 @@ int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
  *     P = rne(exp2(fma(S, qs * ks, log2(127) - m - |m| 2^-22))) in 0..127
  *     (hardware exp2); P.v8 and sum(P) exact in int32 (nk <= 131072);
  *     output fp32(fp32(f32(acc) * vs[c]) / f32(sum P)).
- * q, k, v: [b, h, nq|nk, d] contiguous; d == 128.
+ * q, k, v: [b, h, nq|nk, d] with element strides {batch, head, token} given
+ * per tensor and the d == 128 channels contiguous (e.g. the q, k and v
+ * columns of a packed [tokens, 3 * h * d] QKV projection, or contiguous
+ * [b, h, n, d] tensors); the output takes strides the same way. Every stride
+ * and base address must be a multiple of 16 bytes.
  */
 typedef struct W8A8AttnPrepareArgs {
   uint32_t struct_size;
@@ -259,6 +263,9 @@ typedef struct W8A8AttnPrepareArgs {
   int64_t nk;
   int32_t d;
   float sm_scale;          /* > 0; the reference's default is 1/sqrt(d) */
+  int64_t q_strides[3];    /* element strides of q's batch, head and token dims */
+  int64_t k_strides[3];
+  int64_t v_strides[3];
   int8_t* q8;              /* [b, h, nq, d] */
   float* qs;               /* [b, h, nq] */
   int8_t* k8;              /* [b, h, nkp, d], nkp = 64 * ceil(nk / 64) */
@@ -290,7 +297,8 @@ typedef struct W8A8AttentionArgs {
   int64_t nk;
   int32_t d;
   int32_t reserved;
-  void* out;               /* [b, h, nq, d] of out_dtype */
+  void* out;               /* [b, h, nq, d] of out_dtype, element strides out_strides */
+  int64_t out_strides[3];  /* batch, head, token */
   void* stream;
 } W8A8AttentionArgs;
 

@@ -21,6 +21,7 @@
 #include "w8a8_host.h"
 
 #include <type_traits>
+#include <utility>
 
 namespace w8a8 {
 
@@ -34,10 +35,22 @@ constexpr int kAttnDma = 8 / kAttnWaves;           // 1 KB DMA instructions per 
 constexpr float kLog2e = 0x1.715476p+0f;    // fp32(log2(e))
 constexpr float kLog2_127 = 0x1.bf469cp+2f; // fp32(log2(127))
 
+// Element strides of a [batch, head, token, channel] tensor whose channels
+// are contiguous; at(bh, t) is the offset of token t's row of the flat
+// (batch, head) index bh.
+struct Strides3 {
+  int64_t b, h, t;
+  int heads;
+  __device__ __forceinline__ int64_t at(int64_t bh, int64_t tok) const {
+    return (bh / heads) * b + (bh % heads) * h + tok * t;
+  }
+};
+
 struct AttnPrepParams {
   const void* q;
   const void* k;
   const void* v;
+  Strides3 qst, kst, vst;
   int nq, nk, nkp, nblk, chunks;
   float c0;   // fp32(sm_scale * log2(e))
   int8_t* q8;
@@ -64,11 +77,11 @@ __global__ __launch_bounds__(128) void attn_stats_kernel(AttnPrepParams p) {
   const int d = threadIdx.x, chunk = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int t0 = chunk * kAttnChunk, t1 = min(t0 + kAttnChunk, p.nk);
-  const int64_t base = bh * (int64_t)p.nk * kAttnD + d;
+  const int64_t kb = p.kst.at(bh, 0) + d, vb = p.vst.at(bh, 0) + d;
   float s = 0.0f, m = 0.0f;
   for (int t = t0; t < t1; ++t) {
-    s = s + ld1<DT>(p.k, base + (int64_t)t * kAttnD);
-    m = fmaxf(m, fabsf(ld1<DT>(p.v, base + (int64_t)t * kAttnD)));
+    s = s + ld1<DT>(p.k, kb + t * p.kst.t);
+    m = fmaxf(m, fabsf(ld1<DT>(p.v, vb + t * p.vst.t)));
   }
   const int64_t o = (bh * p.chunks + chunk) * kAttnD + d;
   p.part_sum[o] = s;
@@ -133,7 +146,7 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
   if (blk * kAttnBK < p.nq) {   // workgroup-uniform
     const bool valid = t < p.nq;
     float x[32];
-    if (valid) load32<DT>(p.q, (bh * p.nq + t) * kAttnD + c0, x);
+    if (valid) load32<DT>(p.q, p.qst.at(bh, t) + c0, x);
     else
 #pragma unroll
       for (int i = 0; i < 32; ++i) x[i] = 0.0f;
@@ -156,7 +169,7 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
     const float* mean = p.kmean + bh * kAttnD + c0;
     float x[32];
     if (valid) {
-      load32<DT>(p.k, (bh * p.nk + t) * kAttnD + c0, x);
+      load32<DT>(p.k, p.kst.at(bh, t) + c0, x);
 #pragma unroll
       for (int i = 0; i < 32; ++i) x[i] = x[i] - mean[i];
     } else {
@@ -178,7 +191,7 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
     if (tid == 0) p.ks[bh * p.nblk + blk] = s;
     // V: channel scales, then the tile goes through LDS to be transposed.
     const float* vsc = p.vs + bh * kAttnD + c0;
-    if (valid) load32<DT>(p.v, (bh * p.nk + t) * kAttnD + c0, x);
+    if (valid) load32<DT>(p.v, p.vst.at(bh, t) + c0, x);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       const float sv = vsc[i];
@@ -216,6 +229,7 @@ struct AttnParams {
   const int8_t* vt8;
   const float* vs;
   void* out;
+  Strides3 ost;
   int nq, nk, nkp, nblk;
 };
 
@@ -417,7 +431,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   });
   const float l = (float)(li + __shfl_xor(li, 32, 64));
   if (q0 + fr >= p.nq) return;
-  const int64_t orow = (bh * p.nq + q0 + fr) * kAttnD;
+  const int64_t orow = p.ost.at(bh, q0 + fr);
   const float* vsc = p.vs + bh * kAttnD;
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
@@ -439,6 +453,34 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 }
 
 static int64_t attn_chunks(int64_t nk) { return (nk + kAttnChunk - 1) / kAttnChunk; }
+
+// Non-negative element strides whose byte sizes are multiples of 16 (the
+// kernels move rows in 16-byte pieces).
+static bool strides_aligned(const int64_t (&st)[3], int elem) {
+  for (int i = 0; i < 3; ++i)
+    if (st[i] < 0 || (st[i] * elem) % 16 != 0) return false;
+  return true;
+}
+
+// True when no two (batch, head, token) rows of 128 contiguous elements
+// overlap: taken in increasing stride order, each dimension of size > 1
+// steps past everything the smaller ones span.
+static bool strides_disjoint(const int64_t (&st)[3], const int64_t (&n)[3]) {
+  int order[3] = {0, 1, 2};
+  for (int i = 0; i < 3; ++i)
+    for (int j = i + 1; j < 3; ++j)
+      if (st[order[j]] < st[order[i]]) std::swap(order[i], order[j]);
+  int64_t extent = kAttnD;
+  for (int i = 0; i < 3; ++i) {
+    const int dim = order[i];
+    if (n[dim] <= 1) continue;
+    if (st[dim] < extent) return false;
+    extent += st[dim] * (n[dim] - 1);
+  }
+  return true;
+}
+
+static Strides3 strides3(const int64_t (&st)[3], int64_t heads) { return {st[0], st[1], st[2], (int)heads}; }
 
 }  // namespace w8a8
 
@@ -466,8 +508,15 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   W8A8_REQUIRE(a->workspace_bytes >= w8a8_attention_workspace_size(a->b, a->h, a->nk),
                "w8a8_attention_prepare: workspace below w8a8_attention_workspace_size()");
   W8A8_REQUIRE(a->sm_scale > 0.0f, "w8a8_attention_prepare: sm_scale must be positive");
+  const int elem = a->in_dtype == W8A8_F16 ? 2 : 4;
+  W8A8_REQUIRE(strides_aligned(a->q_strides, elem) && strides_aligned(a->k_strides, elem) &&
+                   strides_aligned(a->v_strides, elem),
+               "w8a8_attention_prepare: strides must be non-negative multiples of 16 bytes");
   AttnPrepParams p;
   p.q = a->q; p.k = a->k; p.v = a->v;
+  p.qst = strides3(a->q_strides, a->h);
+  p.kst = strides3(a->k_strides, a->h);
+  p.vst = strides3(a->v_strides, a->h);
   p.nq = (int)a->nq; p.nk = (int)a->nk;
   p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);
   p.nkp = p.nblk * kAttnBK;
@@ -510,8 +559,13 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   W8A8_REQUIRE(a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->out, "w8a8_attention: null buffer");
   W8A8_REQUIRE(aligned16(a->q8) && aligned16(a->k8) && aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->out),
                "w8a8_attention: tensors must be 16-byte aligned");
+  const int64_t extents[3] = {a->b, a->h, a->nq};
+  W8A8_REQUIRE(strides_aligned(a->out_strides, a->out_dtype == W8A8_F16 ? 2 : 4),
+               "w8a8_attention: out strides must be non-negative multiples of 16 bytes");
+  W8A8_REQUIRE(strides_disjoint(a->out_strides, extents), "w8a8_attention: out strides make rows overlap");
   AttnParams p;
   p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs; p.out = a->out;
+  p.ost = strides3(a->out_strides, a->h);
   p.nq = (int)a->nq; p.nk = (int)a->nk;
   p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);
   p.nkp = p.nblk * kAttnBK;

@@ -62,6 +62,22 @@ def row_linear(module, x, fallback, comm, input_act=None, residual=None, gate=No
         return quant.row_linear(x, module.weight, module.weight_scale, comm, mode=policy.fc2_quantizer,
                                 scaled_transport=policy.row_linear_backend == 'tilelang_scaled_fp16',
                                 residual=residual, gate=gate, gate_labels=labels)
+    if (input_act is None and residual is not None and (gate is None or labels is not None)
+            and policy is not None and policy.row_linear_backend != 'native' and module.world_size == 1
+            and module.convrot and module.convrot_groupsize == 256
+            and x.dtype in (torch.float16, torch.float32) and residual.dtype == torch.float16):
+        # The O projection with the (gated) residual update in the GEMM
+        # epilogue: patches/tilelang_dit_fusion.py:153-199 (row_gated ->
+        # tilelang_transport_p2.row_linear on value.float(), finish_row):
+        # ConvRot256 in FP32, row-order dequant, fp16(fma(branch, gate, X)).
+        from . import kernels
+        flat = x.reshape(-1, x.shape[-1])
+        q, scale = kernels.quantize_rows(flat, convrot=True, round_rotated=False)
+        n = module.weight.shape[0]
+        out = kernels.gemm(q, module.weight, epilogue=kernels.EPI_ROW, row_scale=scale,
+                           col_scale=module.weight_scale, out_dtype=torch.float16,
+                           residual=residual.reshape(-1, n), gate=gate, gate_labels=labels)
+        return out.reshape(*x.shape[:-1], n)
     if input_act == 'swiglu' or (policy is not None and policy.row_linear_backend == 'tilelang_scaled_fp16'):
         # FP32 preparation island, as the reference keeps on fallback geometry.
         x = x.float()

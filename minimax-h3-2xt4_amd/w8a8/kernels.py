@@ -419,10 +419,23 @@ def dequantize(acc, row_scale, col_scale, *, epilogue=EPI_ROW, out_dtype=torch.f
 ATTN_BLOCK_K = 64
 
 
+def _row_strides(t):
+    """(batch, head, token) element strides of a [B, H, N, 128] tensor whose
+    rows the attention kernels can address in place (channels contiguous,
+    16-byte aligned), or None."""
+    esz = t.element_size()
+    st = [0 if n == 1 else s for n, s in zip(t.shape, t.stride())]
+    if st[3] != 1 or t.data_ptr() % 16 or any(s < 0 or (s * esz) % 16 for s in st[:3]):
+        return None
+    return tuple(st[:3])
+
+
 def attention_prepare(q, k, v, *, sm_scale=None):
     """INT8 operands of the attention for q [B, H, Nq, 128], k, v [B, H, Nk,
-    128] (fp16 or fp32, contiguous after this call). Returns a dict with q8,
-    qs, k8, ks, vt8, vs (device tensors) and the shape."""
+    128] (fp16 or fp32). The inputs are read in place when their channels
+    are contiguous and their strides 16-byte multiples (e.g. transposed views
+    of a packed QKV projection), else from contiguous copies. Returns a dict
+    with q8, qs, k8, ks, vt8, vs (device tensors) and the shape."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError('q, k, v must be [batch, heads, tokens, dim]')
     _device(q, k, v)
@@ -436,7 +449,12 @@ def attention_prepare(q, k, v, *, sm_scale=None):
     nk = k.shape[2]
     if nq == 0 or nk == 0 or b * h == 0:
         raise ValueError('empty attention')
-    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if _row_strides(q) is None:
+        q = q.contiguous()
+    if _row_strides(k) is None:
+        k = k.contiguous()
+    if _row_strides(v) is None:
+        v = v.contiguous()
     scale = float(d ** -0.5 if sm_scale is None else sm_scale)
     nkp = -(-nk // ATTN_BLOCK_K) * ATTN_BLOCK_K
     dev = q.device
@@ -451,7 +469,8 @@ def attention_prepare(q, k, v, *, sm_scale=None):
         nbytes = int(_abi.load().w8a8_attention_workspace_size(b, h, nk))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     args = _abi.AttnPrepareArgs(in_dtype=_abi.DTYPE_CODE[q.dtype], q=q.data_ptr(), k=k.data_ptr(), v=v.data_ptr(),
-                                b=b, h=h, nq=nq, nk=nk, d=d, sm_scale=scale,
+                                b=b, h=h, nq=nq, nk=nk, d=d, sm_scale=scale, q_strides=_row_strides(q),
+                                k_strides=_row_strides(k), v_strides=_row_strides(v),
                                 q8=prep['q8'].data_ptr(), qs=prep['qs'].data_ptr(), k8=prep['k8'].data_ptr(),
                                 ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(), vs=prep['vs'].data_ptr(),
                                 workspace=ws.data_ptr(), workspace_bytes=nbytes, stream=_abi.stream_of(q))
@@ -460,18 +479,22 @@ def attention_prepare(q, k, v, *, sm_scale=None):
 
 
 def attention(prep, *, out_dtype=torch.float16, out=None):
-    """Attention output [B, H, Nq, 128] from attention_prepare()'s operands."""
+    """Attention output [B, H, Nq, 128] from attention_prepare()'s operands.
+    ``out`` may be any [B, H, Nq, 128] view with contiguous channels and
+    16-byte strides whose rows do not overlap (e.g. the transpose of a
+    [B, Nq, H, 128] buffer, the layout the output projection reads)."""
     b, h, nq, nk, d = prep['shape']
     if out_dtype not in (torch.float16, torch.float32):
         raise ValueError('output must be float16 or float32')
     q8 = prep['q8']
     if out is None:
         out = torch.empty((b, h, nq, d), dtype=out_dtype, device=q8.device)
-    elif out.shape != (b, h, nq, d) or out.dtype != out_dtype or not out.is_contiguous():
-        raise ValueError('out must be a contiguous [B, H, Nq, D] tensor of out_dtype')
+    elif out.shape != (b, h, nq, d) or out.dtype != out_dtype or _row_strides(out) is None:
+        raise ValueError('out must be a [B, H, Nq, D] view of out_dtype with contiguous, 16-byte aligned rows')
     args = _abi.AttentionArgs(out_dtype=_abi.DTYPE_CODE[out_dtype], q8=q8.data_ptr(), qs=prep['qs'].data_ptr(),
                               k8=prep['k8'].data_ptr(), ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(),
                               vs=prep['vs'].data_ptr(), b=b, h=h, nq=nq, nk=nk, d=d, out=out.data_ptr(),
+                              out_strides=_row_strides(out),
                               stream=_abi.stream_of(q8))
     _abi.call('w8a8_attention', args)
     return out

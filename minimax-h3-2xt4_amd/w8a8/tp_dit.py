@@ -3,18 +3,21 @@
 ColumnParallelLinearINT8 / RowParallelLinearINT8 keep the attribute names of
 patches/tp_dit.py:25-162 (weight int8 [N, K], weight_scale fp32 [N, 1],
 convrot, convrot_groupsize, world_size, in/out features) so shards load the
-same way; with world_size 1 there is no exchange. DiTFeedForwardINT8 is the
-FC1 -> SwiGLU/ConvRot256 -> FC2 (+ residual) part of TPDiTBlockINT8.forward
-(patches/tp_dit.py:350-360) and chunked_rows runs any of them over M in
+same way; with world_size 1 there is no exchange. DiTAttentionINT8 is the attention
+sublayer of TPDiTBlockINT8.forward (patches/tp_dit.py:277-345: modulated
+norm -> QKV -> RMS-RoPE -> INT8 attention -> O + gated residual),
+DiTFeedForwardINT8 the FC1 -> SwiGLU/ConvRot256 -> FC2 (+ residual) part
+(patches/tp_dit.py:347-362), and chunked_rows runs any of them over M in
 fixed row chunks with the weights resident.
 """
 import torch
 from torch import nn
 
-from . import parallel_int8
+from . import kernels, parallel_int8
 from .dit_column_linear import column_linear, column_linear_quantized
 from .h3_tensor_flow import modulated_norm_quantize
 from .h3_operator_policy import H3OperatorPolicy, row_linear as dispatch_row
+from .rms_rope import fused_qkv
 
 
 class ColumnParallelLinearINT8(nn.Module):
@@ -144,6 +147,74 @@ class DiTFeedForwardINT8(nn.Module):
                                                    convrot_groupsize=self.fc1.convrot_groupsize)
         y = self.fc1(x, prepared=(codes, row_scale))
         return self.fc2(y, input_act='swiglu', residual=x, gate=gate, segments=segments)
+
+
+class DiTAttentionINT8(nn.Module):
+    """The DiT attention sublayer on one GPU (patches/tp_dit.py:277-345).
+
+    x <- x + gate_msa * out_proj(attention(rms_rope(qkv_proj(
+    modulated_norm(norm1, x, shift_msa, scale_msa))))) in four library steps:
+    the modulated RMSNorm fused into the QKV activation quantization, the QKV
+    GEMM with the per-head RMSNorm + RoPE of Q and K in its epilogue, the
+    INT8 attention reading Q, K and V in place from the packed projection and
+    writing [tokens, heads, 128] rows, and the O projection with the gated
+    residual update in its epilogue. Attribute names follow the reference
+    block: qkv_proj (3 packed components), out_proj, q_norm / k_norm
+    (RMSNorm over head_dim), heads_per_rank, head_dim, inner_per_rank.
+    """
+
+    def __init__(self, hidden, heads, head_dim=128, *, eps=1e-6, device=None, policy=None):
+        super().__init__()
+        if head_dim != 128:
+            raise ValueError('the INT8 attention and the RoPE epilogue take 128-wide heads')
+        self.heads_per_rank = heads
+        self.head_dim = head_dim
+        self.inner_per_rank = heads * head_dim
+        self.qkv_proj = ColumnParallelLinearINT8(hidden, 3 * self.inner_per_rank, device=device, components=3)
+        self.out_proj = RowParallelLinearINT8(self.inner_per_rank, hidden, device=device)
+        dev = self.qkv_proj.device
+        self.q_norm = nn.RMSNorm(head_dim, eps=eps, device=dev)
+        self.k_norm = nn.RMSNorm(head_dim, eps=eps, device=dev)
+        self.requires_grad_(False)
+        policy = policy or H3OperatorPolicy()
+        self.operator_policy = policy
+        self.qkv_proj.operator_policy = policy
+        self.out_proj.operator_policy = policy
+
+    def qkv(self, x, rope_freqs, *, prepared=None, freqs_pairs=None):
+        """(q, k, v) as [tokens, heads, 128] views of the packed projection,
+        q and k normalized and rotated (patches/tp_dit.py:286-309)."""
+        if rope_freqs is None:
+            raise ValueError('the fused QKV route applies RMS-RoPE: rope_freqs required')
+        return fused_qkv(x, self.qkv_proj.weight, self.qkv_proj.weight_scale, rope_freqs, self.q_norm.weight,
+                         self.k_norm.weight, heads=self.heads_per_rank, dim=self.head_dim, epsilon=self.q_norm.eps,
+                         prepared=prepared, convrot=self.qkv_proj.convrot, freqs_pairs=freqs_pairs)
+
+    def attention(self, q, k, v):
+        """Attention of [tokens, heads, 128] q, k, v (strided views allowed)
+        -> [tokens, heads * 128] FP16, the layout out_proj reads
+        (patches/h3_operator_policy.py:153-216 with the transpose folded
+        into the kernels' strides)."""
+        rows = q.shape[0]
+        prep = kernels.attention_prepare(q.transpose(0, 1)[None], k.transpose(0, 1)[None],
+                                         v.transpose(0, 1)[None])
+        out = torch.empty((rows, self.heads_per_rank, self.head_dim), dtype=torch.float16, device=q.device)
+        kernels.attention(prep, out_dtype=torch.float16, out=out.transpose(0, 1)[None])
+        return out.view(rows, self.inner_per_rank)
+
+    def forward_modulated(self, x, norm, shift, scale, gate, segments, rope_freqs, *, freqs_pairs=None):
+        """x [tokens, hidden] FP16 residual stream; norm the block's norm1;
+        shift / scale / gate the [R, hidden] modulation tables with
+        segments [(a, b, row)] tiling the rows; rope_freqs (1, tokens, 1,
+        half, 2, 2), freqs_pairs optionally rms_rope.pack_freqs(rope_freqs).
+        Returns the updated residual stream."""
+        codes, row_scale = modulated_norm_quantize(norm, x, shift, scale, segments, convrot=self.qkv_proj.convrot,
+                                                   convrot_groupsize=self.qkv_proj.convrot_groupsize)
+        q, k, v = self.qkv(x, rope_freqs, prepared=(codes, row_scale), freqs_pairs=freqs_pairs)
+        del codes, row_scale
+        attn = self.attention(q, k, v)
+        del q, k, v
+        return self.out_proj(attn, residual=x, gate=gate, segments=segments)
 
 
 def chunked_rows(fn, x, *others, chunk_rows=16384, out=None):

@@ -27,6 +27,10 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   where (C*a)*w and C*(a*w) round differently.
 * ``fc2_prologue``      - composition of the pinned pieces, plus the
   invariant that rotated row norms equal the SwiGLU row norms.
+* ``row_linear``        - composition of the pinned pieces; rotating the
+  activation and the weight rows alike leaves x.W^T unchanged (H H^T = I),
+  so the result tracks float64 x.W^T within the INT8 error, which a
+  rotation missing on either side fails.
 * ``fma_f32``           - exact rational arithmetic (fractions) on random
   and constructed midpoint cases, where the unfused a*b+c rounds differently.
 * ``gated_residual_add`` - composition of fma_f32 with the FP16 branch and
@@ -67,7 +71,7 @@ from .w8a8_oracle import (  # noqa: F401
     quantize_rows, convrot256, hadamard256, exp_f32, swiglu_f32,
     prepare_activation, fc2_prologue, int_mm, dequantize_row,
     dequantize_column, residual_add, to_bf16_bits, from_bf16_bits,
-    cast_out, quantize_weight, column_linear, row_linear_fc2, ffn_block,
+    cast_out, quantize_weight, column_linear, row_linear, row_linear_fc2, ffn_block,
     fma_f32, gated_residual_add, rms_sum_squares, modulated_rms_norm,
     norm_quantize, head_sum_squares, rms_rope,
 )

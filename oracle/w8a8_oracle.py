@@ -522,6 +522,26 @@ def row_linear_fc2(x, wq, ws, residual=None, out_dtype='f16', x_dtype='f16', w_f
     return residual_add(residual, branch)
 
 
+def row_linear(x, wq, ws, residual=None, out_dtype='f16', x_dtype='f16', w_f64=None, gate=None, labels=None):
+    """Row projection without an input activation (the DiT O projection).
+
+    Follows patches/parallel_int8.py:26-43,72-94 on one GPU: ConvRot256 and
+    the per-row quantizer in FP32 (the rotated values stay FP32, as
+    patches/tilelang_dit_fusion.py:195-199 rotates value.float()), int_mm,
+    the row-order dequantize, then the residual or gated update of
+    row_linear_fc2 (the finish of patches/tilelang_dit_fusion.py:146-150).
+    """
+    xf = _to_f32(x, x_dtype)
+    q, a = quantize_rows(convrot256(xf).reshape(-1, xf.shape[-1]))
+    acc = int_mm(q, wq, w_f64)
+    if residual is None:
+        return dequantize_row(acc, a, ws, out_dtype)
+    branch = dequantize_row(acc, a, ws, 'f16')
+    if gate is not None:
+        return gated_residual_add(residual, branch, gate, labels)
+    return residual_add(residual, branch)
+
+
 def ffn_block(h, w1q, ws1, w2q, ws2, residual, convrot=True, w1_f64=None, w2_f64=None, gate=None, labels=None):
     """DiT FFN block of the FP16-fix flow on one GPU.
 

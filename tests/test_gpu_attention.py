@@ -110,3 +110,30 @@ def test_reference_api(gpu):
     scaled = int8_attention.int8_attention(q, k, v, scale=0.05)
     want = oa.attention(oa.prepare(_np(q.cpu()), _np(k.cpu()), _np(v.cpu()), sm_scale=0.05), out_dtype='f32')
     assert np.abs(np_of(scaled).astype(np.float64) - want).max() <= 2e-3 * np.abs(want).max() + 1e-3
+
+
+@pytest.mark.parametrize('b,h,n,dtype', [(1, 3, 150, torch.float16), (2, 2, 70, torch.float32)])
+def test_strided_operands_and_output(gpu, b, h, n, dtype):
+    """q, k, v read in place from a packed [b, n, 3 h 128] projection and the
+    output written as [b, n, h, 128] rows give the bits of the contiguous
+    route."""
+    g = torch.Generator().manual_seed(31 + n)
+    packed = torch.randn((b, n, 3 * h * 128), generator=g).to(dtype).to(gpu)
+    q, k, v = (packed[..., i * h * 128:(i + 1) * h * 128].view(b, n, h, 128).transpose(1, 2) for i in range(3))
+    assert kernels._row_strides(q) is not None and not q.is_contiguous()
+    prep = kernels.attention_prepare(q, k, v)
+    flat = kernels.attention_prepare(q.contiguous(), k.contiguous(), v.contiguous())
+    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs'):
+        assert torch.equal(prep[name], flat[name]), name
+    for out_dtype in (torch.float16, torch.float32):
+        want = kernels.attention(flat, out_dtype=out_dtype)
+        rows = torch.full((b, n, h, 128), float('nan'), dtype=out_dtype, device=gpu)
+        got = kernels.attention(prep, out_dtype=out_dtype, out=rows.transpose(1, 2))
+        assert got.data_ptr() == rows.data_ptr()
+        assert torch.equal(rows, want.transpose(1, 2).contiguous())
+    # misaligned rows fall back to a copy on input and are refused as output
+    odd = torch.randn((1, 1, 40, 129), generator=g).to(dtype).to(gpu)[..., 1:]
+    assert kernels._row_strides(odd) is None
+    kernels.attention_prepare(odd, odd, odd)
+    with pytest.raises(ValueError):
+        kernels.attention(flat, out_dtype=torch.float32, out=torch.empty((b, h, n, 130), device=gpu)[..., :128])

@@ -563,3 +563,28 @@ def test_attention_oracle_against_closed_forms():
     # a wrong softmax scale fails the comparison with exact attention
     wrong = oa.attention(oa.prepare(q, k, v, sm_scale=np.float32(2 * 128 ** -0.5))).astype(np.float64)
     assert (wrong * exact).sum() / np.sqrt((wrong * wrong).sum() * (exact * exact).sum()) < 0.99
+
+
+def test_row_linear_rotation_cancels_against_rotated_weights():
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((16, 512)).astype(np.float32)
+    x[:, rng.choice(512, 4, replace=False)] *= 20.0          # outlier channels, which ConvRot spreads
+    w = (rng.standard_normal((96, 512)) * 0.05).astype(np.float32)
+    wq, ws = o.quantize_rows(o.convrot256(w))                 # the checkpoint stores rotated weight rows
+    exact = x.astype(np.float64) @ w.T.astype(np.float64)
+    y = o.row_linear(x, wq, ws, out_dtype='f32', x_dtype='f32').astype(np.float64)
+    rel = np.abs(y - exact).max() / np.abs(exact).max()
+    assert rel < 0.02, rel
+    # the same weights without the activation rotation are far off
+    q, a = o.quantize_rows(x)
+    plain = o.dequantize_row(o.int_mm(q, wq), a, ws, 'f32').astype(np.float64)
+    assert np.abs(plain - exact).max() / np.abs(exact).max() > 0.2
+    # the residual and gated forms cast the branch to FP16 first
+    res = (rng.standard_normal((16, 96)) * 0.1).astype(np.float16)
+    gate = rng.standard_normal((3, 96)).astype(np.float32)
+    labels = np.arange(16) % 3
+    x16 = x.astype(np.float16)
+    branch = o.row_linear(x16, wq, ws, out_dtype='f16')
+    assert np.array_equal(o.row_linear(x16, wq, ws, residual=res), o.residual_add(res, branch))
+    assert np.array_equal(o.row_linear(x16, wq, ws, residual=res, gate=gate, labels=labels),
+                          o.gated_residual_add(res, branch, gate, labels))
