@@ -634,7 +634,7 @@ def run_dit_attention(args, torch, dev):
                ms_per_step=round(ta + tp, 3),
                roofline=dict(bound='mfma', achieved=round(tops, 1), peak=PEAK_INT8_TOPS, unit='TFLOP/s',
                              frac=round(tops / PEAK_INT8_TOPS, 4), traffic=None,
-                             kernel='attention_kernel<1> (128 queries x 64-key blocks per workgroup)',
+                             kernel='attention_kernel<1> (256 queries x 64-key blocks per workgroup)',
                              algorithmic=f'{ops:.4g} int8 ops per launch (4 N^2 D H)'),
                kernels=dict(prepare_us=round(tp * 1e3, 1), attention_us=round(ta * 1e3, 1)))
     if not args.no_cpu_baseline:
@@ -655,7 +655,123 @@ def run_dit_attention(args, torch, dev):
     return res
 
 
-WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_attention': run_dit_attention, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
+def run_dit_attention_block(args, torch, dev):
+    """The DiT attention sublayer of one rank (53504 tokens, hidden 3072, 24
+    heads of 128, rotary prefix 96): modulated norm1 -> QKV with the
+    RMS-RoPE epilogue -> INT8 attention on the packed rows -> O projection
+    with the gated residual update. value = the sublayer's INT8 ops (the two
+    projections, 2 M N K each, and the attention's 4 M^2 D H) per second of
+    the whole sublayer; each stage is also timed alone."""
+    from w8a8 import h3_tensor_flow, kernels, rms_rope, tp_dit, workloads
+    data = workloads.dit_attention_block()
+    m, hidden, heads = data['x'].shape[0], data['hidden'], data['heads']
+    inner = heads * 128
+    block = tp_dit.DiTAttentionINT8(hidden, heads, device=dev)
+    wq, ws = workloads.quantize_weight(data['w_qkv'], dev)
+    wo, so = workloads.quantize_weight(data['w_o'], dev)
+    with torch.no_grad():
+        block.qkv_proj.weight.copy_(wq)
+        block.qkv_proj.weight_scale.copy_(ws.reshape(-1, 1))
+        block.out_proj.weight.copy_(wo)
+        block.out_proj.weight_scale.copy_(so.reshape(-1, 1) / workloads.RESIDUAL_DIVISOR)
+        block.q_norm.weight.copy_(data['q_gain'])
+        block.k_norm.weight.copy_(data['k_gain'])
+    norm = torch.nn.RMSNorm(hidden, eps=data['eps'], device=dev)
+    with torch.no_grad():
+        norm.weight.copy_(data['weight'])
+    x = data['x'].to(dev)
+    shift, scale, gate = (data[t].to(dev) for t in ('shift', 'scale', 'gate'))
+    segments = data['segments']
+    freqs = data['freqs'].to(dev)
+    pairs = rms_rope.pack_freqs(freqs)
+
+    def sublayer():
+        return block.forward_modulated(x, norm, shift, scale, gate, segments, freqs, freqs_pairs=pairs)
+
+    st = {}
+
+    def s_norm():
+        st['codes'] = h3_tensor_flow.modulated_norm_quantize(norm, x, shift, scale, segments)
+
+    def s_qkv():
+        st['qkv'] = block.qkv(x, freqs, prepared=st['codes'], freqs_pairs=pairs)
+
+    def s_prep():
+        q, k, v = st['qkv']
+        st['prep'] = kernels.attention_prepare(q.transpose(0, 1)[None], k.transpose(0, 1)[None],
+                                               v.transpose(0, 1)[None])
+
+    attn = torch.empty((m, heads, 128), dtype=torch.float16, device=dev)
+
+    def s_attn():
+        kernels.attention(st['prep'], out_dtype=torch.float16, out=attn.transpose(0, 1)[None])
+
+    def s_out():
+        return block.out_proj(attn.view(m, inner), residual=x, gate=gate, segments=segments)
+
+    stages = {}
+    for name, fn in (('norm_quantize', s_norm), ('qkv_rope_gemm', s_qkv), ('attention_prepare', s_prep),
+                     ('attention', s_attn), ('out_proj_gated', s_out)):
+        stages[name] = timed(torch, fn, args.steps, args.warmup)
+    st.clear()
+    total = timed(torch, sublayer, args.steps, args.warmup)
+    ops_qkv = 2.0 * m * 3 * inner * hidden
+    ops_att = 4.0 * m * m * 128 * heads
+    ops_o = 2.0 * m * hidden * inner
+    ops = ops_qkv + ops_att + ops_o
+    tops = ops / (total * 1e-3) / 1e12
+    att_tops = ops_att / (stages['attention'] * 1e-3) / 1e12
+    res = dict(metric='DiT attention sublayer 53504 tokens x 24 heads TOPS', value=round(tops, 1), unit='TOPS',
+               higher_is_better=True, dtype='int8', data='synthetic',
+               config=dict(workload='dit_attention_block', tokens=m, hidden=hidden, heads=heads, head_dim=128,
+                           rot_dim=2 * freqs.shape[-3]),
+               ms_per_step=round(total, 3),
+               roofline=dict(bound='mfma', achieved=round(att_tops, 1), peak=PEAK_INT8_TOPS, unit='TFLOP/s',
+                             frac=round(att_tops / PEAK_INT8_TOPS, 4), traffic=None,
+                             kernel='attention_kernel<1> (the sublayer\'s dominant kernel)',
+                             algorithmic=f'{ops_att:.4g} int8 ops per launch (4 N^2 D H)'),
+               kernels={k + '_us': round(v * 1e3, 1) for k, v in stages.items()})
+    res['kernels']['stages_sum_us'] = round(sum(stages.values()) * 1e3, 1)
+    res['kernels']['sublayer_us'] = round(total * 1e3, 1)
+    if not args.no_cpu_baseline:
+        import numpy as np
+        import oracle as o
+        from oracle import int8_attention as oa
+        rows, queries = min(args.cpu_rows // 8, m), 32
+        labels = np.zeros(rows, np.int64)
+        for a, b, row in segments:
+            labels[max(a, 0):min(b, rows)] = row
+        xs = data['x'][:rows].numpy()
+        wq_np, ws_np = wq.cpu().numpy(), ws.cpu().numpy().reshape(-1)
+        wo_np, so_np = wo.cpu().numpy(), block.out_proj.weight_scale.cpu().numpy().reshape(-1)
+        f_np = data['freqs'][0, :rows, 0].float().numpy()
+        gq_np, gk_np = data['q_gain'].numpy(), data['k_gain'].numpy()
+        tabs = [data[t].numpy() for t in ('weight', 'shift', 'scale', 'gate')]
+        rot = 2 * f_np.shape[1]
+
+        def cpu_rows():
+            hn = o.modulated_rms_norm(xs, tabs[0], tabs[1], tabs[2], labels, eps=data['eps'])
+            packed = o.column_linear(hn, wq_np, ws_np, w_f64=wq_np.astype(np.float64))
+            o.rms_rope(packed, f_np, gq_np, gk_np, heads, rot, eps=block.q_norm.eps)
+            return o.row_linear(packed[:, :inner], wo_np, so_np, residual=xs, gate=tabs[3], labels=labels,
+                                w_f64=wo_np.astype(np.float64))
+
+        rng = np.random.default_rng(0)
+        qa = rng.standard_normal((1, 1, queries, 128)).astype(np.float32)
+        ka, va = (rng.standard_normal((1, 1, m, 128)).astype(np.float32) for _ in range(2))
+
+        def cpu_attention():
+            return oa.attention(oa.prepare(qa, ka, va))
+
+        tc = _cpu_rows_timing(cpu_rows) * m / rows + _cpu_rows_timing(cpu_attention, reps=1) * (m / queries) * heads
+        res['cpu_baseline'] = dict(value=round(ops / tc / 1e12, 6), unit='TOPS', cores=blas_threads(), kind='port',
+                                   sample=f'oracle norm + QKV + rms_rope + gated O projection on {rows} of {m} rows '
+                                          f'(scaled x{m / rows:g}) plus oracle attention for {queries} queries of '
+                                          f'1 head against all {m} keys (scaled x{m / queries * heads:g})')
+    return res
+
+
+WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_attention': run_dit_attention, 'dit_attention_block': run_dit_attention_block, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
              'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv, 'dit_qkv_rope': run_dit_qkv_rope,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
 

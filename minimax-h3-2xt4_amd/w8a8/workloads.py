@@ -37,6 +37,12 @@ SHAPES = {
     # Attention of one DiT rank at the c2 token count: 24 heads of 128.
     'dit_attention': dict(seed=8, m=53504, heads=24),
     'dit_norm': dict(seed=5, m=16384, hidden=3072, mod_rows=9, frames=16, eps=1e-6 / RESIDUAL_DIVISOR ** 2),
+    # The DiT attention sublayer of one rank at the c2 token count: residual
+    # stream (divided by 512) -> norm1 + AdaLN -> QKV 3072 -> 3 x 24 heads of
+    # 128 with RMS-RoPE (96-dim rotary prefix) -> attention -> O 3072 -> 3072
+    # with the gated residual update.
+    'dit_attention_block': dict(seed=9, m=53504, hidden=3072, heads=24, rot_dim=96, mod_rows=9, frames=16,
+                                outliers=3, eps=1e-6 / RESIDUAL_DIVISOR ** 2),
 }
 
 
@@ -160,6 +166,31 @@ def dit_attention(m=None, seed=None):
     m = m or s['m']
     shape = (1, s['heads'], m, 128)
     return {n: torch.randn(shape, generator=g, dtype=torch.float32).half() for n in ('q', 'k', 'v')}
+
+
+def dit_attention_block(m=None, seed=None):
+    """Residual rows (/512), norm1 gain, AdaLN shift/scale/gate tables with
+    per-frame segments, QKV and O weights (fp32, ConvRot-domain), fp16
+    rotation matrices (1, m, 1, rot_dim / 2, 2, 2) and the Q/K norm gains."""
+    s = SHAPES['dit_attention_block']
+    g = torch.Generator().manual_seed(s['seed'] if seed is None else seed)
+    m, hidden, heads = m or s['m'], s['hidden'], s['heads']
+    x = (activations(g, m, hidden, s['outliers']).float() / RESIDUAL_DIVISOR).half()
+    weight = torch.rand((hidden,), generator=g) + 0.5
+    shift, scale, gate = (torch.randn((s['mod_rows'], hidden), generator=g) * 0.1 for _ in range(3))
+    frames = min(s['frames'], m)
+    bounds = [m * i // frames for i in range(frames + 1)]
+    segments = [(bounds[i], bounds[i + 1], i % s['mod_rows']) for i in range(frames) if bounds[i] < bounds[i + 1]]
+    w_qkv = weights(g, 3 * heads * 128, hidden)
+    w_o = weights(g, hidden, heads * 128)
+    half = s['rot_dim'] // 2
+    ang = torch.rand((m, half), generator=g, dtype=torch.float64) * 6.283185307179586
+    c, sn = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack([torch.stack([c, -sn], -1), torch.stack([sn, c], -1)], -2).half().reshape(1, m, 1, half, 2, 2)
+    q_gain = torch.rand(128, generator=g) + 0.5
+    k_gain = torch.rand(128, generator=g) + 0.5
+    return dict(x=x, weight=weight, shift=shift, scale=scale, gate=gate, segments=segments, eps=s['eps'],
+                w_qkv=w_qkv, w_o=w_o, freqs=freqs, q_gain=q_gain, k_gain=k_gain, heads=heads, hidden=hidden)
 
 
 def quantize_weight(w, device):

@@ -10,7 +10,9 @@ compares) and give the GPU tests an input/output set that does not depend on
 running the oracle at test time. Inputs follow the reference's test patterns:
 row tails (benchmarks/test_bounded_column_int8.py:11-28), signed extremes
 (benchmarks/test_te_column_layout.py:28-34), adversarial INT32 values
-(benchmarks/test_tp2_p2_epilogue.py:18-25).
+(benchmarks/test_tp2_p2_epilogue.py:18-25). The later fixtures (gated residual,
+modulated norm + quantize, RMS-RoPE, INT8 attention) draw from a second seeded
+generator so the earlier files stay byte-identical.
 """
 import sys
 from pathlib import Path
@@ -61,6 +63,41 @@ def fixtures():
                            row_f32=o.dequantize_row(acc, ra, wa, 'f32'),
                            col_f16=o.dequantize_column(acc, ra, wa, 'f16', bias),
                            col_bf16=o.dequantize_column(acc, ra, wa, 'bf16'))
+    rng = np.random.default_rng(20261202)
+    # 6. DiT gated residual update in the row epilogue
+    res = (rng.standard_normal((17, 256)) * 0.05).astype(np.float16)
+    gate = rng.standard_normal((3, 256)).astype(np.float32)
+    labels = rng.integers(0, 3, 17).astype(np.int32)
+    branch = o.dequantize_row(acc, ra, wa, 'f16')
+    out['gated'] = dict(acc=acc, a=ra, w=wa, residual=res, gate=gate, labels=labels,
+                        out=o.gated_residual_add(res, branch, gate, labels))
+    # 7. modulated RMSNorm -> ConvRot256 -> INT8 (one zero row, one outlier channel)
+    xn = (rng.standard_normal((13, 512)) * 3).astype(np.float16)
+    xn[5] = 0
+    xn[:, 11] *= 20
+    nw = (rng.random(512) + 0.5).astype(np.float32)
+    shift = (rng.standard_normal((4, 512)) * 0.1).astype(np.float32)
+    scale = (rng.standard_normal((4, 512)) * 0.1).astype(np.float32)
+    nl = rng.integers(0, 4, 13).astype(np.int32)
+    qn, sn, y = o.norm_quantize(xn, nw, shift, scale, nl, eps=1e-6)
+    out['norm_quant'] = dict(x=xn, weight=nw, shift=shift, scale=scale, labels=nl, y=y, q=qn, row_scale=sn)
+    # 8. per-head RMS norm + split-half RoPE of a packed QKV row block (2 heads, rotary prefix 96)
+    packed = (rng.standard_normal((7, 3 * 2 * 128)) * 2).astype(np.float16)
+    ang = rng.random((7, 48)) * 2 * np.pi
+    c, sn_ = np.cos(ang), np.sin(ang)
+    freqs = np.stack([np.stack([c, -sn_], -1), np.stack([sn_, c], -1)], -2).astype(np.float32)
+    gq = (rng.random(128) + 0.5).astype(np.float32)
+    gk = (rng.random(128) + 0.5).astype(np.float32)
+    rq, rk = o.rms_rope(packed, freqs, gq, gk, 2, 96, eps=1e-6)
+    out['rms_rope'] = dict(packed=packed, freqs=freqs, q_gain=gq, k_gain=gk, q=rq, k=rk)
+    # 9. INT8 attention: prepared operands (exact) and the oracle output
+    from oracle import int8_attention as oa
+    qa = rng.standard_normal((1, 2, 37, 128)).astype(np.float16)
+    ka = (rng.standard_normal((1, 2, 70, 128)) + 0.5).astype(np.float16)
+    va = rng.standard_normal((1, 2, 70, 128)).astype(np.float16)
+    prep = oa.prepare(qa.astype(np.float32), ka.astype(np.float32), va.astype(np.float32))
+    out['attention'] = dict(q=qa, k=ka, v=va, **{n: prep[n] for n in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs')},
+                            out=oa.attention(prep, out_dtype='f32'))
     return out
 
 

@@ -52,3 +52,34 @@ def test_kernels_reproduce_golden_fixtures(gpu):
                       'col f16')
     assert_bits_equal(np_of(kernels.dequantize(acc, a, w, epilogue=kernels.EPI_COLUMN, out_dtype=torch.bfloat16)),
                       d['col_bf16'], 'col bf16')
+
+
+@pytest.mark.gpu
+def test_kernels_reproduce_golden_fixtures_of_the_dit_rows(gpu):
+    import torch
+    from helpers import assert_bits_equal, np_of
+    from w8a8 import kernels
+
+    t = lambda a: torch.from_numpy(a).to(gpu)  # noqa: E731
+    d = load('gated')
+    got = kernels.dequantize(t(d['acc']), t(d['a']), t(d['w']), epilogue=kernels.EPI_ROW, residual=t(d['residual']),
+                             gate=t(d['gate']), gate_labels=t(d['labels']))
+    assert_bits_equal(np_of(got), d['out'], 'golden gated residual')
+    d = load('norm_quant')
+    r = kernels.norm_quantize(t(d['x']), t(d['weight']), t(d['shift']), t(d['scale']), t(d['labels']), eps=1e-6,
+                              want_normalized=True)
+    assert_bits_equal(np_of(r['y']), d['y'], 'golden modulated norm')
+    assert_bits_equal(np_of(r['q']), d['q'], 'golden norm codes')
+    assert_bits_equal(np_of(r['scale']).reshape(-1), d['row_scale'], 'golden norm row scales')
+    d = load('rms_rope')
+    q, k = kernels.rms_rope(t(d['packed']), t(d['freqs']), t(d['q_gain']), t(d['k_gain']), heads=2, rot_dim=96,
+                            eps=1e-6)
+    assert_bits_equal(np_of(q), d['q'], 'golden rms_rope q')
+    assert_bits_equal(np_of(k), d['k'], 'golden rms_rope k')
+    d = load('attention')
+    prep = kernels.attention_prepare(t(d['q']), t(d['k']), t(d['v']))
+    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs'):
+        assert_bits_equal(np_of(prep[name]), d[name], f'golden attention {name}')
+    out = np_of(kernels.attention(prep, out_dtype=torch.float32)).astype(np.float64)
+    # the GPU takes the hardware exp2: within 2e-3 of the oracle's output
+    assert np.abs(out - d['out']).max() <= 2e-3 * np.abs(d['out']).max()
