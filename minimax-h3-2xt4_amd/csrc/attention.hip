@@ -221,6 +221,23 @@ __device__ __forceinline__ void lds_dma16(const int8_t* g, int8_t* l) {
 // s_waitcnt vmcnt(0) (loads, including the LDS DMA, have landed).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector-memory
+// operations (LDS DMA included) done; LDS and export counters unconstrained.
+// Workgroup barrier without a memory fence (__syncthreads() would also wait
+// for every outstanding DMA): callers wait for the DMA they need with
+// wait_vm first, and every LDS read before it has been consumed.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 16, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
+}
+
 struct AttnParams {
   const int8_t* q8;
   const float* qs;
@@ -241,7 +258,14 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   // probabilities against it and accumulates P.V and sum(P) in int32. In
   // both, step j issues the scores of block j + 1 before working on block j
   // (the MFMAs run under the VALU work) and DMAs block j + 2.
-  __shared__ __attribute__((aligned(16))) int8_t lds[3][2][kAttnBK * kAttnD];
+  // The ring's three stages are separate arrays: pass 1 names them by
+  // compile-time index, so the compiler sees that the fragment reads of one
+  // stage do not alias a DMA still landing in another and does not wait
+  // for that DMA before them. Pass 2 picks them at run time through lds.
+  __shared__ __attribute__((aligned(16))) int8_t stage0[2][kAttnBK * kAttnD];
+  __shared__ __attribute__((aligned(16))) int8_t stage1[2][kAttnBK * kAttnD];
+  __shared__ __attribute__((aligned(16))) int8_t stage2[2][kAttnBK * kAttnD];
+  auto lds = [&](int st) -> int8_t (*)[kAttnBK * kAttnD] { return st == 0 ? stage0 : st == 1 ? stage1 : stage2; };
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hh = lane >> 5;
   const int64_t bh = blockIdx.y;
@@ -257,7 +281,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + 32 * ds);
   }
   const float qscale = p.qs[bh * p.nq + qrow];
-  const float* ksc = p.ks + bh * p.nblk;
+  // The per-block K scales of the head, staged in LDS (read before the
+  // first DMA) so the block loops issue no vector-memory loads besides the
+  // DMA and their waits can count it exactly.
+  __shared__ float ksc[2048];   // nblk <= 131072 / 64
+  for (int i = tid; i < p.nblk; i += 64 * kAttnWaves) ksc[i] = p.ks[bh * p.nblk + i];
   // Tiles are DMA'd global -> LDS, each wave filling 2 KB of each: K rows
   // are 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7),
   // V^T rows 64 bytes with chunk c at c ^ ((row >> 2) & 3) (the fragment
@@ -269,10 +297,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     for (int u = 0; u < kAttnDma; ++u) {
       const int kb = kAttnDma * wave + u;
       const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
-      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, lds[st][0] + kb * 1024);
+      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, lds(st)[0] + kb * 1024);
       if constexpr (decltype(with_v)::value) {
         const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
-        lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, lds[st][1] + kb * 1024);
+        lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, lds(st)[1] + kb * 1024);
       }
     }
   };
@@ -290,7 +318,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
         sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
       }
   };
-  auto scores = [&](int st, v16i (&sacc)[2]) { scores_at(lds[st][0], sacc); };
+  auto scores = [&](int st, v16i (&sacc)[2]) { scores_at(lds(st)[0], sacc); };
   // K tile of block j DMA'd to dst (the layout of dma_tiles).
   auto dma_k = [&](int j, int8_t* dst) {
 #pragma unroll
@@ -353,37 +381,55 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       if (mx != INT32_MIN) ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
     };
     const int npairs = (p.nblk + 1) / 2;
-    auto dma_pair = [&](int u, int st) {
-      dma_k(2 * u, lds[st][0]);
-      if (2 * u + 1 < p.nblk) dma_k(2 * u + 1, lds[st][1]);
+    // Every pair issues exactly two DMA instructions per wave, so the waits
+    // below count them exactly (the compiler's own wait placement then sees
+    // the same counts): past the last block it re-loads in-range blocks
+    // into a stage whose scores are never computed.
+    auto dma_pair = [&](int u, int8_t (*stg)[kAttnBK * kAttnD]) {
+      const int b0 = 2 * min(u, npairs - 1);
+      dma_k(b0, stg[0]);
+      dma_k(min(b0 + 1, p.nblk - 1), stg[1]);
     };
-    auto pair_scores = [&](int u, int st, v16i (&s0)[2], v16i (&s1)[2]) {
-      scores_at(lds[st][0], s0);
-      if (2 * u + 1 < p.nblk) scores_at(lds[st][1], s1);
+    auto pair_scores = [&](int u, int8_t (*stg)[kAttnBK * kAttnD], v16i (&s0)[2], v16i (&s1)[2]) {
+      scores_at(stg[0], s0);
+      if (2 * u + 1 < p.nblk) scores_at(stg[1], s1);
     };
-    dma_pair(0, 0);
-    if (npairs > 1) dma_pair(1, 1);
-    wait_vmem();
+    // Pair u lives in stage u % 3. Step u computes the scores of pair u + 1,
+    // refills stage u % 3 (whose scores step u - 1 computed) with pair
+    // u + 3, works on pair u, then waits for pair u + 2 only: each DMA has
+    // two steps of lead.
+    dma_pair(0, stage0);
+    dma_pair(1, stage1);
+    dma_pair(2, stage2);
+    wait_vm<2>();   // pairs 0 and 1 landed
     __syncthreads();
     v16i a0[2], a1[2], b0[2], b1[2];
-    pair_scores(0, 0, a0, a1);
-    auto step = [&](int u, int st1, int st2, const v16i (&c0)[2], const v16i (&c1)[2], v16i (&n0)[2],
-                    v16i (&n1)[2]) {
-      if (u + 2 < npairs) dma_pair(u + 2, st2);
-      if (u + 1 < npairs) pair_scores(u + 1, st1, n0, n1);
+    pair_scores(0, stage0, a0, a1);
+    // Step u with pair u in stage s0 and pair u + 1 in stage s1.
+    auto step = [&](int u, int8_t (*s0)[kAttnBK * kAttnD], int8_t (*s1)[kAttnBK * kAttnD],
+                    const v16i (&c0)[2], const v16i (&c1)[2], v16i (&n0)[2], v16i (&n1)[2]) {
+      if (u + 1 < npairs) pair_scores(u + 1, s1, n0, n1);
+      dma_pair(u + 3, s0);
       block_max(2 * u, c0);
       if (2 * u + 1 < p.nblk) block_max(2 * u + 1, c1);
-      wait_vmem();
-      __syncthreads();
+      wait_vm<2>();   // pair u + 2 landed; pair u + 3 may still be in flight
+      lds_barrier();
     };
-    int st = 0, u = 0;
-    for (; u + 1 < npairs; u += 2) {
-      const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
-      step(u, s1, s2, a0, a1, b0, b1);
-      step(u + 1, s2, st, b0, b1, a0, a1);
-      st = s2;
+    // Six steps return to stage 0 and to the first score buffers.
+    int u = 0;
+    for (; u + 6 <= npairs; u += 6) {
+      step(u, stage0, stage1, a0, a1, b0, b1);
+      step(u + 1, stage1, stage2, b0, b1, a0, a1);
+      step(u + 2, stage2, stage0, a0, a1, b0, b1);
+      step(u + 3, stage0, stage1, b0, b1, a0, a1);
+      step(u + 4, stage1, stage2, a0, a1, b0, b1);
+      step(u + 5, stage2, stage0, b0, b1, a0, a1);
     }
-    if (u < npairs) step(u, st == 2 ? 0 : st + 1, st == 0 ? 2 : st - 1, a0, a1, b0, b1);
+    if (u < npairs) step(u, stage0, stage1, a0, a1, b0, b1);
+    if (u + 1 < npairs) step(u + 1, stage1, stage2, b0, b1, a0, a1);
+    if (u + 2 < npairs) step(u + 2, stage2, stage0, a0, a1, b0, b1);
+    if (u + 3 < npairs) step(u + 3, stage0, stage1, b0, b1, a0, a1);
+    if (u + 4 < npairs) step(u + 4, stage1, stage2, a0, a1, b0, b1);
   }
   const float m = fmaxf(ml, __shfl_xor(ml, 32, 64));
   // log2(127) - m, lowered by |m| 2^-22 so that the largest exponent cannot
@@ -424,7 +470,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         const int r = 32 * ct + fr, ck = 2 * t + hh;
-        const v4i vf = *reinterpret_cast<const v4i*>(lds[st][1] + r * kAttnBK + ((ck ^ ((r >> 2) & 3)) << 4));
+        const v4i vf = *reinterpret_cast<const v4i*>(lds(st)[1] + r * kAttnBK + ((ck ^ ((r >> 2) & 3)) << 4));
         oi[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, oi[ct], 0, 0, 0);
       }
     }
