@@ -252,20 +252,21 @@ struct AttnParams {
 
 template <int OUT>
 __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p) {
-  // Three-stage ring of [0: K tile, 64 keys x 128 bytes; 1: V^T tile, 128
-  // channels x 64 bytes]. Two passes over the keys: the first finds each
-  // query's largest logit (K tiles only), the second quantizes the
-  // probabilities against it and accumulates P.V and sum(P) in int32. In
-  // both, step j issues the scores of block j + 1 before working on block j
-  // (the MFMAs run under the VALU work) and DMAs block j + 2.
-  // The ring's three stages are separate arrays: pass 1 names them by
-  // compile-time index, so the compiler sees that the fragment reads of one
-  // stage do not alias a DMA still landing in another and does not wait
-  // for that DMA before them. Pass 2 picks them at run time through lds.
+  // A ring of LDS stages, each [0: K tile, 64 keys x 128 bytes; 1: V^T
+  // tile, 128 channels x 64 bytes]. Two passes over the keys: the first
+  // finds each query's largest logit (K tiles only, two blocks per stage,
+  // three stages), the second quantizes the probabilities against it and
+  // accumulates P.V and sum(P) in int32 (one block per stage, four stages).
+  // In both, a step computes the next block's scores before working on the
+  // current one (the MFMAs run under the VALU work), and every DMA has two
+  // steps to land. The stages are separate arrays named by compile-time
+  // index, so the compiler sees that reads of one stage do not alias a DMA
+  // still landing in another and does not wait for that DMA before them.
   __shared__ __attribute__((aligned(16))) int8_t stage0[2][kAttnBK * kAttnD];
   __shared__ __attribute__((aligned(16))) int8_t stage1[2][kAttnBK * kAttnD];
   __shared__ __attribute__((aligned(16))) int8_t stage2[2][kAttnBK * kAttnD];
-  auto lds = [&](int st) -> int8_t (*)[kAttnBK * kAttnD] { return st == 0 ? stage0 : st == 1 ? stage1 : stage2; };
+  __shared__ __attribute__((aligned(16))) int8_t stage3[2][kAttnBK * kAttnD];
+  using Stage = int8_t (*)[kAttnBK * kAttnD];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hh = lane >> 5;
   const int64_t bh = blockIdx.y;
@@ -292,16 +293,14 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   // reads, 32 rows of one chunk column, are then free of bank conflicts). A
   // DMA lane writes the next 16 bytes of its instruction's kilobyte, so it
   // loads the chunk that lands on its physical position.
-  auto dma_tiles = [&](auto with_v, int j, int st) {
+  auto dma_tiles = [&](int j, Stage stg) {
 #pragma unroll
     for (int u = 0; u < kAttnDma; ++u) {
       const int kb = kAttnDma * wave + u;
       const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
-      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, lds(st)[0] + kb * 1024);
-      if constexpr (decltype(with_v)::value) {
-        const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
-        lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, lds(st)[1] + kb * 1024);
-      }
+      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, stg[0] + kb * 1024);
+      const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
+      lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, stg[1] + kb * 1024);
     }
   };
   // S^T of the K tile at kt: sacc[t][4 g + i] is the score of key
@@ -318,7 +317,6 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
         sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
       }
   };
-  auto scores = [&](int st, v16i (&sacc)[2]) { scores_at(lds(st)[0], sacc); };
   // K tile of block j DMA'd to dst (the layout of dma_tiles).
   auto dma_k = [&](int j, int8_t* dst) {
 #pragma unroll
@@ -330,35 +328,6 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   };
   // Keys of the last block past nk.
   auto masked = [&](int j, int t, int x) { return kAttnBK * j + 32 * t + 8 * (x >> 2) + 4 * hh + (x & 3) >= p.nk; };
-  // One pass over the blocks: prologue (blocks 0 and 1 in stages 0 and 1,
-  // scores of block 0), then work(j, st, cur) per block with the score
-  // buffers swapping without copies.
-  auto run_pass = [&](auto with_v, auto work) {
-    dma_tiles(with_v, 0, 0);
-    if (p.nblk > 1) dma_tiles(with_v, 1, 1);
-    wait_vmem();
-    __syncthreads();
-    v16i sa[2], sb[2];
-    scores(0, sa);
-    auto step = [&](int j, int st, int st1, int st2, const v16i (&cur)[2], v16i (&nxt)[2]) {
-      if (j + 2 < p.nblk) dma_tiles(with_v, j + 2, st2);
-      if (j + 1 < p.nblk) scores(st1, nxt);
-      work(j, st, cur);
-      // Block j + 2 landed, and every wave is done with the stages this
-      // step read before they are refilled.
-      wait_vmem();
-      __syncthreads();
-    };
-    int st = 0, j = 0;
-    for (; j + 1 < p.nblk; j += 2) {
-      const int s1 = st == 2 ? 0 : st + 1, s2 = s1 == 2 ? 0 : s1 + 1;
-      step(j, st, s1, s2, sa, sb);
-      step(j + 1, s1, s2, st, sb, sa);
-      st = s2;
-    }
-    if (j < p.nblk) step(j, st, st == 2 ? 0 : st + 1, st == 0 ? 2 : st - 1, sa, sb);
-  };
-
   // Pass 1: the largest logit of the query, max over blocks of
   // fp32(max(S) * c_j) (the lane's half of the keys, then the other half).
   // It takes two key blocks per step (K only: block 2u in the K half of a
@@ -442,7 +411,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) oi[ct] = v16i{};
   int li = 0;
-  run_pass(std::true_type{}, [&](int j, int st, const v16i (&s)[2]) {
+  auto work = [&](int j, Stage stg, const v16i (&s)[2]) {
     const float c = qscale * ksc[j];
     const bool tail = kAttnBK * (j + 1) > p.nk;
     uint32_t pw[2][4];
@@ -470,11 +439,44 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         const int r = 32 * ct + fr, ck = 2 * t + hh;
-        const v4i vf = *reinterpret_cast<const v4i*>(lds(st)[1] + r * kAttnBK + ((ck ^ ((r >> 2) & 3)) << 4));
+        const v4i vf = *reinterpret_cast<const v4i*>(stg[1] + r * kAttnBK + ((ck ^ ((r >> 2) & 3)) << 4));
         oi[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, oi[ct], 0, 0, 0);
       }
     }
-  });
+  };
+  {
+    // Block j lives in stage j % 4. Step j computes the scores of block
+    // j + 1, refills stage (j + 3) % 4 (read by steps j - 2 and j - 1) with
+    // block j + 3, works on block j, then waits for block j + 2 only. Every
+    // block issues exactly two DMA instructions per wave (past the last
+    // block an in-range block is re-loaded into a stage never read), so the
+    // waits count exactly.
+    auto dma_blk = [&](int j, Stage stg) { dma_tiles(min(j, p.nblk - 1), stg); };
+    dma_blk(0, stage0);
+    dma_blk(1, stage1);
+    dma_blk(2, stage2);
+    wait_vm<2>();   // blocks 0 and 1 landed
+    __syncthreads();
+    v16i sa[2], sb[2];
+    scores_at(stage0[0], sa);
+    auto step = [&](int j, Stage s0, Stage s1, Stage s3, const v16i (&cur)[2], v16i (&nxt)[2]) {
+      if (j + 1 < p.nblk) scores_at(s1[0], nxt);
+      dma_blk(j + 3, s3);
+      work(j, s0, cur);
+      wait_vm<2>();   // block j + 2 landed; block j + 3 may still be in flight
+      lds_barrier();
+    };
+    int j = 0;
+    for (; j + 4 <= p.nblk; j += 4) {
+      step(j, stage0, stage1, stage3, sa, sb);
+      step(j + 1, stage1, stage2, stage0, sb, sa);
+      step(j + 2, stage2, stage3, stage1, sa, sb);
+      step(j + 3, stage3, stage0, stage2, sb, sa);
+    }
+    if (j < p.nblk) step(j, stage0, stage1, stage3, sa, sb);
+    if (j + 1 < p.nblk) step(j + 1, stage1, stage2, stage0, sb, sa);
+    if (j + 2 < p.nblk) step(j + 2, stage2, stage3, stage1, sa, sb);
+  }
   const float l = (float)(li + __shfl_xor(li, 32, 64));
   if (q0 + fr >= p.nq) return;
   const int64_t orow = p.ost.at(bh, q0 + fr);
