@@ -64,40 +64,99 @@ struct AttnPrepParams {
   float* kmean;
 };
 
+// 8 consecutive channels of one token row (16-byte loads).
 template <int DT>
-__device__ __forceinline__ float ld1(const void* base, int64_t i) {
-  if constexpr (DT == kF32) return reinterpret_cast<const float*>(base)[i];
-  else return h2f(reinterpret_cast<const uint16_t*>(base)[i]);
+__device__ __forceinline__ void load8(const void* base, int64_t off, float (&x)[8]) {
+  if constexpr (DT == kF32) {
+    const float4* q = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(base) + off);
+    const float4 a = q[0], b = q[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = h2f((uint16_t)(u[i] & 0xffffu));
+      x[2 * i + 1] = h2f((uint16_t)(u[i] >> 16));
+    }
+  }
 }
 
 // Partial statistics of 256 keys of one (batch, head): the fp32 sum of k
-// (sequential from +0) and the absmax of v, per channel (thread = channel).
+// (sequential from +0) and the absmax of v, per channel. Thread (chunk
+// tid / 16, channels 8 (tid % 16) + [0, 8)) walks its chunk's tokens in
+// order; a workgroup covers 16 chunks.
 template <int DT>
-__global__ __launch_bounds__(128) void attn_stats_kernel(AttnPrepParams p) {
-  const int d = threadIdx.x, chunk = blockIdx.x;
+__global__ __launch_bounds__(256) void attn_stats_kernel(AttnPrepParams p) {
+  const int cg = threadIdx.x & 15, chunk = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int64_t bh = blockIdx.y;
+  if (chunk >= p.chunks) return;
   const int t0 = chunk * kAttnChunk, t1 = min(t0 + kAttnChunk, p.nk);
-  const int64_t kb = p.kst.at(bh, 0) + d, vb = p.vst.at(bh, 0) + d;
-  float s = 0.0f, m = 0.0f;
-  for (int t = t0; t < t1; ++t) {
-    s = s + ld1<DT>(p.k, kb + t * p.kst.t);
-    m = fmaxf(m, fabsf(ld1<DT>(p.v, vb + t * p.vst.t)));
+  const int64_t kb = p.kst.at(bh, 0) + 8 * cg, vb = p.vst.at(bh, 0) + 8 * cg;
+  float s[8], m[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s[i] = m[i] = 0.0f;
+  // Eight tokens' loads are issued before their adds, in token order.
+  int t = t0;
+  for (; t + 8 <= t1; t += 8) {
+    float k[8][8], v[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      load8<DT>(p.k, kb + (t + u) * p.kst.t, k[u]);
+      load8<DT>(p.v, vb + (t + u) * p.vst.t, v[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the sixteen loads ahead of the adds
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        s[i] = s[i] + k[u][i];
+        m[i] = fmaxf(m[i], fabsf(v[u][i]));
+      }
   }
-  const int64_t o = (bh * p.chunks + chunk) * kAttnD + d;
-  p.part_sum[o] = s;
-  p.part_max[o] = m;
+  for (; t < t1; ++t) {
+    float k[8], v[8];
+    load8<DT>(p.k, kb + t * p.kst.t, k);
+    load8<DT>(p.v, vb + t * p.vst.t, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s[i] = s[i] + k[i];
+      m[i] = fmaxf(m[i], fabsf(v[i]));
+    }
+  }
+  const int64_t o = (bh * p.chunks + chunk) * kAttnD + 8 * cg;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p.part_sum[o + i] = s[i];
+    p.part_max[o + i] = m[i];
+  }
 }
 
 // Key mean (the partials added in chunk order, then one division by Nk) and
-// the per-channel V scale.
+// the per-channel V scale. The partials are loaded 16 chunks at a time.
 __global__ __launch_bounds__(128) void attn_finalize_kernel(AttnPrepParams p) {
   const int d = threadIdx.x;
   const int64_t bh = blockIdx.x;
+  const float* ps = p.part_sum + bh * p.chunks * kAttnD + d;
+  const float* pm = p.part_max + bh * p.chunks * kAttnD + d;
   float s = 0.0f, m = 0.0f;
-  for (int c = 0; c < p.chunks; ++c) {
-    const int64_t o = (bh * p.chunks + c) * kAttnD + d;
-    s = s + p.part_sum[o];
-    m = fmaxf(m, p.part_max[o]);
+  int c = 0;
+  for (; c + 16 <= p.chunks; c += 16) {
+    float a[16], b[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      a[u] = ps[(int64_t)(c + u) * kAttnD];
+      b[u] = pm[(int64_t)(c + u) * kAttnD];
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      s = s + a[u];
+      m = fmaxf(m, b[u]);
+    }
+  }
+  for (; c < p.chunks; ++c) {
+    s = s + ps[(int64_t)c * kAttnD];
+    m = fmaxf(m, pm[(int64_t)c * kAttnD]);
   }
   p.kmean[bh * kAttnD + d] = s / (float)p.nk;
   p.vs[bh * kAttnD + d] = row_scale_of(m);
@@ -578,13 +637,13 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   p.kmean = ws + 2 * bh * p.chunks * kAttnD;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   const int qblocks = (p.nq + kAttnBK - 1) / kAttnBK;
-  const dim3 gstat((unsigned)p.chunks, (unsigned)bh), gq((unsigned)max(qblocks, p.nblk), (unsigned)bh);
+  const dim3 gstat((unsigned)((p.chunks + 15) / 16), (unsigned)bh), gq((unsigned)max(qblocks, p.nblk), (unsigned)bh);
   if (a->in_dtype == W8A8_F16) {
-    hipLaunchKernelGGL(attn_stats_kernel<kF16>, gstat, dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_stats_kernel<kF16>, gstat, dim3(256), 0, s, p);
     hipLaunchKernelGGL(attn_finalize_kernel, dim3((unsigned)bh), dim3(128), 0, s, p);
     hipLaunchKernelGGL(attn_quant_kernel<kF16>, gq, dim3(256), 0, s, p);
   } else {
-    hipLaunchKernelGGL(attn_stats_kernel<kF32>, gstat, dim3(128), 0, s, p);
+    hipLaunchKernelGGL(attn_stats_kernel<kF32>, gstat, dim3(256), 0, s, p);
     hipLaunchKernelGGL(attn_finalize_kernel, dim3((unsigned)bh), dim3(128), 0, s, p);
     hipLaunchKernelGGL(attn_quant_kernel<kF32>, gq, dim3(256), 0, s, p);
   }
