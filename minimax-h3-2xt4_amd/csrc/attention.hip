@@ -189,6 +189,37 @@ __device__ __forceinline__ void store32_i8(int8_t* dst, const int (&q)[32]) {
   reinterpret_cast<uint4*>(dst)[1] = w[1];
 }
 
+// 32 consecutive channels of one token row kept as raw 16-byte words, so
+// the loads of several rows can be in flight before any is converted.
+template <int DT>
+struct Raw32 {
+  uint4 w[DT == kF32 ? 8 : 4];
+};
+
+template <int DT>
+__device__ __forceinline__ void load_raw32(const void* base, int64_t off, Raw32<DT>& r) {
+  const uint4* q = reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + off * (DT == kF32 ? 4 : 2));
+#pragma unroll
+  for (int i = 0; i < (DT == kF32 ? 8 : 4); ++i) r.w[i] = q[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack32(const Raw32<DT>& r, float (&x)[32]) {
+#pragma unroll
+  for (int i = 0; i < (DT == kF32 ? 8 : 4); ++i) {
+    const uint32_t u[4] = {r.w[i].x, r.w[i].y, r.w[i].z, r.w[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == kF32) {
+        x[4 * i + j] = __uint_as_float(u[j]);
+      } else {
+        x[8 * i + 2 * j] = h2f((uint16_t)(u[j] & 0xffffu));
+        x[8 * i + 2 * j + 1] = h2f((uint16_t)(u[j] >> 16));
+      }
+    }
+  }
+}
+
 // Block blk of 64 tokens of one (batch, head): thread (token tid / 4, part
 // tid % 4) handles 32 channels. Q rows get their own scale; K rows are
 // centred and share one scale per block; V is quantized with the channel
@@ -202,13 +233,21 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
   const int64_t bh = blockIdx.y;
   const int t = blk * kAttnBK + tl;
   const int c0 = 32 * part;
-  if (blk * kAttnBK < p.nq) {   // workgroup-uniform
-    const bool valid = t < p.nq;
+  // The Q, K and V rows are loaded up front, in the order they are used
+  // (rows past the end re-read the last row and are then ignored).
+  Raw32<DT> rq, rk, rv;
+  load_raw32<DT>(p.q, p.qst.at(bh, min(t, p.nq - 1)) + c0, rq);
+  load_raw32<DT>(p.k, p.kst.at(bh, min(t, p.nk - 1)) + c0, rk);
+  load_raw32<DT>(p.v, p.vst.at(bh, min(t, p.nk - 1)) + c0, rv);
+  // Both phases run in every workgroup (one basic block keeps the three
+  // loads ahead); the stores are masked to the rows that exist.
+  const bool q_blk = blk * kAttnBK < p.nq, k_blk = blk < p.nblk;   // workgroup-uniform
+  {
+    const bool valid = q_blk && t < p.nq;
     float x[32];
-    if (valid) load32<DT>(p.q, p.qst.at(bh, t) + c0, x);
-    else
+    unpack32<DT>(rq, x);
 #pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+    for (int i = 0; i < 32; ++i) x[i] = valid ? x[i] : 0.0f;
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
@@ -223,18 +262,13 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
       if (part == 0) p.qs[bh * p.nq + t] = s * p.c0;
     }
   }
-  if (blk < p.nblk) {   // workgroup-uniform
-    const bool valid = t < p.nk;
+  {
+    const bool valid = k_blk && t < p.nk;
     const float* mean = p.kmean + bh * kAttnD + c0;
     float x[32];
-    if (valid) {
-      load32<DT>(p.k, p.kst.at(bh, t) + c0, x);
+    unpack32<DT>(rk, x);
 #pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = x[i] - mean[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) x[i] = 0.0f;
-    }
+    for (int i = 0; i < 32; ++i) x[i] = valid ? x[i] - mean[i] : 0.0f;
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
@@ -246,11 +280,13 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
     int q[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) q[i] = quant1(x[i], s, rcp);
-    store32_i8(p.k8 + (bh * p.nkp + t) * kAttnD + c0, q);
-    if (tid == 0) p.ks[bh * p.nblk + blk] = s;
+    if (k_blk) {
+      store32_i8(p.k8 + (bh * p.nkp + t) * kAttnD + c0, q);
+      if (tid == 0) p.ks[bh * p.nblk + blk] = s;
+    }
     // V: channel scales, then the tile goes through LDS to be transposed.
     const float* vsc = p.vs + bh * kAttnD + c0;
-    if (valid) load32<DT>(p.v, p.vst.at(bh, t) + c0, x);
+    unpack32<DT>(rv, x);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       const float sv = vsc[i];
@@ -266,7 +302,7 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
       const int key = 8 * ((pos >> 2) & 3) + 4 * (pos >> 4) + (pos & 3);
       vb[pos] = vtile[(32 * gq + key) * kAttnD + ch];
     }
-    store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * gq, vb);
+    if (k_blk) store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * gq, vb);
   }
 }
 
