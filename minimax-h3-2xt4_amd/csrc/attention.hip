@@ -508,7 +508,6 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   int li = 0;
   auto work = [&](int j, Stage stg, const v16i (&s)[2]) {
     const float c = qscale * ksc[j];
-    const bool tail = kAttnBK * (j + 1) > p.nk;
     uint32_t pw[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -517,10 +516,6 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
         float qv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) qv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)s[t][4 * g + i], c, nm));
-        if (tail) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) qv[i] = masked(j, t, 4 * g + i) ? 0.0f : qv[i];
-        }
         // v_cvt_pk_u8_f32 rounds to nearest even and packs the byte.
         uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(qv[0], 0, 0u);
         w = __builtin_amdgcn_cvt_pk_u8_f32(qv[1], 1, w);
@@ -571,6 +566,20 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     if (j < p.nblk) step(j, stage0, stage1, stage3, sa, sb);
     if (j + 1 < p.nblk) step(j + 1, stage1, stage2, stage0, sb, sa);
     if (j + 2 < p.nblk) step(j + 2, stage2, stage3, stage1, sa, sb);
+  }
+  // Keys past nk in the last block have all-zero K and V^T codes: each
+  // scored 0, added nothing to P.V, and added the same byte
+  // cvt_pk_u8(exp2(fma(0, c, nm))) to this lane's sum (as a signed byte,
+  // like every other); take them out exactly.
+  {
+    const int jl = p.nblk - 1, kl = p.nk - kAttnBK * jl;
+    int npad = 0;
+#pragma unroll
+    for (int x = 0; x < 32; ++x) npad += (32 * (x >> 4) + 8 * ((x >> 2) & 3) + 4 * hh + (x & 3)) >= kl;
+    if (npad) {
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(0.0f, qscale * ksc[jl], nm));
+      li -= npad * (int)(int8_t)(__builtin_amdgcn_cvt_pk_u8_f32(e, 0, 0u) & 0xffu);
+    }
   }
   const float l = (float)(li + __shfl_xor(li, 32, 64));
   if (q0 + fr >= p.nq) return;
