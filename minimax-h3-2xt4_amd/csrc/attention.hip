@@ -429,6 +429,15 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   // stage, block 2u + 1 in its V half), halving the barriers.
   float ml = -__builtin_inff();
   {
+    // A full block (every key below nk): no masks, no checks.
+    auto block_max_full = [&](int j, const v16i (&s)[2]) {
+      int mx = INT32_MIN;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) mx = max(mx, s[t][x]);
+      ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
+    };
     auto block_max = [&](int j, const v16i (&s)[2]) {
       int mx = INT32_MIN;
       if (kAttnBK * (j + 1) > p.nk) {
@@ -479,21 +488,36 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       wait_vm<2>();   // pair u + 2 landed; pair u + 3 may still be in flight
       lds_barrier();
     };
+    // The same step for u <= npairs - 3: pairs u and u + 1 are whole and
+    // hold no key past nk (only the last block can), so nothing is checked.
+    auto step_full = [&](int u, int8_t (*s0)[kAttnBK * kAttnD], int8_t (*s1)[kAttnBK * kAttnD],
+                         const v16i (&c0)[2], const v16i (&c1)[2], v16i (&n0)[2], v16i (&n1)[2]) {
+      scores_at(s1[0], n0);
+      scores_at(s1[1], n1);
+      dma_pair(u + 3, s0);
+      block_max_full(2 * u, c0);
+      block_max_full(2 * u + 1, c1);
+      wait_vm<2>();
+      lds_barrier();
+    };
     // Six steps return to stage 0 and to the first score buffers.
     int u = 0;
-    for (; u + 6 <= npairs; u += 6) {
-      step(u, stage0, stage1, a0, a1, b0, b1);
-      step(u + 1, stage1, stage2, b0, b1, a0, a1);
-      step(u + 2, stage2, stage0, a0, a1, b0, b1);
-      step(u + 3, stage0, stage1, b0, b1, a0, a1);
-      step(u + 4, stage1, stage2, a0, a1, b0, b1);
-      step(u + 5, stage2, stage0, b0, b1, a0, a1);
+    for (; u + 8 <= npairs; u += 6) {
+      step_full(u, stage0, stage1, a0, a1, b0, b1);
+      step_full(u + 1, stage1, stage2, b0, b1, a0, a1);
+      step_full(u + 2, stage2, stage0, a0, a1, b0, b1);
+      step_full(u + 3, stage0, stage1, b0, b1, a0, a1);
+      step_full(u + 4, stage1, stage2, a0, a1, b0, b1);
+      step_full(u + 5, stage2, stage0, b0, b1, a0, a1);
     }
+    // At most seven steps remain.
     if (u < npairs) step(u, stage0, stage1, a0, a1, b0, b1);
     if (u + 1 < npairs) step(u + 1, stage1, stage2, b0, b1, a0, a1);
     if (u + 2 < npairs) step(u + 2, stage2, stage0, a0, a1, b0, b1);
     if (u + 3 < npairs) step(u + 3, stage0, stage1, b0, b1, a0, a1);
     if (u + 4 < npairs) step(u + 4, stage1, stage2, a0, a1, b0, b1);
+    if (u + 5 < npairs) step(u + 5, stage2, stage0, b0, b1, a0, a1);
+    if (u + 6 < npairs) step(u + 6, stage0, stage1, a0, a1, b0, b1);
   }
   const float m = fmaxf(ml, __shfl_xor(ml, 32, 64));
   // log2(127) - m, lowered by |m| 2^-22 so that the largest exponent cannot
