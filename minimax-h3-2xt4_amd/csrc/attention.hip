@@ -580,16 +580,26 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       wait_vm<2>();   // block j + 2 landed; block j + 3 may still be in flight
       lds_barrier();
     };
+    // The same step when block j + 1 exists (no check).
+    auto step_full = [&](int j, Stage s0, Stage s1, Stage s3, const v16i (&cur)[2], v16i (&nxt)[2]) {
+      scores_at(s1[0], nxt);
+      dma_blk(j + 3, s3);
+      work(j, s0, cur);
+      wait_vm<2>();
+      lds_barrier();
+    };
     int j = 0;
-    for (; j + 4 <= p.nblk; j += 4) {
-      step(j, stage0, stage1, stage3, sa, sb);
-      step(j + 1, stage1, stage2, stage0, sb, sa);
-      step(j + 2, stage2, stage3, stage1, sa, sb);
-      step(j + 3, stage3, stage0, stage2, sb, sa);
+    for (; j + 5 <= p.nblk; j += 4) {
+      step_full(j, stage0, stage1, stage3, sa, sb);
+      step_full(j + 1, stage1, stage2, stage0, sb, sa);
+      step_full(j + 2, stage2, stage3, stage1, sa, sb);
+      step_full(j + 3, stage3, stage0, stage2, sb, sa);
     }
+    // At most four steps remain.
     if (j < p.nblk) step(j, stage0, stage1, stage3, sa, sb);
     if (j + 1 < p.nblk) step(j + 1, stage1, stage2, stage0, sb, sa);
     if (j + 2 < p.nblk) step(j + 2, stage2, stage3, stage1, sa, sb);
+    if (j + 3 < p.nblk) step(j + 3, stage3, stage0, stage2, sb, sa);
   }
   // Keys past nk in the last block have all-zero K and V^T codes: each
   // scored 0, added nothing to P.V, and added the same byte
