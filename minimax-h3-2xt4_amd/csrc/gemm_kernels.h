@@ -812,7 +812,7 @@ void gemm_i8_persistent(GemmParams p) {
       off_b[j] = (uint32_t)((int64_t)min(tn * kBN + row, p.n - 1) * p.ldb + chunk * 16);
     }
   };
-  int dma_i = 0, dma_ks = ks_begin(item_of(0));
+  int dma_i = 0, dma_ks = ks_begin(item_of(0)), dma_end = ks_end(item_of(0));
   point(0);
   // The ring: unit h (the A tile of global stage h / 2 for even h, its B
   // tile for odd h) goes to slot h % kSlots. A unit is 8 DMA instructions
@@ -820,12 +820,16 @@ void gemm_i8_persistent(GemmParams p) {
   // would stall the issuing wave behind the address unit). The cursor
   // advances after a B tile's second half; past the last stage of the last
   // tile it stays put and re-reads that stage into slots never consumed.
+  // dma_end (the cursor item's last stage + 1) is recomputed only when the
+  // cursor moves to the next item, keeping its divisions out of the stages.
   auto advance = [&]() {
-    if (dma_ks + 1 < ks_end(item_of(dma_i))) {
+    if (dma_ks + 1 < dma_end) {
       ++dma_ks;
     } else if (dma_i + 1 < ntiles) {
       ++dma_i;
-      dma_ks = ks_begin(item_of(dma_i));
+      const int it = item_of(dma_i);
+      dma_ks = ks_begin(it);
+      dma_end = ks_end(it);
       point(dma_i);
     }
   };
