@@ -279,7 +279,7 @@ typedef struct W8A8AttnPrepareArgs {
 
 int w8a8_attention_prepare(const W8A8AttnPrepareArgs* args);
 
-/* Scratch bytes w8a8_attention_prepare needs (key statistics). */
+/* Scratch bytes w8a8_attention_prepare needs (key statistics, V reciprocals). */
 int64_t w8a8_attention_workspace_size(int64_t b, int64_t h, int64_t nk);
 
 typedef struct W8A8AttentionArgs {

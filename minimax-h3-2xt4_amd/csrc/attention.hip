@@ -62,6 +62,7 @@ struct AttnPrepParams {
   float* part_sum;
   float* part_max;
   float* kmean;
+  float* vrcp;   // 1 / vs per channel (IEEE), so tokens do not divide
 };
 
 // 8 consecutive channels of one token row (16-byte loads).
@@ -159,7 +160,9 @@ __global__ __launch_bounds__(128) void attn_finalize_kernel(AttnPrepParams p) {
     m = fmaxf(m, pm[(int64_t)c * kAttnD]);
   }
   p.kmean[bh * kAttnD + d] = s / (float)p.nk;
-  p.vs[bh * kAttnD + d] = row_scale_of(m);
+  const float sv = row_scale_of(m);
+  p.vs[bh * kAttnD + d] = sv;
+  p.vrcp[bh * kAttnD + d] = 1.0f / sv;
 }
 
 // 32 consecutive channels [32 part, 32 part + 32) of token t (16-byte loads).
@@ -286,11 +289,12 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
     }
     // V: channel scales, then the tile goes through LDS to be transposed.
     const float* vsc = p.vs + bh * kAttnD + c0;
+    const float* vrc = p.vrcp + bh * kAttnD + c0;
     unpack32<DT>(rv, x);
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       const float sv = vsc[i];
-      q[i] = valid ? quant1(x[i], sv, 1.0f / sv) : 0;
+      q[i] = valid ? quant1(x[i], sv, vrc[i]) : 0;
     }
     store32_i8(vtile + tl * kAttnD + c0, q);
     __syncthreads();
@@ -673,7 +677,7 @@ static Strides3 strides3(const int64_t (&st)[3], int64_t heads) { return {st[0],
 extern "C" int64_t w8a8_attention_workspace_size(int64_t b, int64_t h, int64_t nk) {
   using namespace w8a8;
   if (b <= 0 || h <= 0 || nk <= 0) return 0;
-  return b * h * (2 * attn_chunks(nk) + 1) * kAttnD * (int64_t)sizeof(float);
+  return b * h * (2 * attn_chunks(nk) + 2) * kAttnD * (int64_t)sizeof(float);
 }
 
 extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
@@ -714,6 +718,7 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   p.part_sum = ws;
   p.part_max = ws + bh * p.chunks * kAttnD;
   p.kmean = ws + 2 * bh * p.chunks * kAttnD;
+  p.vrcp = p.kmean + bh * kAttnD;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   const int qblocks = (p.nq + kAttnBK - 1) / kAttnBK;
   const dim3 gstat((unsigned)((p.chunks + 15) / 16), (unsigned)bh), gq((unsigned)max(qblocks, p.nblk), (unsigned)bh);

@@ -113,7 +113,7 @@ def test_gemm_rope_epilogue_checks():
 
 def test_attention_argument_checks():
     lib = _abi.load()
-    assert lib.w8a8_attention_workspace_size(1, 2, 300) == 2 * (2 * 2 + 1) * 128 * 4
+    assert lib.w8a8_attention_workspace_size(1, 2, 300) == 2 * (2 * 2 + 2) * 128 * 4
     assert lib.w8a8_attention_workspace_size(0, 2, 300) == 0
     base = dict(struct_size=ctypes.sizeof(_abi.AttnPrepareArgs), in_dtype=_abi.F16, q=4096, k=8192, v=12288, b=1,
                 h=2, nq=100, nk=300, d=128, sm_scale=0.088, q8=16384, qs=20480, k8=24576, ks=28672, vt8=32768,
