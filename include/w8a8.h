@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 9
+#define W8A8_ABI_VERSION 10
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -74,6 +74,11 @@ typedef enum w8a8_epilogue {
  * row_max: optional [rows] external absmax (e.g. a global maximum over
  *   tensor-parallel owners); NULL computes the row's own absmax.
  * q: [rows, cols] int8, row stride ldq. scale: [rows] fp32.
+ * row_max_out: optional [rows] fp32, receives the row's own absmax of the
+ *   (rotated) values: the local maximum a tensor-parallel owner contributes
+ *   to the MAX exchange (patches/tilelang_row_quant.py:49-62 maximum_kernel,
+ *   :136-146). Requires row_max == NULL. With q == scale == NULL only the
+ *   maximum is computed (the maximum phase).
  * Requirements: cols % 16 == 0 (cols % 256 == 0 with convrot), x, q 16-byte
  *   aligned, ldx * elem and ldq multiples of 16 bytes.
  */
@@ -91,6 +96,7 @@ typedef struct W8A8QuantArgs {
   int64_t ldq;
   float* scale;
   void* stream;
+  float* row_max_out;
 } W8A8QuantArgs;
 
 int w8a8_quantize_rows(const W8A8QuantArgs* args);

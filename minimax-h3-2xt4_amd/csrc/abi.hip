@@ -17,7 +17,7 @@ void set_error(const char* fmt, ...) {
 
 }  // namespace w8a8
 
-static_assert(sizeof(W8A8QuantArgs) == 88, "W8A8QuantArgs layout");
+static_assert(sizeof(W8A8QuantArgs) == 96, "W8A8QuantArgs layout");
 static_assert(sizeof(W8A8SwigluArgs) == 96, "W8A8SwigluArgs layout");
 static_assert(sizeof(W8A8GemmArgs) == 192, "W8A8GemmArgs layout");
 static_assert(sizeof(W8A8RopeEpilogue) == 48, "W8A8RopeEpilogue layout");

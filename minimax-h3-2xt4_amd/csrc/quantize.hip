@@ -24,7 +24,7 @@ template <int DT, int ROT, int J>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t cols,
     const float* __restrict__ row_max, int8_t* __restrict__ q, int64_t ldq,
-    float* __restrict__ scale) {
+    float* __restrict__ scale, float* __restrict__ row_max_out) {
   __shared__ float lds[ROT ? kQuantWaves * 1024 : 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + wave;
@@ -67,6 +67,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
       }
     }
     amax = row_max ? row_max[row] : wave_max(amax);
+    if (row_max_out != nullptr && lane == 0) row_max_out[row] = amax;
+    if (q == nullptr) return;  // maximum phase only
     const float s = row_scale_of(amax);
     const float rcp = 1.0f / s;
 #pragma unroll
@@ -91,6 +93,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
       }
       amax = wave_max(amax);
     }
+    if (row_max_out != nullptr && lane == 0) row_max_out[row] = amax;
+    if (q == nullptr) return;  // maximum phase only
     const float s = row_scale_of(amax);
     const float rcp = 1.0f / s;
     for (int j = 0; j < jcount; ++j) {
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
 template <int DT, int ROT, int J>
 __global__ __launch_bounds__(256) void quantize_row_wg_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t cols, const float* __restrict__ row_max,
-    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, float* __restrict__ row_max_out) {
   __shared__ float lds[ROT ? 4 * 1024 : 1];
   __shared__ float wmax[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -142,6 +146,8 @@ __global__ __launch_bounds__(256) void quantize_row_wg_kernel(
   if (lane == 0) wmax[wave] = amax;
   __syncthreads();
   amax = row_max ? row_max[row] : fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (row_max_out != nullptr && tid == 0) row_max_out[row] = amax;
+  if (q == nullptr) return;  // maximum phase only
   const float s = row_scale_of(amax);
   const float rcp = 1.0f / s;
 #pragma unroll
@@ -168,7 +174,7 @@ static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
     const dim3 g((unsigned)a->rows), b(256);
 #define W8A8_WLAUNCH(JJ)                                                                              \
   hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, JJ>), g, b, 0, stream, a->x, a->ldx, a->cols, \
-                     a->row_max, a->q, a->ldq, a->scale)
+                     a->row_max, a->q, a->ldq, a->scale, a->row_max_out)
     switch (jw) {
       case 1: W8A8_WLAUNCH(1); break;
       case 2: W8A8_WLAUNCH(2); break;
@@ -184,7 +190,7 @@ static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
   const dim3 block(64 * kQuantWaves);
 #define W8A8_QLAUNCH(JJ)                                                                      \
   hipLaunchKernelGGL((quantize_rows_kernel<DT, ROT, JJ>), grid, block, 0, stream, a->x, a->ldx, \
-                     a->rows, a->cols, a->row_max, a->q, a->ldq, a->scale)
+                     a->rows, a->cols, a->row_max, a->q, a->ldq, a->scale, a->row_max_out)
   switch (jneed) {
     case 1: W8A8_QLAUNCH(1); break;
     case 2: W8A8_QLAUNCH(2); break;
@@ -217,9 +223,15 @@ extern "C" int w8a8_quantize_rows(const W8A8QuantArgs* a) {
     W8A8_REQUIRE(a->cols != 0 || a->rows == 0, "w8a8_quantize_rows: zero-width rows have no scale");
     return W8A8_OK;
   }
-  W8A8_REQUIRE(a->x && a->q && a->scale, "w8a8_quantize_rows: null buffer");
-  W8A8_REQUIRE(a->ldx >= a->cols && a->ldq >= a->cols, "w8a8_quantize_rows: leading dimension below cols");
-  W8A8_REQUIRE(aligned16(a->x) && aligned16(a->q) && (a->ldx * es) % 16 == 0 && a->ldq % 16 == 0,
+  W8A8_REQUIRE(a->x != nullptr, "w8a8_quantize_rows: null x");
+  W8A8_REQUIRE((a->q == nullptr) == (a->scale == nullptr), "w8a8_quantize_rows: q and scale go together");
+  W8A8_REQUIRE(a->q != nullptr || a->row_max_out != nullptr, "w8a8_quantize_rows: no output requested");
+  W8A8_REQUIRE(a->row_max_out == nullptr || a->row_max == nullptr,
+               "w8a8_quantize_rows: row_max_out reports the row's own maximum (no external row_max)");
+  W8A8_REQUIRE(a->ldx >= a->cols && (a->q == nullptr || a->ldq >= a->cols),
+               "w8a8_quantize_rows: leading dimension below cols");
+  W8A8_REQUIRE(aligned16(a->x) && (a->ldx * es) % 16 == 0 &&
+               (a->q == nullptr || (aligned16(a->q) && a->ldq % 16 == 0)),
                "w8a8_quantize_rows: x/q must be 16-byte aligned with 16-byte row strides");
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
   W8A8_REQUIRE(a->round_rotated == 0 || a->round_rotated == 1, "w8a8_quantize_rows: round_rotated must be 0 or 1");

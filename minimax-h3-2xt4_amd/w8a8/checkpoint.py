@@ -73,9 +73,10 @@ def plan(reader, kind, index, rank=0, world_size=1):
     column projections (``components`` equal chunks, each split in
     ``world_size`` contiguous parts), K halves for row projections (K must
     divide into whole 256-channel ConvRot groups per rank), replicated norms
-    and AdaLN tensors. Raises ValueError on a dtype, shape or metadata name the
-    layout does not allow, and on tensors under the block prefix that the
-    layout does not know.
+    and AdaLN tensors (all required). Raises ValueError on a dtype, shape or
+    metadata name the layout does not allow, on a missing tensor, on shapes
+    that do not form one block geometry, and on tensors under the block
+    prefix that the layout does not know.
     """
     if world_size not in (1, 2) or not 0 <= rank < world_size:
         raise ValueError('world_size 1 or 2 and a rank below it required')
@@ -87,9 +88,10 @@ def plan(reader, kind, index, rank=0, world_size=1):
         raise ValueError('Only TE and DiT blocks are supported')
     result, known = [], set()
     for target, source in replicated.items():
-        if prefix + source in reader.header:
-            result.append((target, prefix + source, None, None))
-            known.add(prefix + source)
+        if prefix + source not in reader.header:
+            raise ValueError('Missing replicated block tensor: ' + prefix + source)
+        result.append((target, prefix + source, None, None))
+        known.add(prefix + source)
     quant_names = []
     for target, (source, components) in linears.items():
         for suffix in ('weight', 'weight_scale'):
@@ -125,7 +127,52 @@ def plan(reader, kind, index, rank=0, world_size=1):
     unexpected = {n for n in reader.header if n.startswith(prefix)} - known
     if unexpected:
         raise ValueError('Unqualified Native block metadata/tensors: ' + str(sorted(unexpected)))
+    _check_geometry(reader, kind, prefix, linears, replicated)
     return result, quant_names
+
+
+def _check_geometry(reader, kind, prefix, linears, replicated):
+    """The block's tensors must agree with one transformer geometry (the
+    reference checks them against its TP module shells,
+    patches/rank_local_int8.py:84-90): hidden size from the first column
+    projection's K, 128-wide heads, FFN widths that pair up."""
+    def shape(target):
+        if target in linears:
+            return reader.header[prefix + linears[target][0] + '.weight']['shape']
+        return reader.header[prefix + replicated[target]]['shape']
+
+    def need(ok, target):
+        if not ok:
+            name = prefix + (linears[target][0] + '.weight' if target in linears else replicated[target])
+            raise ValueError('Checkpoint shape differs from Native TP configuration: ' + name)
+
+    head = 128
+    if kind == 'dit':
+        hidden = shape('qkv_proj')[1]
+        inner = shape('out_proj')[1]
+        need(shape('qkv_proj')[0] == 3 * inner and inner % head == 0, 'qkv_proj')
+        need(shape('out_proj')[0] == hidden, 'out_proj')
+        need(shape('fc1')[1] == hidden and shape('fc1')[0] % 2 == 0, 'fc1')
+        need(shape('fc2') == [hidden, shape('fc1')[0] // 2], 'fc2')
+        for n in ('norm1.weight', 'norm2.weight'):
+            need(shape(n) == [hidden], n)
+        for n in ('q_norm.weight', 'k_norm.weight'):
+            need(shape(n) == [head], n)
+        w, b = shape('adaln_proj.weight'), shape('adaln_proj.bias')
+        need(len(w) == 2 and w[0] == 18 * hidden, 'adaln_proj.weight')
+        need(b == [18 * hidden], 'adaln_proj.bias')
+    else:
+        hidden = shape('q_proj')[1]
+        for n in ('q_proj', 'k_proj', 'v_proj', 'gate_proj', 'up_proj'):
+            need(shape(n)[1] == hidden and shape(n)[0] % head == 0, n)
+        need(shape('k_proj')[0] == shape('v_proj')[0], 'v_proj')
+        need(shape('o_proj') == [hidden, shape('q_proj')[0]], 'o_proj')
+        need(shape('up_proj')[0] == shape('gate_proj')[0], 'up_proj')
+        need(shape('down_proj') == [hidden, shape('gate_proj')[0]], 'down_proj')
+        for n in ('input_layernorm.weight', 'post_attention_layernorm.weight'):
+            need(shape(n) == [hidden], n)
+        for n in ('q_norm.weight', 'k_norm.weight'):
+            need(shape(n) == [head], n)
 
 
 class INT8Block(nn.Module):
@@ -186,7 +233,11 @@ def load_block(source, kind, index, *, rank=0, world_size=1, device=None):
         m.weight.data.copy_(w)
         m.weight_scale.data.copy_(s)
         projections[target] = m
-    replicated = {t: tensors[t].to(device) for t in tensors if not t.split('.')[0] in linears}
+    # Replicated tensors take the dtype of the reference's module shells
+    # (patches/rank_local_int8.py:12-15,108-109): FP32 for the DiT, FP16 for
+    # the text encoder.
+    dtype = torch.float32 if kind == 'dit' else torch.float16
+    replicated = {t: tensors[t].to(device=device, dtype=dtype) for t in tensors if not t.split('.')[0] in linears}
     return INT8Block(kind, projections, replicated, metadata).eval().requires_grad_(False)
 
 

@@ -91,12 +91,33 @@ def row_linear(module, x, fallback, comm, input_act=None, residual=None, gate=No
     return out
 
 
+def adjacent_cat(gate, up):
+    """cat((gate, up), -1), without a copy when up directly follows gate in
+    the columns of one buffer (project_columns' packed output)."""
+    g2 = gate.reshape(-1, gate.shape[-1])
+    u2 = up.reshape(-1, up.shape[-1])
+    w = g2.shape[1]
+    if (g2.stride(1) == 1 and u2.stride(1) == 1 and g2.stride(0) == u2.stride(0)
+            and u2.data_ptr() == g2.data_ptr() + w * g2.element_size()
+            and g2.untyped_storage().data_ptr() == u2.untyped_storage().data_ptr()):
+        return g2.as_strided((g2.shape[0], 2 * w), (g2.stride(0), 1)).view(*gate.shape[:-1], 2 * w)
+    return torch.cat((gate, up), -1)
+
+
 def row_linear_parts(module, gate, up, fallback, comm):
-    """TE down projection from separate gate/up halves (h3_operator_policy.py:240-255)."""
+    """TE down projection from separate gate/up halves (h3_operator_policy.py:240-255).
+
+    With a fused FC2 quantizer (and a non-native row backend) the halves are
+    concatenated and run through the fused FP32 SwiGLU route; only that route
+    requires matching halves. Otherwise the product silu(gate) * up is formed
+    in the halves' own dtype (torch's elementwise ops, with their storage
+    rounding and FP16 overflow, as the reference's eager fallback) and the
+    row projection runs with no input activation.
+    """
     policy = getattr(module, 'operator_policy', None)
-    if gate.shape != up.shape or gate.dtype != up.dtype or gate.device != up.device:
-        raise ValueError('Matching gate/up required')
     if (policy is not None and policy.row_linear_backend != 'native'
             and policy.fc2_quantizer in ('fused_stored', 'fused_recompute')):
-        return row_linear(module, torch.cat((gate, up), -1), fallback, comm, 'swiglu')
-    return row_linear(module, torch.cat((gate, up), -1).float(), fallback, comm, 'swiglu')
+        if gate.shape != up.shape or gate.dtype != up.dtype or gate.device != up.device:
+            raise ValueError('Matching gate/up required')
+        return row_linear(module, adjacent_cat(gate, up), fallback, comm, 'swiglu')
+    return row_linear(module, torch.nn.functional.silu(gate) * up, fallback, comm)

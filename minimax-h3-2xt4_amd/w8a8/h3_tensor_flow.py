@@ -1,11 +1,16 @@
 """FP16-fix tensor flow: residual divisor folding and the residual updates.
 
 Mirrors the linear-path parts of patches/h3_tensor_flow.py: TensorFlowPolicy
-(:16-37), fold_linear (:82-103; the divisor goes into the FP32 INT8 weight
-scales of the row projections), prepare_tp (:114-127, projection folds),
+(:16-37), StableNorm / stable_norms (:48-79), fold_linear (:82-103; the
+divisor goes into the FP32 INT8 weight scales of the row projections),
+prepare_tp (:114-127: projection folds, StableNorm, norm eps / c**2),
 residual_add (:130-131), modulated_norm (:134-142) and gated_add
 (:145-152), plus the DiT modulation segment -> row-label map of
 patches/tilelang_dit_fusion.py:93-124.
+
+For residual rows stored as y = x / c, an RMSNorm with eps / c**2 gives the
+same normalized rows as the unscaled stream with eps: with c a power of two
+every scaling step is exact in fp32, so the fold changes no bit.
 """
 from dataclasses import dataclass
 
@@ -42,6 +47,52 @@ class TensorFlowPolicy:
         return float(2 ** self.residual_exponent)
 
 
+class StableNorm(nn.Module):
+    """FP32 statistics, gain and epsilon, then the activation storage cast
+    (patches/h3_tensor_flow.py:48-69). ``eps`` is the wrapped norm's epsilon
+    divided by divisor**2. RMSNorm only: the LayerNorm variant belongs to
+    the vision/VAE paths this build leaves out.
+
+    Calling it on 16-bit rows on the GPU runs the library's RMSNorm kernel
+    (fixed-order fp32 sum of squares, IEEE sqrt and division); FP32 rows run
+    torch's F.rms_norm in fp32, the reference's own expression. The DiT
+    sublayers read ``weight`` and ``eps`` from it and fuse the norm into the
+    next projection's quantization.
+    """
+
+    def __init__(self, norm, divisor=1.):
+        super().__init__()
+        if 'LayerNorm' in type(norm).__name__ or getattr(norm, 'layer_norm', False):
+            raise ValueError('StableNorm here wraps RMSNorm modules only')
+        self.weight = norm.weight
+        self.normalized_shape = tuple(norm.normalized_shape)
+        eps = norm.eps if norm.eps is not None else torch.finfo(torch.float32).eps
+        self.eps = float(eps) / (divisor * divisor)
+        self.layer_norm = False
+
+    def forward(self, x):
+        if x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and len(self.normalized_shape) == 1:
+            weight = self.weight.detach().to(device=x.device, dtype=torch.float32) if self.weight is not None \
+                else None
+            flat = x.reshape(-1, x.shape[-1])
+            y = kernels.norm_quantize(flat, weight, eps=self.eps, quantize=False)['y']
+            return y.reshape(x.shape)
+        weight = self.weight.to(device=x.device, dtype=torch.float32) if self.weight is not None else None
+        return torch.nn.functional.rms_norm(x.float(), self.normalized_shape, weight, self.eps).to(x.dtype)
+
+
+def stable_norms(module):
+    """Replace every norm child (anything with normalized_shape and eps) by
+    a StableNorm, recursively (patches/h3_tensor_flow.py:72-79)."""
+    for name, child in list(module.named_children()):
+        if isinstance(child, StableNorm):
+            continue
+        if hasattr(child, 'normalized_shape') and hasattr(child, 'eps'):
+            setattr(module, name, StableNorm(child))
+        else:
+            stable_norms(child)
+
+
 def fold_linear(module, divisor):
     """Divide the FP32 INT8 weight scale (and any bias) by the divisor once.
 
@@ -57,16 +108,30 @@ def fold_linear(module, divisor):
 
 
 def prepare_tp(block, kind, policy):
-    """Fold the divisor into the row projections of a block (linear part of :114-127)."""
+    """Prepare a block for the scaled residual flow (patches/h3_tensor_flow.py:114-127).
+
+    Folds the divisor c into the row projections (out_proj/fc2 for DiT,
+    o_proj/down_proj for TE), installs StableNorm in place of every norm,
+    and divides the eps of the residual-stream norms (norm1/norm2 for DiT,
+    input_layernorm/post_attention_layernorm for TE) by c**2. A sub-block
+    that holds only some of these (e.g. an FFN sublayer, whose norm the
+    caller passes in) gets the folds for what it holds.
+    """
     if not policy.enabled:
         return block
     if hasattr(block, 'tensor_flow'):
         raise ValueError('Tensor flow already prepared')
     block.tensor_flow = policy
+    c = policy.divisor
     for name in (('o_proj', 'down_proj') if kind == 'te' else ('out_proj', 'fc2')):
         module = getattr(block, name, None)
         if module is not None:
-            fold_linear(module, policy.divisor)
+            fold_linear(module, c)
+    stable_norms(block)
+    for name in (('input_layernorm', 'post_attention_layernorm') if kind == 'te' else ('norm1', 'norm2')):
+        norm = getattr(block, name, None)
+        if norm is not None:
+            norm.eps /= c * c
     return block
 
 

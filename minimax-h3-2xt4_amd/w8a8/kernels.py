@@ -52,7 +52,6 @@ def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=Non
     row_max [M] (or [M,1]) fp32 replaces the row's own absmax.
     """
     x = _rows_2d(x)
-    _device(x, row_max)
     if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError('x must be float16, bfloat16 or float32')
     rows, cols = x.shape
@@ -60,6 +59,15 @@ def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=Non
         raise ValueError('ConvRot group size must divide input features')
     if cols % 16:
         raise ValueError('input features must be a multiple of 16')
+    if out is not None:
+        if (out.dtype != torch.int8 or out.ndim != 2 or tuple(out.shape) != (rows, cols) or out.stride(1) != 1
+                or out.stride(0) < cols or out.stride(0) % 16 or out.data_ptr() % 16):
+            raise ValueError(f'out must be int8 [{rows}, {cols}] with unit column stride and 16-byte aligned rows')
+    if scale_out is not None:
+        if (scale_out.dtype != torch.float32 or tuple(scale_out.shape) not in ((rows, 1), (rows,))
+                or (rows > 1 and scale_out.stride(0) != 1)):
+            raise ValueError(f'scale_out must be contiguous float32 [{rows}, 1]')
+    _device(x, row_max, out, scale_out)
     q = out if out is not None else torch.empty((rows, cols), dtype=torch.int8, device=x.device)
     scale = scale_out if scale_out is not None else torch.empty((rows, 1), dtype=torch.float32, device=x.device)
     if row_max is not None:
@@ -74,6 +82,32 @@ def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=Non
                           stream=_abi.stream_of(x))
     _abi.call('w8a8_quantize_rows', args)
     return q, scale
+
+
+def row_absmax(x, *, convrot=False, round_rotated=True):
+    """Maximum phase of quantize_rows: fp32 [M, 1] row absmax of x [M, K]
+    (after ConvRot256 when convrot), the value a tensor-parallel owner of a
+    K slice contributes to the MAX exchange before quantizing with the
+    global maximum (quantize_rows(row_max=...)). No codes are written.
+    """
+    x = _rows_2d(x)
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError('x must be float16, bfloat16 or float32')
+    rows, cols = x.shape
+    if (convrot and cols % 256) or cols % 16:
+        raise ValueError('input features must be a multiple of 16 (256 with ConvRot256)')
+    _device(x)
+    res = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
+    if rows == 0:
+        return res
+    if cols == 0:
+        return res.zero_()
+    args = _abi.QuantArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows, cols=cols,
+                          convrot=256 if convrot else 0, round_rotated=1 if round_rotated else 0,
+                          row_max=None, q=None, ldq=0, scale=None, stream=_abi.stream_of(x),
+                          row_max_out=res.data_ptr())
+    _abi.call('w8a8_quantize_rows', args)
+    return res
 
 
 def _table(t, name, cols):
@@ -237,8 +271,11 @@ def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dty
         if bias is not None or residual is not None:
             raise ValueError('raw int32 output takes no bias or residual')
         out = out if out is not None else torch.empty((m, n), dtype=torch.int32, device=device)
-        if out.dtype != torch.int32:
-            raise ValueError('int32 output required')
+        if out.dtype != torch.int32 or tuple(out.shape) != (m, n) or out.stride(-1) != 1 or out.stride(0) < n:
+            raise ValueError(f'out must be int32 [{m}, {n}] with unit column stride')
+        _device(out)
+        if out.device != device:
+            raise ValueError('all tensors must be on the same device')
         if gate is not None:
             raise ValueError('raw int32 output takes no gate')
         return dict(row_scale=None, col_scale=None, col_scale_stride=0, bias=None, bias_dtype=0,
@@ -285,10 +322,13 @@ def _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dty
         keep += [gate, gate_labels]
     elif gate_labels is not None:
         raise ValueError('gate_labels without a gate')
-    _device(a, w, bias, residual, gate, gate_labels)
-    out = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=device)
-    if out.dtype != out_dtype or out.shape != (m, n) or out.stride(-1) != 1:
+    if out is not None and (out.dtype != out_dtype or out.shape != (m, n) or out.stride(-1) != 1
+                            or out.stride(0) < n):
         raise ValueError('out must be [M, N] of out_dtype with unit column stride')
+    _device(a, w, bias, residual, gate, gate_labels, out)
+    if a.device != device:
+        raise ValueError('all tensors must be on the same device')
+    out = out if out is not None else torch.empty((m, n), dtype=out_dtype, device=device)
     return dict(row_scale=a.data_ptr(), col_scale=w.data_ptr(), col_scale_stride=wstride,
                 bias=_abi.ptr(bias), bias_dtype=bias_dtype, out_dtype=_abi.DTYPE_CODE[out_dtype],
                 residual=_abi.ptr(residual), ldr=ldr, gate=_abi.ptr(gate), gate_labels=_abi.ptr(gate_labels),
@@ -361,7 +401,6 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
         raise ValueError('weight must be 2-D [N, K]')
     if weight.stride(-1) != 1:
         weight = weight.contiguous()
-    _device(q, weight)
     if q.dtype != torch.int8 or weight.dtype != torch.int8:
         raise ValueError('int8 operands required')
     m, k = q.shape
@@ -372,6 +411,7 @@ def gemm(q, weight, *, epilogue=EPI_INT32, row_scale=None, col_scale=None, bias=
         raise ValueError('K and the operand row strides must be multiples of 16')
     fields, out, keep = _epilogue_args(m, n, epilogue, row_scale, col_scale, bias, residual, out_dtype, out,
                                        q.device, gate, gate_labels)
+    _device(q, weight, out)
     if m == 0 or n == 0:
         return out
     rope_args = None

@@ -31,6 +31,11 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   activation and the weight rows alike leaves x.W^T unchanged (H H^T = I),
   so the result tracks float64 x.W^T within the INT8 error, which a
   rotation missing on either side fails.
+* ``row_partial``, ``rank_row_max`` - the sharding identity: over two
+  rank halves (whole 256-channel groups each) the maximum of the ranks'
+  row maxima equals the unsharded row maximum, and the ranks' int32
+  partials quantized with it add up exactly to the unsharded accumulator;
+  a wrong K slice, a wrong gate/up pairing or a local maximum fails it.
 * ``fma_f32``           - exact rational arithmetic (fractions) on random
   and constructed midpoint cases, where the unfused a*b+c rounds differently.
 * ``gated_residual_add`` - composition of fma_f32 with the FP16 branch and
@@ -73,5 +78,5 @@ from .w8a8_oracle import (  # noqa: F401
     dequantize_column, residual_add, to_bf16_bits, from_bf16_bits,
     cast_out, quantize_weight, column_linear, row_linear, row_linear_fc2, ffn_block,
     fma_f32, gated_residual_add, rms_sum_squares, modulated_rms_norm,
-    norm_quantize, head_sum_squares, rms_rope,
+    norm_quantize, head_sum_squares, rms_rope, row_partial, rank_row_max,
 )

@@ -542,6 +542,36 @@ def row_linear(x, wq, ws, residual=None, out_dtype='f16', x_dtype='f16', w_f64=N
     return residual_add(residual, branch)
 
 
+def row_partial(x, wq, row_max=None, swiglu=False, x_dtype='f16', w_f64=None):
+    """One tensor-parallel rank's row projection before the SUM exchange.
+
+    x is the rank's input: its K slice, or with ``swiglu`` its [gate_r |
+    up_r] halves. Follows patches/tilelang_swiglu_quant.py:67-92 (prologue,
+    then the quantizer with the MAX-exchanged row maximum) and, without
+    SwiGLU, patches/tilelang_row_quant.py:114-146 / optimized_tp.py:53-87
+    (FP32 ConvRot256 of the owned slice, external-maximum quantizer); then
+    int_mm against the rank's weight columns (parallel_int8.py:86-91, before
+    its all_reduce). ``row_max`` None uses the rank's own maximum.
+    Returns (acc int32 [M, N], a fp32 [M]); the FP32 partial of the rank
+    alone is dequantize_row(acc, a, ws, 'f32').
+    """
+    if swiglu:
+        q, a, _ = fc2_prologue(x, row_max=row_max, x_dtype=x_dtype)
+    else:
+        xf = _to_f32(x, x_dtype)
+        q, a = quantize_rows(convrot256(xf).reshape(-1, xf.shape[-1]), row_max)
+    return int_mm(q, wq, w_f64), a
+
+
+def rank_row_max(x, swiglu=False, x_dtype='f16'):
+    """A rank's own row maximum, the MAX exchange's input (fp32 [M]): the
+    absmax of ConvRot256(SwiGLU) or of the FP32 ConvRot256 of its slice."""
+    xf = _to_f32(x, x_dtype)
+    if swiglu:
+        return fc2_prologue(xf, x_dtype='f32')[2].max(-1)
+    return np.abs(convrot256(xf).reshape(-1, xf.shape[-1])).max(-1).astype(np.float32)
+
+
 def ffn_block(h, w1q, ws1, w2q, ws2, residual, convrot=True, w1_f64=None, w2_f64=None, gate=None, labels=None):
     """DiT FFN block of the FP16-fix flow on one GPU.
 

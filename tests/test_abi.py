@@ -35,7 +35,7 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [88, 96, 192, 144, 144, 104, 216, 136]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [96, 96, 192, 144, 144, 104, 216, 136]
     assert ctypes.sizeof(_abi.RopeEpilogue) == 48   # static_assert'ed in the library too
 
 
@@ -60,7 +60,11 @@ def test_quantize_argument_checks():
                     'multiple of 16')
     _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'x': 4097}), 'aligned')
     _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'ldx': 100}), 'leading dimension')
-    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'scale': None}), 'null buffer')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'scale': None}), 'go together')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'x': None}), 'null x')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'q': None, 'scale': None}), 'no output')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'row_max': 4096, 'row_max_out': 4096}),
+                    'own maximum')
 
 
 def test_gemm_argument_checks():

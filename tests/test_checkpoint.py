@@ -16,7 +16,8 @@ def _dit_weights(g, hidden=512, ffn=1024):
                'fc2': q(hidden, ffn)}
     rep = {'norm1.weight': torch.rand(hidden, generator=g), 'norm2.weight': torch.rand(hidden, generator=g),
            'q_norm.weight': torch.rand(128, generator=g), 'k_norm.weight': torch.rand(128, generator=g),
-           'adaln_proj.weight': torch.randn((6 * hidden, 256), generator=g), 'adaln_proj.bias': torch.randn(6 * hidden, generator=g)}
+           'adaln_proj.weight': torch.randn((18 * hidden, 8), generator=g),
+           'adaln_proj.bias': torch.randn(18 * hidden, generator=g)}
     return weights, rep
 
 
@@ -96,12 +97,47 @@ def test_te_block_layout(tmp_path):
     h, f = 512, 1024
     weights = {'q_proj': q(h, h), 'k_proj': q(h // 2, h), 'v_proj': q(h // 2, h), 'o_proj': q(h, h),
                'gate_proj': q(f, h), 'up_proj': q(f, h), 'down_proj': q(h, f)}
-    rep = {'input_layernorm.weight': torch.rand(h, generator=g), 'q_norm.weight': torch.rand(128, generator=g)}
+    rep = {'input_layernorm.weight': torch.rand(h, generator=g), 'q_norm.weight': torch.rand(128, generator=g),
+           'post_attention_layernorm.weight': torch.rand(h, generator=g), 'k_norm.weight': torch.rand(128, generator=g)}
     path = ck.save_block(tmp_path / 'te.safetensors', 'te', 7, weights, rep)
     b = ck.load_block(path, 'te', 7, rank=1, world_size=2, device='cpu')
     assert torch.equal(b.k_proj.weight.data, weights['k_proj'][0][h // 4:])
     assert torch.equal(b.down_proj.weight.data, weights['down_proj'][0][:, f // 2:])
-    assert torch.equal(b.tensor('q_norm.weight'), rep['q_norm.weight'])
+    # replicated TE tensors take the FP16 of the reference's TE module shells
+    assert b.tensor('q_norm.weight').dtype == torch.float16
+    assert torch.equal(b.tensor('q_norm.weight'), rep['q_norm.weight'].half())
+    partial = {k: v for k, v in rep.items() if k != 'post_attention_layernorm.weight'}
+    ck.save_block(tmp_path / 'te2.safetensors', 'te', 7, weights, partial)
+    with pytest.raises(ValueError, match='Missing replicated'):
+        ck.load_block(tmp_path / 'te2.safetensors', 'te', 7, device='cpu')
+    bad = dict(weights, down_proj=q(h, f // 2))
+    ck.save_block(tmp_path / 'te3.safetensors', 'te', 7, bad, rep)
+    with pytest.raises(ValueError, match='shape differs'):
+        ck.load_block(tmp_path / 'te3.safetensors', 'te', 7, device='cpu')
+
+
+def test_dit_replicated_tensors_required_and_checked(tmp_path):
+    g = torch.Generator().manual_seed(4)
+    weights, rep = _dit_weights(g)
+    for drop in ('norm1.weight', 'adaln_proj.bias'):
+        ck.save_block(tmp_path / 'm.safetensors', 'dit', 0, weights, {k: v for k, v in rep.items() if k != drop})
+        with pytest.raises(ValueError, match='Missing replicated'):
+            ck.load_block(tmp_path / 'm.safetensors', 'dit', 0, device='cpu')
+    for key, bad in (('norm2.weight', torch.rand(256)), ('k_norm.weight', torch.rand(64)),
+                     ('adaln_proj.weight', torch.rand(6 * 512, 8))):
+        ck.save_block(tmp_path / 's.safetensors', 'dit', 0, weights, dict(rep, **{key: bad}))
+        with pytest.raises(ValueError, match='shape differs'):
+            ck.load_block(tmp_path / 's.safetensors', 'dit', 0, device='cpu')
+    w = dict(weights, fc2=(weights['fc2'][0][:, :512].contiguous(), weights['fc2'][1]))
+    ck.save_block(tmp_path / 'f.safetensors', 'dit', 0, w, rep)
+    with pytest.raises(ValueError, match='shape differs'):
+        ck.load_block(tmp_path / 'f.safetensors', 'dit', 0, device='cpu')
+    # FP16 replicated tensors in the file load as the DiT shells' FP32
+    half = {k: v.half() for k, v in rep.items()}
+    ck.save_block(tmp_path / 'h.safetensors', 'dit', 0, weights, half)
+    b = ck.load_block(tmp_path / 'h.safetensors', 'dit', 0, device='cpu')
+    assert b.tensor('norm1.weight').dtype == torch.float32
+    assert torch.equal(b.tensor('norm1.weight'), half['norm1.weight'].float())
 
 
 @pytest.mark.gpu

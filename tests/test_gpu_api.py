@@ -236,6 +236,22 @@ def test_gemm_w8a8_linear_full_size(gpu):
     assert_bits_equal(np_of(y), o.dequantize_row(np_of(acc), oa, np_of(ws), 'f16', np_of(data['bias'])), 'c0 out')
 
 
+def test_dit_qkv_full_size_with_bias(gpu):
+    """The DiT QKV workload (53504 x 3072 -> 9216, ConvRot256, FP16 bias in
+    the epilogue) on sampled rows against the oracle."""
+    data = workloads.dit_qkv()
+    print('DiT QKV 53504 x 3072 -> 9216 with bias', flush=True)
+    wq, ws = _wq(data['w'], gpu)
+    y = dit_column_linear.column_linear(data['x'].to(gpu), wq, ws, bias=data['bias'].to(gpu))
+    assert y.shape == (53504, 9216) and torch.isfinite(y).all()
+    rows = np.array([0, 1, 255, 256, 26751, 40000, 53248, 53502, 53503])
+    want = o.column_linear(np_of(data['x'])[rows], np_of(wq), np_of(ws).reshape(-1), convrot=True,
+                           bias=np_of(data['bias']))
+    assert_bits_equal(np_of(y[torch.from_numpy(rows).to(gpu)]), want, 'c2 rows with bias')
+    plain = dit_column_linear.column_linear(data['x'].to(gpu), wq, ws)
+    assert not torch.equal(plain, y)
+
+
 def test_row_linear_writes_into_a_row_range(gpu):
     g = torch.Generator().manual_seed(41)
     x = (torch.randn((70, 2 * 512), generator=g) * 0.5).half().to(gpu)

@@ -18,6 +18,13 @@ SHAPES = [
     (2, 3, 200, 64, torch.float32),
     (1, 1, 128, 300, torch.float16),
     (1, 2, 257, 1000, torch.float16),
+    # long key sequences: the max pass's unrolled loop plus its seven-step
+    # tail (1537..1664 keys), several loop iterations with a key count that
+    # is not a multiple of 64, and a long sequence (queries are independent,
+    # so a short query set exercises the whole key loop)
+    (1, 1, 64, 1600, torch.float16),
+    (1, 2, 40, 4000, torch.float16),
+    (1, 2, 48, 16384, torch.float16),
 ]
 
 
@@ -66,7 +73,10 @@ def test_attention_matches_oracle(gpu, b, h, nq, nk, dtype):
     oprep = oa.prepare(_np(q), _np(k), _np(v))
     want = oa.attention(oprep).astype(np.float64)
     exact = oa.reference_attention(_np(q), _np(k), _np(v))
-    rel = _check(out, want, exact, 2e-3)
+    # Against exact softmax attention the quantized probabilities lose
+    # accuracy as the softmax flattens over many keys (cosine 0.9985 at
+    # 16384 random keys); the GPU-vs-oracle bound is the same at every length.
+    rel = _check(out, want, exact, 2e-3, min_cos=0.999 if nk <= 4096 else 0.998)
     print(f'b={b} h={h} nq={nq} nk={nk}: max |gpu - oracle| / max |oracle| = {rel:.2e}')
     out16 = kernels.attention(prep, out_dtype=torch.float16)
     assert torch.equal(out16, out.half())

@@ -168,6 +168,7 @@ def test_gemm_rope_epilogue_full_dit_shape(gpu):
     got = np_of(fused[rows.to(gpu)])
     assert_bits_equal(got[:, :width].reshape(-1, heads, 128), wq_, 'full-shape q rows')
     assert_bits_equal(got[:, width:2 * width].reshape(-1, heads, 128), wk_, 'full-shape k rows')
+    assert_bits_equal(got[:, 2 * width:], packed[:, 2 * width:], 'full-shape v rows')
 
 
 @pytest.mark.parametrize('fq_dt', [torch.float16, torch.float32])

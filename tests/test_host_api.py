@@ -98,3 +98,118 @@ def test_segment_labels():
         assert segment_key(5, segments) is None      # gap, overlap, row out of range
     assert labels_for(5, [(2, 5, 0), (0, 2, 7)]).tolist() == [7, 7, 0, 0, 0]
     assert labels_for(5, [(0, 4, 1)]) is None
+
+
+def test_output_buffers_are_validated_before_any_launch():
+    x = torch.randn(8, 256).half()
+    with pytest.raises(ValueError, match='out must be int8'):
+        kernels.quantize_rows(x, out=torch.empty(4, 256, dtype=torch.int8))
+    with pytest.raises(ValueError, match='out must be int8'):
+        kernels.quantize_rows(x, out=torch.empty(8, 256, dtype=torch.int16))
+    with pytest.raises(ValueError, match='out must be int8'):
+        kernels.quantize_rows(x, out=torch.empty(256, 8, dtype=torch.int8).t())
+    with pytest.raises(ValueError, match='scale_out'):
+        kernels.quantize_rows(x, scale_out=torch.empty(4, 1))
+    with pytest.raises(ValueError, match='scale_out'):
+        kernels.quantize_rows(x, scale_out=torch.empty(8, 1, dtype=torch.float16))
+    q = torch.zeros(8, 256, dtype=torch.int8)
+    w = torch.zeros(32, 256, dtype=torch.int8)
+    with pytest.raises(ValueError, match='out must be int32'):
+        kernels.gemm(q, w, out=torch.empty(4, 32, dtype=torch.int32))
+    with pytest.raises(ValueError, match='out must be int32'):
+        kernels.gemm(q, w, out=torch.empty(32, 8, dtype=torch.int32).t())
+    with pytest.raises(ValueError, match='out must be'):
+        kernels.gemm(q, w, epilogue=kernels.EPI_ROW, row_scale=torch.ones(8), col_scale=torch.ones(32),
+                     out=torch.empty(8, 16, dtype=torch.float16))
+    with pytest.raises(ValueError, match='HIP device'):      # shapes right: the device check follows
+        kernels.gemm(q, w, out=torch.empty(8, 32, dtype=torch.int32))
+
+
+class _Recorder:
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, x, weight, weight_scale, comm, world_size, groupsize, input_act):
+        self.calls.append((x, input_act))
+        return torch.zeros(x.shape[0], weight.shape[0], dtype=x.dtype)
+
+
+def test_row_linear_parts_branches_on_the_host():
+    from w8a8.h3_operator_policy import H3OperatorPolicy, row_linear_parts
+    from w8a8.tp_qwen3vl import RowParallelLinearINT8
+    m = RowParallelLinearINT8(256, 32, device='cpu')
+    gate = torch.randn(4, 256).half()
+    up = torch.randn(4, 256).half()
+    m.operator_policy = H3OperatorPolicy()
+    with pytest.raises(ValueError, match='Matching gate/up'):     # only the fused route checks
+        row_linear_parts(m, gate, up.float(), _Recorder(), None)
+    m.operator_policy = H3OperatorPolicy(fc2_quantizer='native')
+    rec = _Recorder()
+    row_linear_parts(m, gate, up, rec, None)
+    (x, act), = rec.calls
+    assert act is None and x.dtype == torch.float32    # the scaled-FP16 backend's FP32 island
+    assert torch.equal(x, (torch.nn.functional.silu(gate) * up).float())
+    rec = _Recorder()
+    row_linear_parts(m, gate, up.float(), rec, None)    # mismatched halves are fine off the fused route
+    assert rec.calls[0][1] is None
+
+
+def test_prepare_tp_folds_norms_and_projections():
+    from w8a8.h3_tensor_flow import StableNorm, prepare_tp
+    from w8a8.tp_dit import TPDiTBlockINT8
+    b = TPDiTBlockINT8(hidden=256, heads=2, ffn=512, device='cpu')
+    for m in (b.out_proj, b.fc2, b.fc1):
+        m.weight_scale.data.copy_(torch.rand(m.weight_scale.shape) + 1e-3)
+    before = {n: getattr(b, n).weight_scale.detach().clone() for n in ('out_proj', 'fc2', 'fc1')}
+    prepare_tp(b, 'dit', TensorFlowPolicy(mode='fp16'))
+    assert torch.equal(b.out_proj.weight_scale * 512, before['out_proj'])
+    assert torch.equal(b.fc2.weight_scale * 512, before['fc2'])
+    assert torch.equal(b.fc1.weight_scale, before['fc1'])          # column projections are not folded
+    for n in ('norm1', 'norm2', 'q_norm', 'k_norm'):
+        assert isinstance(getattr(b, n), StableNorm), n
+    assert b.norm1.eps == 1e-5 / 512 ** 2 and b.norm2.eps == 1e-5 / 512 ** 2 and b.k_norm.eps == 1e-5
+    with pytest.raises(ValueError, match='already prepared'):
+        prepare_tp(b, 'dit', TensorFlowPolicy(mode='fp16'))
+    legacy = TPDiTBlockINT8(hidden=256, heads=2, ffn=512, device='cpu')
+    assert prepare_tp(legacy, 'dit', TensorFlowPolicy()) is legacy and legacy.norm1.eps == 1e-5
+    # StableNorm on FP32 rows: torch's fp32 RMSNorm with the folded eps
+    x = torch.randn(5, 256)
+    want = torch.nn.functional.rms_norm(x, (256,), b.norm1.weight.float(), 1e-5 / 512 ** 2)
+    assert torch.equal(b.norm1(x), want)
+
+
+def test_te_prepare_and_adjacent_columns():
+    from w8a8.h3_operator_policy import adjacent_cat
+    from w8a8.h3_tensor_flow import StableNorm, prepare_tp
+    from w8a8.tp_qwen3vl import TEFeedForwardINT8
+    ffn = TEFeedForwardINT8(256, 512, device='cpu')
+    ffn.down_proj.weight_scale.data.fill_(1.0)
+    prepare_tp(ffn, 'te', TensorFlowPolicy(mode='fp16'))
+    assert isinstance(ffn.post_attention_layernorm, StableNorm)
+    assert ffn.post_attention_layernorm.eps == 1e-6 / 512 ** 2
+    assert torch.all(ffn.down_proj.weight_scale == 1 / 512)
+    buf = torch.randn(6, 40)
+    g, u = buf[:, 4:20], buf[:, 20:36]
+    cat = adjacent_cat(g, u)
+    assert cat.data_ptr() == g.data_ptr() and torch.equal(cat, torch.cat((g, u), -1))
+    other = adjacent_cat(buf[:, :16], buf[:, 20:36])          # not adjacent: a copy
+    assert other.data_ptr() != buf.data_ptr() and torch.equal(other, torch.cat((buf[:, :16], buf[:, 20:36]), -1))
+
+
+def test_rank_shard_contracts():
+    from w8a8.tp_dit import RowParallelLinearINT8
+    m = RowParallelLinearINT8(1024, 64, rank=1, world_size=2, device='cpu')
+    assert m.in_features_per_rank == 512
+    with pytest.raises(ValueError, match='rank shard takes'):
+        m.partial(torch.zeros(3, 1024).half())
+    with pytest.raises(ValueError, match='rank shard takes'):
+        m.local_maximum(torch.zeros(3, 512).half(), 'swiglu')
+    with pytest.raises(ValueError, match='SUM exchange'):
+        m(torch.zeros(3, 512).half(), residual=torch.zeros(3, 64).half())
+    with pytest.raises(ValueError, match='requires reduction'):
+        m(torch.zeros(3, 512).half(), reduce_sum=False)
+    with pytest.raises(ValueError, match='HIP device'):       # contract met: the CPU tensor is refused
+        m.partial(torch.zeros(3, 512).half())
+    whole = RowParallelLinearINT8(1024, 64, device='cpu')
+    with pytest.raises(ValueError, match='MAX exchange'):
+        whole(torch.zeros(3, 1024).half(), row_max=torch.ones(3, 1))

@@ -588,3 +588,44 @@ def test_row_linear_rotation_cancels_against_rotated_weights():
     assert np.array_equal(o.row_linear(x16, wq, ws, residual=res), o.residual_add(res, branch))
     assert np.array_equal(o.row_linear(x16, wq, ws, residual=res, gate=gate, labels=labels),
                           o.gated_residual_add(res, branch, gate, labels))
+
+
+def test_rank_partials_sum_to_the_unsharded_accumulator():
+    """Two rank halves of a row projection (whole 256-channel groups each):
+    the MAX of the ranks' row maxima is the unsharded row maximum, and the
+    int32 partials quantized with it add up to the unsharded accumulator."""
+    rng = np.random.default_rng(17)
+    m, k, n = 9, 1024, 48
+    wq = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    # O projection: the K slice [0, k/2) on rank 0, [k/2, k) on rank 1
+    x = (rng.standard_normal((m, k)) * 3).astype(np.float16)
+    x[2] = 0
+    halves = [x[:, :k // 2], x[:, k // 2:]]
+    maxima = [o.rank_row_max(h) for h in halves]
+    gmax = np.maximum(*maxima)
+    assert np.array_equal(gmax, o.rank_row_max(x))
+    assert not np.array_equal(maxima[0], gmax)      # the local maxima differ from the global
+    parts = [o.row_partial(h, wq[:, r * k // 2:(r + 1) * k // 2], row_max=gmax) for r, h in enumerate(halves)]
+    whole_acc, whole_a = o.row_partial(x, wq)
+    assert np.array_equal(parts[0][0].astype(np.int64) + parts[1][0], whole_acc)
+    assert np.array_equal(parts[0][1], whole_a) and np.array_equal(parts[1][1], whole_a)
+    # a rank quantizing with its own maximum is a different operator
+    own = o.row_partial(halves[0], wq[:, :k // 2])
+    assert not np.array_equal(own[1], whole_a)
+    # FC2: rank r holds [gate_r | up_r]; the unsharded input is [gate | up]
+    w = 512
+    gu = (rng.standard_normal((m, 2 * w)) * 2).astype(np.float16)
+    gate, up = gu[:, :w], gu[:, w:]
+    ranks = [np.concatenate([gate[:, r * w // 2:(r + 1) * w // 2], up[:, r * w // 2:(r + 1) * w // 2]], 1)
+             for r in (0, 1)]
+    wq2 = rng.integers(-128, 128, (n, w), dtype=np.int8)
+    gmax2 = np.maximum(*[o.rank_row_max(r_, swiglu=True) for r_ in ranks])
+    assert np.array_equal(gmax2, o.rank_row_max(gu, swiglu=True))
+    p2 = [o.row_partial(r_, wq2[:, r * w // 2:(r + 1) * w // 2], row_max=gmax2, swiglu=True)
+          for r, r_ in enumerate(ranks)]
+    acc2, a2 = o.row_partial(gu, wq2, swiglu=True)
+    assert np.array_equal(p2[0][0].astype(np.int64) + p2[1][0], acc2) and np.array_equal(p2[1][1], a2)
+    # pairing rank 0's gate with rank 1's up breaks the identity
+    swapped = np.concatenate([ranks[0][:, :w // 2], ranks[1][:, w // 2:]], 1)
+    bad = o.row_partial(swapped, wq2[:, :w // 2], row_max=gmax2, swiglu=True)[0]
+    assert not np.array_equal(bad.astype(np.int64) + p2[1][0], acc2)
