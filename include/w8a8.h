@@ -408,6 +408,22 @@ typedef struct W8A8GemmArgs {
 int w8a8_gemm(const W8A8GemmArgs* args);
 
 /*
+ * w8a8_gemm that allocates nothing and takes no workspace. No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split-K partials go to a file-scope device array of
+ * W8A8_GEMM_SCRATCH_BYTES per GPU, which the library holds until the process
+ * ends; a shape whose split needs more is rejected (W8A8_ERR_INVALID), as is
+ * a non-NULL args->workspace or a non-zero workspace_bytes. Every call on one
+ * GPU shares that GPU's array, so calls that overlap on one GPU (e.g. on two
+ * streams) race. Nothing in the array needs clearing: every split writes its
+ * whole partial tile before the reduction reads it. Otherwise identical to
+ * w8a8_gemm (same arguments, numerics and errors).
+ */
+#define W8A8_GEMM_SCRATCH_BYTES (64ll << 20)
+int w8a8_gemm_noalloc(const W8A8GemmArgs* args);
+
+/*
  * Workspace bytes w8a8_gemm would use for an m x n x k GEMM on the current
  * device (0: the shape does not split K). No counterpart in the reference
  * (its int_mm calls a vendor GEMM that manages its own workspace); it lets

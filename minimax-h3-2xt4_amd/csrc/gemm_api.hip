@@ -1,6 +1,8 @@
 // C ABI of the INT8 GEMM and the standalone epilogue: argument checks, then
 // dispatch to the (epilogue, output dtype) launcher instantiated in
 // gemm_inst.hip.
+#include <mutex>
+
 #include "gemm_launch.h"
 #include "w8a8_device.h"
 
@@ -80,11 +82,11 @@ static void fill_epilogue(GemmParams& p, const Args* a) {
 
 }  // namespace w8a8
 
-extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
-  using namespace w8a8;
-  W8A8_REQUIRE(a != nullptr, "w8a8_gemm: null args");
-  W8A8_REQUIRE(a->struct_size == sizeof(W8A8GemmArgs), "w8a8_gemm: struct_size %u != %zu", a->struct_size,
-               sizeof(W8A8GemmArgs));
+namespace w8a8 {
+
+// Checks and dispatch shared by w8a8_gemm (the caller's workspace) and
+// w8a8_gemm_noalloc (the file-scope scratch array).
+static int gemm_entry(const W8A8GemmArgs* a, void* workspace, int64_t workspace_bytes) {
   W8A8_REQUIRE(a->m >= 0 && a->n >= 0 && a->k >= 0, "w8a8_gemm: negative shape");
   W8A8_REQUIRE(a->m < (1LL << 31) && a->n < (1LL << 31) && a->k < (1LL << 31), "w8a8_gemm: shape too large");
   W8A8_REQUIRE(a->k * 128 * 128 < (1LL << 31), "w8a8_gemm: k=%lld could overflow int32 accumulation",
@@ -106,10 +108,10 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
   p.a = a->a; p.b = a->b; p.lda = a->lda; p.ldb = a->ldb;
   p.k = (int)a->k;
   p.ksplit = 1;
-  W8A8_REQUIRE(a->workspace_bytes >= 0 && (a->workspace == nullptr || aligned16(a->workspace)),
+  W8A8_REQUIRE(workspace_bytes >= 0 && (workspace == nullptr || aligned16(workspace)),
                "w8a8_gemm: workspace must be 16-byte aligned with workspace_bytes >= 0");
-  p.ws = a->workspace_bytes > 0 ? a->workspace : nullptr;
-  p.ws_bytes = a->workspace_bytes;
+  p.ws = workspace_bytes > 0 ? workspace : nullptr;
+  p.ws_bytes = workspace_bytes;
   {
     const int es = (a->out_dtype == W8A8_F16 || a->out_dtype == W8A8_BF16) ? 2 : 4;
     p.vec16 = aligned16(a->out) && (a->ldc * es) % 16 == 0 &&
@@ -153,6 +155,76 @@ extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
   }
   if (rc2 != W8A8_OK) return rc2;
   return launch_status("w8a8_gemm");
+}
+
+// No-allocation variant: the split-K partials of w8a8_gemm_noalloc live in
+// this file-scope array, one instance per GPU, held until the process ends.
+// Host code never passes `scratch` itself (its host-side name is not a device
+// address): the entry point looks up each device's address once with
+// hipGetSymbolAddress and passes that pointer to the kernels.
+constexpr int64_t kScratchBytes = W8A8_GEMM_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[kScratchDevices];
+
+// The current device's scratch address (looked up on the first call on that
+// device, with the device current).
+static int scratch_of_current_device(void** out, int* device) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_error("w8a8_gemm_noalloc: no usable current device (%s)", hipGetErrorString(e));
+    return W8A8_ERR_LAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_error("w8a8_gemm_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return W8A8_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  *device = dev;
+  return W8A8_OK;
+}
+
+}  // namespace w8a8
+
+extern "C" int w8a8_gemm(const W8A8GemmArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_gemm: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8GemmArgs), "w8a8_gemm: struct_size %u != %zu", a->struct_size,
+               sizeof(W8A8GemmArgs));
+  return gemm_entry(a, a->workspace, a->workspace_bytes);
+}
+
+extern "C" int w8a8_gemm_noalloc(const W8A8GemmArgs* a) {
+  using namespace w8a8;
+  W8A8_REQUIRE(a != nullptr, "w8a8_gemm_noalloc: null args");
+  W8A8_REQUIRE(a->struct_size == sizeof(W8A8GemmArgs), "w8a8_gemm_noalloc: struct_size %u != %zu",
+               a->struct_size, sizeof(W8A8GemmArgs));
+  W8A8_REQUIRE(a->workspace == nullptr && a->workspace_bytes == 0,
+               "w8a8_gemm_noalloc: the static scratch replaces the workspace (pass NULL and 0)");
+  void* ws = nullptr;
+  int dev = 0;
+  int rc = scratch_of_current_device(&ws, &dev);
+  if (rc != W8A8_OK) return rc;
+  if (a->m > 0 && a->n > 0 && a->k > 0 && a->rope == nullptr && a->m < (1LL << 31) && a->n < (1LL << 31) &&
+      a->k < (1LL << 31)) {
+    int64_t need = 0;
+    gemm_ksplit(a->m, a->n, a->k, dev, &need);
+    W8A8_REQUIRE(need <= kScratchBytes,
+                 "w8a8_gemm_noalloc: %lld x %lld x %lld splits K and needs %lld scratch bytes, above the "
+                 "%lld-byte static scratch",
+                 (long long)a->m, (long long)a->n, (long long)a->k, (long long)need, (long long)kScratchBytes);
+  }
+  return gemm_entry(a, ws, kScratchBytes);
 }
 
 extern "C" int64_t w8a8_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {

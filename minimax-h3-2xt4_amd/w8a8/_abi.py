@@ -91,8 +91,10 @@ class AttentionArgs(ctypes.Structure):
 STRUCTS = (QuantArgs, SwigluArgs, GemmArgs, DequantArgs, NormArgs, RmsRopeArgs, AttnPrepareArgs, AttentionArgs)
 STRUCT_ENTRY_POINTS = ('w8a8_quantize_rows', 'w8a8_swiglu_quantize', 'w8a8_gemm', 'w8a8_dequantize',
                        'w8a8_norm_quantize', 'w8a8_rms_rope', 'w8a8_attention_prepare', 'w8a8_attention')
-ENTRY_POINTS = STRUCT_ENTRY_POINTS + ('w8a8_abi_version', 'w8a8_struct_size', 'w8a8_last_error',
-                                      'w8a8_gemm_workspace_size', 'w8a8_attention_workspace_size')
+ENTRY_POINTS = STRUCT_ENTRY_POINTS + ('w8a8_gemm_noalloc', 'w8a8_abi_version', 'w8a8_struct_size',
+                                      'w8a8_last_error', 'w8a8_gemm_workspace_size',
+                                      'w8a8_attention_workspace_size')
+GEMM_SCRATCH_BYTES = 64 << 20   # W8A8_GEMM_SCRATCH_BYTES: the no-allocation GEMM's split-K scratch per GPU
 
 _LIB = None
 
@@ -123,7 +125,7 @@ def load(path=None):
     lib.w8a8_gemm_workspace_size.argtypes = [_c.c_int64, _c.c_int64, _c.c_int64]
     lib.w8a8_attention_workspace_size.restype = _c.c_int64
     lib.w8a8_attention_workspace_size.argtypes = [_c.c_int64, _c.c_int64, _c.c_int64]
-    for name, st in zip(STRUCT_ENTRY_POINTS, STRUCTS):
+    for name, st in zip(STRUCT_ENTRY_POINTS + ('w8a8_gemm_noalloc',), STRUCTS + (GemmArgs,)):
         fn = getattr(lib, name)
         fn.restype = _c.c_int
         fn.argtypes = [ctypes.POINTER(st)]
