@@ -114,7 +114,6 @@ def run_dit_ffn(args, torch, dev):
     ref = block(h, res)
     if not torch.equal(step(), ref):
         raise RuntimeError('bench step differs from DiTFeedForwardINT8.forward')
-    del ref
 
     for _ in range(args.warmup):
         step()
@@ -182,38 +181,100 @@ def run_dit_ffn(args, torch, dev):
                            for k, v in kernels_out.items()},
                   roofline=roofline)
     if not args.no_cpu_baseline:
-        result['cpu_baseline'] = cpu_baseline_ffn(args, data, block, m, ops_fc1 + ops_fc2)
+        result['cpu_baseline'] = cpu_baseline_ffn(args, data, block, m, ops_fc1 + ops_fc2, gpu_out=ref)
     return result
 
 
-def cpu_baseline_ffn(args, data, block, m, ops_block):
-    """The CPU oracle (numpy, float64 BLAS for the exact INT32 GEMM) on a row
-    sample of the same block, extrapolated linearly in rows (rows are
-    independent under per-row scales)."""
+def cpu_threads():
+    """Host threads for the CPU baseline: the process's CPU affinity, capped
+    by OMP_NUM_THREADS when the host sets it (the GPU box's CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        n = min(n, int(os.environ.get('OMP_NUM_THREADS', n)))
+    except ValueError:
+        pass
+    return max(n, 1)
+
+
+def lscpu_model():
+    import subprocess
+    try:
+        out = subprocess.run(['lscpu'], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.strip().startswith('Model name'):
+                return line.split(':', 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return cpu_model()
+
+
+def torch_cpu_ffn(torch, h, w1, ws1, w2, ws2, res, hmat):
+    """The DiT FFN block restated in torch CPU ops, as the reference's torch
+    path computes it (patches/parallel_int8.py:26-69, dit_column_linear.py:
+    13-37, tilelang_swiglu_quant.py:18-64 and the quantizer restatement of
+    benchmarks/verify_dit_p0a_p0c_local.py:140-147): ConvRot256 as an FP32
+    GEMM against the 256 x 256 rotation, per-row absmax quantization,
+    torch._int_mm (INT32), the column / row dequantization orders and the
+    FP16 residual add. The rotation GEMM and torch's exp may round a few
+    values differently from the GPU kernels (same arithmetic, other orders).
+    """
+    r127 = torch.tensor(1.0 / 127.0, dtype=torch.float32)
+
+    def rotate(x):
+        m, k = x.shape
+        return (x.view(m, k // 256, 256) @ hmat).view(m, k)
+
+    def quantize(x):
+        scale = torch.clamp(x.abs().amax(-1, keepdim=True) * r127, min=1e-30)
+        return torch.clamp(torch.round(x / scale), -128, 127).to(torch.int8), scale
+
+    q1, a1 = quantize(rotate(h.float()).half().float())
+    y1 = (torch._int_mm(q1, w1.t()).float() * (a1 * ws1.view(1, -1))).half()
+    f = y1.shape[1] // 2
+    g = y1[:, :f].float()
+    act = (g / (1.0 + torch.exp(-g))) * y1[:, f:].float()
+    q2, a2 = quantize(rotate(act))
+    y2 = ((torch._int_mm(q2, w2.t()).float() * a2) * ws2.view(1, -1)).half()
+    return (res.float() + y2.float()).half()
+
+
+def cpu_baseline_ffn(args, data, block, m, ops_block, gpu_out=None):
+    """The reference's CPU path (torch quantize ops + torch._int_mm + dequant)
+    on the whole M=16384 block, on this host's CPU threads: 1 warm-up and 3
+    timed repetitions, median."""
     import numpy as np
+    import torch
 
     import oracle as o
-    rows = args.cpu_rows
-    w1 = block.fc1.weight.detach().cpu().numpy()
-    w2 = block.fc2.weight.detach().cpu().numpy()
-    s1 = block.fc1.weight_scale.detach().cpu().numpy().reshape(-1)
-    s2 = block.fc2.weight_scale.detach().cpu().numpy().reshape(-1)
-    w1f = w1.astype(np.float64)
-    w2f = w2.astype(np.float64)
-    h = data['h'][:rows].numpy()
-    r = data['residual'][:rows].numpy()
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    w1 = block.fc1.weight.detach().cpu()
+    w2 = block.fc2.weight.detach().cpu()
+    s1 = block.fc1.weight_scale.detach().cpu().reshape(-1).float()
+    s2 = block.fc2.weight_scale.detach().cpu().reshape(-1).float()
+    hmat = torch.from_numpy(o.hadamard256().astype(np.float32))
+    rows = m
+    h = data['h'][:rows]
+    r = data['residual'][:rows]
     times = []
     for rep in range(4):     # one warm-up, three timed
         t0 = time.perf_counter()
-        o.ffn_block(h, w1, s1, w2, s2, r, w1_f64=w1f, w2_f64=w2f)
+        out = torch_cpu_ffn(torch, h, w1, s1, w2, s2, r, hmat)
         if rep:
             times.append(time.perf_counter() - t0)
     t = float(np.median(times))
     full_s = t * m / rows
-    return dict(value=round(ops_block / full_s / 1e12, 4), unit='TOPS', cores=blas_threads(), kind='port',
-                sample=f'oracle DiT FFN block on {rows} of {m} rows (median of 3 after 1 warm-up, '
-                       f'{t:.2f} s), extrapolated x{m // rows} to {full_s * 1e6:.0f} us per block; '
-                       f'numpy float64 BLAS for the exact int32 GEMM; CPU: {cpu_model()}')
+    agree = ''
+    if gpu_out is not None:
+        g = gpu_out[:rows].cpu()
+        same = float((g.view(torch.int16) == out.view(torch.int16)).double().mean())
+        diff = float((g.float() - out.float()).abs().max())
+        agree = f'; {same * 100:.3f}% of the fp16 outputs bit-identical to the GPU block (max |diff| {diff:.3g})'
+    scale = '' if rows == m else f', extrapolated x{m / rows:.2f} to {full_s * 1e6:.0f} us'
+    return dict(value=round(ops_block / full_s / 1e12, 4), unit='TOPS', cores=threads, kind='port',
+                sample=f'torch CPU restatement (ConvRot256 fp32 GEMM, quantize, torch._int_mm, dequant, '
+                       f'SwiGLU, residual) of the DiT FFN block on {rows} of {m} rows: median of 3 after 1 '
+                       f'warm-up {t:.3f} s{scale}; {threads} threads; CPU: {lscpu_model()}{agree}')
 
 
 def traffic_from_profiles(kernel_key):

@@ -89,7 +89,7 @@ __device__ __forceinline__ void modulate16(float (&v)[16], uint32_t (&bits)[8], 
 template <int DT, int MODE, int J, int TB>
 __global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
   constexpr int ROT = rot_of<MODE>();
-  __shared__ float lds[ROT ? kNormWaves * 1024 : 1];
+  __shared__ float lds[ROT ? kNormWaves * kRotWave : 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kNormWaves + wave;
   if (row >= p.rows) return;
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
     sh = p.shift + (int64_t)l * p.ld_mod;
     sc = p.mscale + (int64_t)l * p.ld_mod;
   }
-  float* buf = ROT ? lds + wave * 1024 + (lane >> 4) * 256 : nullptr;
+  float* buf = ROT ? rot_slot(lds, wave, lane) : nullptr;
   const int t = lane & 15;
 
   // Normalize one unit (v holds x), store y, rotate for the quantizer.

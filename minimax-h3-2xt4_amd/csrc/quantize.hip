@@ -25,14 +25,14 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t cols,
     const float* __restrict__ row_max, int8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale, float* __restrict__ row_max_out) {
-  __shared__ float lds[ROT ? kQuantWaves * 1024 : 1];
+  __shared__ float lds[ROT ? kQuantWaves * kRotWave : 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + wave;
   if (row >= rows) return;
   const int units = (int)(cols >> 4);
   const int jcount = (units + 63) >> 6;
   const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * dt_bytes<DT>();
-  float* buf = ROT ? lds + wave * 1024 + (lane >> 4) * 256 : nullptr;
+  float* buf = ROT ? rot_slot(lds, wave, lane) : nullptr;
   const int t = lane & 15;
 
   auto load_unit = [&](int u, float (&v)[16]) {
@@ -46,12 +46,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     }
   };
   auto store_unit = [&](int u, const float (&v)[16], float s, float rcp) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = pack4(quant1(v[4 * i], s, rcp), quant1(v[4 * i + 1], s, rcp),
-                   quant1(v[4 * i + 2], s, rcp), quant1(v[4 * i + 3], s, rcp));
-    *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = quant16(v, s, rcp);
   };
 
   if constexpr (J > 0) {
@@ -116,13 +111,13 @@ template <int DT, int ROT, int J>
 __global__ __launch_bounds__(256) void quantize_row_wg_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t cols, const float* __restrict__ row_max,
     int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, float* __restrict__ row_max_out) {
-  __shared__ float lds[ROT ? 4 * 1024 : 1];
+  __shared__ float lds[ROT ? 4 * kRotWave : 1];
   __shared__ float wmax[4];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const int units = (int)(cols >> 4);
   const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * dt_bytes<DT>();
-  float* buf = ROT ? lds + wave * 1024 + (lane >> 4) * 256 : nullptr;
+  float* buf = ROT ? rot_slot(lds, wave, lane) : nullptr;
   const int t = lane & 15;
   float v[J][16];
   float amax = 0.0f;
@@ -153,14 +148,7 @@ __global__ __launch_bounds__(256) void quantize_row_wg_kernel(
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int u = tid + 256 * j;
-    if (u < units) {
-      uint32_t w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = pack4(quant1(v[j][4 * i], s, rcp), quant1(v[j][4 * i + 1], s, rcp),
-                     quant1(v[j][4 * i + 2], s, rcp), quant1(v[j][4 * i + 3], s, rcp));
-      *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    if (u < units) *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = quant16(v[j], s, rcp);
   }
   if (tid == 0) scale[row] = s;
 }

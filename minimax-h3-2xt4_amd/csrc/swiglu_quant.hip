@@ -5,6 +5,8 @@
 // [16t, 16t + 16) of the group with 128-bit loads). The rotated FP32 values
 // stay in registers until the row maximum is known, so the only HBM traffic
 // is the FP16 gate|up row in and the int8 row out (plus the fp32 scale).
+// (Timed on one box: at width 8192 two passes of 4-wave workgroups run
+// 220 us against 262 us for one pass of 8-wave workgroups.)
 #include "w8a8_device.h"
 #include "w8a8_host.h"
 
@@ -23,24 +25,25 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
     const float* __restrict__ row_max_in, float* __restrict__ row_max_out,
     float* __restrict__ group_max, int8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale) {
-  __shared__ float lds[4 * 1024];
-  __shared__ float wmax[4];
+  constexpr int kWaves = 4, kSlots = 4 * kWaves;
+  __shared__ float lds[kWaves * kRotWave];
+  __shared__ float wmax[kWaves];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const int groups = (int)(width >> 8);
   const int slot = tid >> 4;
   const int t = tid & 15;
-  float* buf = lds + wave * 1024 + (lane >> 4) * 256;
+  float* buf = rot_slot(lds, wave, lane);
   const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * sw_bytes<DT>();
 
-  // v[j] <- rotated element 16 j + t of group g.
+  // v[i] <- rotated element 16 t + i of group g.
   auto transform = [&](int g, float (&v)[16]) {
     float gv[16], uv[16];
     load16<DT>(xrow + ((int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), gv);
     load16<DT>(xrow + (width + (int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), uv);
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = swiglu(gv[i], uv[i]);
-    convrot256_lanes<false>(v, buf, t);
+    convrot256_lanes<true>(v, buf, t);
   };
   auto group_absmax = [&](int g, const float (&v)[16]) {
     float m = 0.0f;
@@ -51,19 +54,16 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
     return m;
   };
   auto store_group = [&](int g, const float (&v)[16], float s, float rcp) {
-    uint8_t* bytes = reinterpret_cast<uint8_t*>(buf);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) bytes[16 * j + t] = (uint8_t)quant1(v[j], s, rcp);
-    wave_lds_sync();
-    const uint4 packed = reinterpret_cast<const uint4*>(bytes)[t];
-    *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)g * 256 + 16 * t) = packed;
-    wave_lds_sync();
+    *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)g * 256 + 16 * t) = quant16(v, s, rcp);
   };
   auto row_reduce = [&](float m) {
     m = wave_max(m);
     if (lane == 0) wmax[wave] = m;
     __syncthreads();
-    return fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) r = fmaxf(r, wmax[w]);
+    return r;
   };
 
   if constexpr (P > 0) {
@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
     float local = 0.0f;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      const int g = slot + 16 * p;
+      const int g = slot + kSlots * p;
       if (g < groups) {
         transform(g, v[p]);
         local = fmaxf(local, group_absmax(g, v[p]));
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
       const float rcp = 1.0f / s;
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        const int g = slot + 16 * p;
+        const int g = slot + kSlots * p;
         if (g < groups) store_group(g, v[p], s, rcp);
       }
       if (tid == 0) scale[row] = s;
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
     float local = 0.0f;
     const bool need_max = !row_max_in || row_max_out || group_max;
     if (need_max) {
-      for (int g = slot; g < groups; g += 16) {
+      for (int g = slot; g < groups; g += kSlots) {
         float v[16];
         transform(g, v);
         local = fmaxf(local, group_absmax(g, v));
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
     if (q) {
       const float s = row_scale_of(row_max_in ? row_max_in[row] : rmax);
       const float rcp = 1.0f / s;
-      for (int g = slot; g < groups; g += 16) {
+      for (int g = slot; g < groups; g += kSlots) {
         float v[16];
         transform(g, v);
         store_group(g, v, s, rcp);

@@ -99,21 +99,23 @@ __device__ __forceinline__ float round_to(float x) {
 // ------------------------------------------------------------- exponential
 // Cephes single-precision exp (Moshier, Cephes Math Library expf.c):
 // Cody-Waite reduction with ln2 = C1 + C2, degree-5 minimax polynomial,
-// separate fp32 multiplies/adds, n rounded half to even, inputs clamped to
-// [-104, 89] (beyond which fp32 exp is 0 / inf), scaled by ldexp.
+// n rounded half to even, inputs clamped to [-104, 89] (beyond which fp32
+// exp is 0 / inf), scaled by ldexp. The reduction steps, the Horner steps and
+// the final p*z + r are single-rounding fused multiply-adds (n*C1 is exact,
+// so the first step equals x - n*C1).
 __device__ __forceinline__ float exp_f32(float x) {
   x = fminf(fmaxf(x, -104.0f), 89.0f);
   const float n = rintf(x * 1.44269504088896341f);
-  float r = x - n * 0.693359375f;
-  r = r - n * -2.12194440e-4f;
+  float r = __builtin_fmaf(-n, 0.693359375f, x);
+  r = __builtin_fmaf(-n, -2.12194440e-4f, r);
   const float z = r * r;
   float p = 1.9875691500e-4f;
-  p = p * r + 1.3981999507e-3f;
-  p = p * r + 8.3334519073e-3f;
-  p = p * r + 4.1665795894e-2f;
-  p = p * r + 1.6666665459e-1f;
-  p = p * r + 5.0000001201e-1f;
-  const float y = (p * z + r) + 1.0f;
+  p = __builtin_fmaf(p, r, 1.3981999507e-3f);
+  p = __builtin_fmaf(p, r, 8.3334519073e-3f);
+  p = __builtin_fmaf(p, r, 4.1665795894e-2f);
+  p = __builtin_fmaf(p, r, 1.6666665459e-1f);
+  p = __builtin_fmaf(p, r, 5.0000001201e-1f);
+  const float y = __builtin_fmaf(p, z, r) + 1.0f;
   return ldexpf(y, (int)n);
 }
 
@@ -128,12 +130,13 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 // q = clamp(rne(x / s), -128, 127) with the IEEE quotient x / s.
 // rcp = 1/s (IEEE). The product x*rcp is within 2^-15 of the quotient for
 // |quotient| < 128, so away from half-integers both round to the same
-// integer; near a half-integer (or out of range, or NaN) the exact quotient
-// is computed.
+// integer; near a half-integer (or for NaN / inf) the exact quotient is
+// computed. Beyond |quotient| >= 128 both saturate to the same code (they
+// share the sign, and neither can land on the other side of the clamp).
 __device__ __forceinline__ int quant1(float x, float s, float rcp) {
   const float y = x * rcp;
   float n = rintf(y);
-  if (!(fabsf(y - n) < kTieGuard && fabsf(y) < 128.0f)) n = rintf(x / s);
+  if (!(fabsf(y - n) < kTieGuard)) n = rintf(x / s);
   n = fminf(fmaxf(n, -128.0f), 127.0f);
   return (int)n;
 }
@@ -150,12 +153,17 @@ __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
 // ------------------------------------------------------------- ConvRot256
 // One radix-4 stage of the regular H4 butterfly on four values e0..e3 that
 // differ only in the stage's digit: output digit d negates input 3-d, and
-// the sum runs ((p + q) + r) + s in input order.
+// the sum runs ((p + q) + r) + s in input order. e0 + e1 and e0 - e1 are
+// shared: a + (-b) is a - b exactly, and ((-e0) + e1) equals -(e0 - e1)
+// except for the sign of a zero sum, which no output of the path keeps
+// (absmax and the int8 codes map -0 and +0 alike).
 __device__ __forceinline__ void h4(float& e0, float& e1, float& e2, float& e3) {
-  const float o0 = ((e0 + e1) + e2) + (-e3);
-  const float o1 = ((e0 + e1) + (-e2)) + e3;
-  const float o2 = ((e0 + (-e1)) + e2) + e3;
-  const float o3 = (((-e0) + e1) + e2) + e3;
+  const float t = e0 + e1;
+  const float u = e0 - e1;
+  const float o0 = (t + e2) - e3;
+  const float o1 = (t - e2) + e3;
+  const float o2 = (u + e2) + e3;
+  const float o3 = (e2 - u) + e3;
   e0 = o0; e1 = o1; e2 = o2; e3 = o3;
 }
 
@@ -176,21 +184,39 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// LDS layout of the ConvRot256 lane transpose: each 16-lane slot of a
+// wavefront owns kRotSlot floats (256 plus a 16-float skew, so the four
+// slots of a wavefront start on different banks), a wavefront kRotWave.
+// Lane t's row of 16 floats (elements 16t..16t+15 of the group) is stored
+// as four 16-byte chunks with chunk i at position i ^ ((t >> 1) & 3): the
+// eight lanes of one 128-byte write then cover distinct banks, and the
+// transposed reads (16 lanes reading 16 consecutive floats) stay
+// conflict-free.
+constexpr int kRotSlot = 272;
+constexpr int kRotWave = 4 * kRotSlot;
+
+__device__ __forceinline__ float* rot_slot(float* lds, int wave, int lane) {
+  return lds + wave * kRotWave + (lane >> 4) * kRotSlot;
+}
+
 // ConvRot256 of one 256-element group held by 16 consecutive lanes, lane t
 // holding elements 16t..16t+15 in v (natural order). buf is this group's
-// 256-float LDS slice. On return, if NATURAL, v again holds elements
+// slot (rot_slot). On return, if NATURAL, v again holds elements
 // 16t..16t+15; otherwise v[j] holds element 16j + t. The 1/16 factor is
 // applied last, as in the reference butterfly.
 template <bool NATURAL>
 __device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int t) {
   h4_low_digits(v);
+  const int sw = (t >> 1) & 3;
   float4* row = reinterpret_cast<float4*>(buf + 16 * t);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) row[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  for (int i = 0; i < 4; ++i) row[i ^ sw] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   wave_lds_sync();
+  // Element 16 j + t sits in lane j's row, chunk (t >> 2) ^ ((j >> 1) & 3),
+  // position t & 3: float 16 j + (t ^ (4 * ((j >> 1) & 3))).
   float w[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) w[j] = buf[16 * j + t];
+  for (int j = 0; j < 16; ++j) w[j] = buf[16 * j + (t ^ (4 * ((j >> 1) & 3)))];
   // w[j] = element 16 j + t: j = 4*d3 + d2; digit d2 (stride 16), then d3.
 #pragma unroll
   for (int b = 0; b < 4; ++b) h4(w[4 * b + 0], w[4 * b + 1], w[4 * b + 2], w[4 * b + 3]);
@@ -199,12 +225,14 @@ __device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int
 #pragma unroll
   for (int j = 0; j < 16; ++j) w[j] = w[j] * kInv16;
   if constexpr (NATURAL) {
+    // Each lane writes back exactly the floats it read (the transposed read
+    // is a bijection), so no other lane's read can be overtaken.
 #pragma unroll
-    for (int j = 0; j < 16; ++j) buf[16 * j + t] = w[j];
+    for (int j = 0; j < 16; ++j) buf[16 * j + (t ^ (4 * ((j >> 1) & 3)))] = w[j];
     wave_lds_sync();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float4 q = row[i];
+      float4 q = row[i ^ sw];
       v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
     }
     wave_lds_sync();
@@ -213,6 +241,17 @@ __device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int
     for (int j = 0; j < 16; ++j) v[j] = w[j];
     wave_lds_sync();
   }
+}
+
+// The 16 int8 codes of elements 16t..16t+15 (natural order), packed for one
+// 16-byte store.
+__device__ __forceinline__ uint4 quant16(const float (&v)[16], float s, float rcp) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = pack4(quant1(v[4 * i], s, rcp), quant1(v[4 * i + 1], s, rcp), quant1(v[4 * i + 2], s, rcp),
+                 quant1(v[4 * i + 3], s, rcp));
+  return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // ------------------------------------------------------------- reductions

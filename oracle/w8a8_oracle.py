@@ -144,21 +144,24 @@ def exp_f32(x):
     (patches/tilelang_swiglu_quant.py:22); that routine is not reproduced.
     This is the Cephes single-precision method (Cody-Waite reduction with the
     two-part ln2 C1 + C2, degree-5 minimax polynomial, Moshier's Cephes Math
-    Library expf.c), evaluated with separate fp32 multiplies and adds, n by
-    round-half-even, inputs clamped to [-104, 89] (outside, fp32 exp is 0 or
-    inf anyway), result scaled by ldexp.
+    Library expf.c): inputs clamped to [-104, 89] (outside, fp32 exp is 0 or
+    inf anyway), n = rne(x * log2 e) with one fp32 product, then the two
+    reduction steps, the five Horner steps and p*z + r as fp32 fused
+    multiply-adds (``fma_f32``, one rounding each; n*C1 is exact, so the first
+    step equals x - n*C1), z = r*r and the final + 1 as fp32 operations, and
+    the result scaled by ldexp.
     """
     x = _f32(x)
     with np.errstate(over='ignore', under='ignore', invalid='ignore'):
         x = np.fmin(np.fmax(x, _EXP_LO), _EXP_HI)
-        n = np.rint(x * _LOG2E)
-        r = x - n * _C1
-        r = r - n * _C2
+        n = np.rint(x * _LOG2E).astype(np.float32)
+        r = fma_f32(-n, _C1, x)
+        r = fma_f32(-n, _C2, r)
         z = r * r
         p = np.full_like(r, _EXP_P[0])
         for c in _EXP_P[1:]:
-            p = p * r + c
-        y = (p * z + r) + F32(1.0)
+            p = fma_f32(p, r, c)
+        y = fma_f32(p, z, r) + F32(1.0)
         return np.ldexp(y, n.astype(np.int32)).astype(np.float32)
 
 
