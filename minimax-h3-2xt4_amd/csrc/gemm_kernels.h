@@ -733,15 +733,25 @@ __device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw,
 // (global_load_lds_dwordx4). One workgroup per CU walks its tiles; the
 // operand stream runs across tile boundaries.
 //
-// A stage holds K = 128 of both operand tiles (256 rows x 128 bytes each,
-// 64 KB): every row segment is a whole 128-byte line, which streams from L2
-// about 1.6x faster per CU than half lines. The LDS holds a two-stage ring
-// (128 KB) and a dedicated 32 KB epilogue staging area (8 KB per wave).
-// Stage s + 2 is issued into the buffer of stage s as soon as every wave has
-// finished reading it (a few MFMAs into the stage's last K sub-step), and is
-// awaited at the same point of stage s + 1: a whole stage time in flight.
-// Every wait is vmcnt(0), which also covers the epilogue's stores (they
-// share the counter).
+// A stage holds K = 128 of both operand tiles (256 rows x 128 bytes each):
+// every row segment is a whole 128-byte line, which streams from L2 about
+// 1.6x faster per CU than half lines. The 160 KB of LDS is a ring of five
+// 32 KB slots, one operand tile of one stage each: unit h (the A tile of
+// stage h / 2 for even h, its B tile for odd h) lives in slot h % 5. While
+// stage g computes from units 2g and 2g + 1, units 2g + 2 .. 2g + 4 stream
+// in; the barrier at the end of stage g releases two slots for units 2g + 5
+// and 2g + 6. Each K = 32 sub-step issues 4 of a unit's 8 DMA instructions
+// per wave, one after each MFMA row, so the address unit never queues a burst
+// in front of the MFMAs. A tile's epilogue stages its accumulators through
+// the B slot of its last stage, whose next unit is issued only during the
+// next stage.
+//
+// The waits count outstanding loads instead of draining them: before each
+// stage barrier vmcnt(8) lgkmcnt(0) (the next stage landed; only the one unit
+// issued after it may still be in flight; this wave's fragment reads of the
+// stage returned), and before the epilogue vmcnt(12) (the tile's scale and
+// bias loads, issued before its K loop, have landed). Loads return in order,
+// so a count is exact whenever at least that many younger loads exist.
 //
 // LDS rows are 128 bytes: 16-byte chunk c of row r sits at physical chunk
 // c ^ ((r >> 1) & 7), which keeps both the DMA writes (lane i writes bytes

@@ -64,8 +64,12 @@ Pinning (what checks each function, beyond "the same formula retyped"):
   to +-127 and the folded softmax scale; identical keys give the mean of the
   quantized values, one dominant key gives its value row; random inputs
   within cosine 0.999 of float64 softmax attention, which a wrong softmax
-  scale fails. Bit parity with the reference's vendored Kitchen kernel is
-  unpinned (its source is not part of the reference).
+  scale fails. ``kitchen_attention`` (the reference's vendored kernel,
+  restated): u8 tiles of exactly 255 on identical keys (the log2 255 offset),
+  a dominant key returning its value row, the kernel's per-thread scale
+  groups, cosine 0.9998 against float64 attention and agreement between its
+  two key-block sizes. Kitchen's quantizer and CUDA's ex2.approx / rcp.approx
+  are absent, so its bits are unpinned.
 
 Functions that only an import of the absent third-party comfy-kitchen 0.2.37
 could pin bit for bit (its GEMM-based rotation summation order) are noted

@@ -4,16 +4,20 @@ The reference routes DiT attention through comfy-kitchen 0.2.37's INT8
 attention (patches/h3_operator_policy.py:153-209: ``prequantize_int8_attention``
 then ``int8_attention_from_prequantized``; patches/kitchen_attention.py:227-238
 and the launcher patches/kitchen_attention_native/attention.cu:20-38, which
-instantiates the vendored SageAttention kernel ``qk_int_sv_i8_attn_kernel``).
-The kernel header and Kitchen's quantizers are not in the reference
-(kitchen_attention_native/vendor is empty; comfy-kitchen is not installed), so
-their bits cannot be reproduced: **parity with the reference is unpinned**.
-This module restates the algorithm this build implements, which follows the
-published SageAttention scheme and the properties the reference's design
-notes record (docs/design/TP2_GROUP32_KITCHEN_DESIGN.md:35-45: INT8 Q/K with
-scales covering the channel reduction, key centering, signed INT8 V,
-quantized probabilities for an integer P.V, FP32 softmax and output state,
-exp2-domain online softmax):
+instantiates the vendored SageAttention kernel ``qk_int_sv_i8_attn_kernel`` of
+kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh and attn_utils.cuh).
+That kernel's arithmetic is restated at the end of this module
+(``kitchen_prepare`` / ``kitchen_attention``); Kitchen's quantizer is not in
+the reference (comfy-kitchen is not installed), so the restatement assumes
+the SageAttention quantizer and is **parity unpinned** for those bits and for
+CUDA's approximate exp2 / reciprocal. This build's GPU kernel implements a
+different scheme, restated first (``prepare`` / ``attention``): two passes
+instead of one online pass, 7-bit probabilities relative to the row's
+largest logit instead of u8 probabilities relative to each 64-key tile's
+largest logit, per-token Q and per-64-key K scales instead of the kernel's
+per-thread groups. Its error against exact attention grows with the key
+count (max-abs error over max |output| about 0.04-0.07 at 1000-16384 random
+keys, against 0.014-0.017 for the restated reference scheme):
 
 prepare (exact, checked bit for bit):
   * K is centred per channel: mean[d] = (sum over tokens of k[t][d], fp32,
@@ -153,3 +157,156 @@ def reference_attention(q, k, v, sm_scale=None):
     w = np.exp(s)
     w = w / w.sum(-1, keepdims=True)
     return np.einsum('bhqk,bhkd->bhqd', w, v)
+
+
+# --------------------------------------------------------------------------
+# The reference's vendored kernel, restated.
+#
+# patches/kitchen_attention_native/attention.cu:20-38 instantiates
+# qk_int_sv_i8_attn_kernel (vendor/qk_int_sv_i8_cuda.cuh, comfy-kitchen
+# 0.2.37) for 128-wide heads with per-thread Q and K scale granularity, INT8
+# V with a fused per-channel V scale, no V mean, FP32 output. Its arithmetic
+# per query row, following the vendored source:
+#   * scores S = q8 . k8 (int32) for key blocks of CTA_K keys (64, or 128 when
+#     Kitchen's packer chooses it: attention.cu:43-66);
+#   * the score scale of a (row, key) pair is fp32(c0 * fp32(qs * ks)) with
+#     c0 = fp32(sm_scale * log2 e) (qk_int_sv_i8_cuda.cuh:170,546-549); the
+#     Q scale is shared by the rows of a 32-row group with the same row mod 8,
+#     the K scale by the keys of a block with the same (key mod 8) // 2 - the
+#     key set of one thread of the MMA quad (:174-227);
+#   * one pass of online softmax in the exp2 domain
+#     (attn_utils.cuh:716-790 update_mdo_i32_u8): the tile maximum
+#     tile_m = max fma(f32(S), scale, -S_U8_OFFSET) with S_U8_OFFSET = log2 255
+#     (attn_utils.cuh:40), the running max m (initially -50000),
+#     smaller = exp2(-|m_prev - tile_m|), the old state (output and
+#     denominator, initially 0 and 1) scaled by smaller when the tile raises
+#     the maximum, the tile's contribution by smaller otherwise;
+#   * probabilities P = sat_u8(rne(exp2(fma(f32(S), scale, -tile_m)))) in
+#     0..255 relative to the tile's own maximum (mma.cuh:769-781 pack_u8x4);
+#   * each thread's denominator adds fp32(sum of four P bytes) * tile_scale;
+#     P . V is exact in int32 (m16n8k32 u8 x s8) and the output accumulates
+#     fma(f32(P . V), tile_scale, O) (attn_utils.cuh:1148-1186);
+#   * the last key block takes the generic path instead
+#     (qk_int_sv_i8_cuda.cuh:900-1000, attn_utils.cuh:569-650,918-934): keys
+#     past Nk get the raw score -1e30, the tile max starts at -50000 in the
+#     raw score domain, and the denominator adds the FP32 probabilities
+#     (((p0 + p1) + (p4 + p5)) per 16-key tile) rather than their u8 codes;
+#   * finally the quad's four denominators are summed ((d0 + d1) + (d2 + d3)),
+#     O is multiplied by 1/d and then by the channel's V scale
+#     (attn_utils.cuh:1103-1130, qk_int_sv_i8_cuda.cuh:1054-1071).
+#
+# Parity unpinned: (1) Kitchen's quantizer (prequantize_int8_attention) is
+# absent from the reference; kitchen_prepare assumes the SageAttention
+# per-thread quantizer (amax / 127 per group, round half away from zero, K
+# centred by its per-channel mean, V per channel). (2) ex2.approx.ftz and
+# rcp.approx are CUDA hardware approximations; exact exp2 and 1/d stand in.
+# (3) The fp32 updates d += den * ts and O *= o_scale are taken as nvcc
+# emits them by default (d += den * ts contracted to one fma).
+# --------------------------------------------------------------------------
+S_U8_OFFSET = F32(7.9943534)
+
+
+def _round_half_away(x):
+    return np.where(x >= 0, np.floor(x + 0.5), np.ceil(x - 0.5))
+
+
+def kitchen_prepare(q, k, v, cta_k=64):
+    """INT8 operands in the layout qk_int_sv_i8_attn_kernel reads, with one
+    effective scale per query row (qs) and per key (ks); see the section
+    comment for what is assumed of Kitchen's quantizer."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    b, h, nq, d = q.shape
+    nk = k.shape[2]
+    nq32 = -(-nq // 32) * 32
+    qp = np.zeros((b, h, nq32, d), F32)
+    qp[:, :, :nq] = q
+    g = qp.reshape(b, h, nq32 // 32, 4, 8, d)                  # row = 32 G + 8 i + j
+    qgs = (np.abs(g).max(axis=(3, 5)) / F32(127)).astype(F32)  # [b, h, G, 8]
+    safe = np.where(qgs > 0, qgs, F32(1))
+    q8 = np.clip(_round_half_away(g / safe[:, :, :, None, :, None]), -128, 127).astype(np.int8)
+    q8 = q8.reshape(b, h, nq32, d)[:, :, :nq]
+    qs = np.broadcast_to(qgs[:, :, :, None, :], (b, h, nq32 // 32, 4, 8)).reshape(b, h, nq32)[:, :, :nq]
+    mean = (k.astype(np.float64).sum(2) / nk).astype(F32)
+    nkp = -(-nk // cta_k) * cta_k
+    kc = np.zeros((b, h, nkp, d), F32)
+    kc[:, :, :nk] = (k - mean[:, :, None, :]).astype(F32)
+    kb = kc.reshape(b, h, nkp // cta_k, cta_k // 8, 4, 2, d)    # key = cta_k B + 8 t + 2 c + e
+    kgs = (np.abs(kb).max(axis=(3, 5, 6)) / F32(127)).astype(F32)   # [b, h, B, 4]
+    safe = np.where(kgs > 0, kgs, F32(1))
+    k8 = np.clip(_round_half_away(kb / safe[:, :, :, None, :, None, None]), -128, 127).astype(np.int8)
+    k8 = k8.reshape(b, h, nkp, d)
+    ks = np.broadcast_to(kgs[:, :, :, None, :, None], kb.shape[:-1]).reshape(b, h, nkp)
+    vs = (np.abs(v).max(2) / F32(127)).astype(F32)
+    safe = np.where(vs > 0, vs, F32(1))
+    v8 = np.zeros((b, h, nkp, d), np.int8)
+    v8[:, :, :nk] = np.clip(_round_half_away(v / safe[:, :, None, :]), -128, 127).astype(np.int8)
+    return dict(q8=q8, qs=np.ascontiguousarray(qs), k8=k8, ks=np.ascontiguousarray(ks), v8=v8, vs=vs, nk=nk,
+                cta_k=cta_k)
+
+
+def _exp2(x):
+    with np.errstate(over='ignore', under='ignore'):
+        return np.exp2(_f32(x).astype(np.float64)).astype(F32)
+
+
+def kitchen_attention(prep, sm_scale=None):
+    """qk_int_sv_i8_attn_kernel's arithmetic (section comment) on
+    kitchen_prepare's operands: [B, H, Nq, D] fp32."""
+    from .w8a8_oracle import fma_f32
+    q8 = prep['q8'].astype(np.int64)
+    k8 = prep['k8'].astype(np.int64)
+    v8 = prep['v8'].astype(np.int64)
+    qs, ks, vs, nk, ck = prep['qs'], prep['ks'], prep['vs'], prep['nk'], prep['cta_k']
+    b, h, nq, d = q8.shape
+    nkp = k8.shape[2]
+    nblk = nkp // ck
+    c0 = F32(F32(default_scale(d) if sm_scale is None else sm_scale) * LOG2E)
+    key = np.arange(ck)
+    thread = (key % 8) // 2                      # the quad thread holding each key of a block
+    tile = key // 16
+    in_tile = key % 16
+    out = np.zeros((b, h, nq, d), F32)
+    for bi in range(b):
+        for hi in range(h):
+            s_all = q8[bi, hi] @ k8[bi, hi].T                       # exact
+            m = np.full(nq, F32(-50000.0), F32)
+            dsum = np.ones((nq, 4), F32)
+            o = np.zeros((nq, d), F32)
+            for bj in range(nblk):
+                keys = bj * ck + key
+                s = s_all[:, keys]
+                kscale = ks[bi, hi][keys]                            # per key (constant per thread)
+                sc = (c0 * (qs[bi, hi][:, None] * kscale[None, :]).astype(F32)).astype(F32)   # [nq, ck]
+                last = bj == nblk - 1
+                if last:
+                    sf = np.where(keys[None, :] < nk, s.astype(F32), F32(-1e30))
+                    mt = np.stack([np.maximum(F32(-50000.0), sf[:, thread == c].max(1)) for c in range(4)], 1)
+                else:
+                    sf = s.astype(F32)
+                    mt = np.stack([sf[:, thread == c].max(1) for c in range(4)], 1)
+                tsc = np.stack([sc[:, np.argmax(thread == c)] for c in range(4)], 1)   # the thread's scale
+                tile_m = fma_f32(mt, tsc, -S_U8_OFFSET).max(1)
+                m_prev = m
+                m = np.maximum(m_prev, tile_m)
+                smaller = _exp2(-np.abs(m_prev - tile_m))
+                o_scale = np.where(m_prev < tile_m, smaller, F32(1))
+                t_scale = np.where(tile_m < m_prev, smaller, F32(1))
+                dsum = (dsum * o_scale[:, None]).astype(F32)
+                o = (o * o_scale[:, None]).astype(F32)
+                p = _exp2(fma_f32(sf, sc, -tile_m[:, None]))
+                u8 = np.clip(np.rint(p), 0, 255).astype(np.int64)
+                for c in range(4):
+                    for t in range(ck // 16):
+                        sel = [16 * t + 2 * c, 16 * t + 2 * c + 1, 16 * t + 8 + 2 * c, 16 * t + 9 + 2 * c]
+                        if last:
+                            part = ((p[:, sel[0]] + p[:, sel[1]]).astype(F32)
+                                    + (p[:, sel[2]] + p[:, sel[3]]).astype(F32)).astype(F32)
+                        else:
+                            part = u8[:, sel].sum(1).astype(F32)
+                        dsum[:, c] = fma_f32(part, t_scale, dsum[:, c])
+                pv = u8 @ v8[bi, hi][keys]                          # exact int32
+                o = fma_f32(pv.astype(F32), t_scale[:, None], o)
+            dt = ((dsum[:, 0] + dsum[:, 1]).astype(F32) + (dsum[:, 2] + dsum[:, 3]).astype(F32)).astype(F32)
+            rcp = (F32(1) / dt).astype(F32)
+            out[bi, hi] = ((o * rcp[:, None]).astype(F32) * vs[bi, hi][None, :]).astype(F32)
+    return out

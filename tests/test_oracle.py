@@ -629,3 +629,64 @@ def test_rank_partials_sum_to_the_unsharded_accumulator():
     swapped = np.concatenate([ranks[0][:, :w // 2], ranks[1][:, w // 2:]], 1)
     bad = o.row_partial(swapped, wq2[:, :w // 2], row_max=gmax2, swiglu=True)[0]
     assert not np.array_equal(bad.astype(np.int64) + p2[1][0], acc2)
+
+
+# ------------------------------------------------ the reference attention kernel
+def _qkv_np(rng, nq, nk, kshift=0.5):
+    q = rng.standard_normal((1, 1, nq, 128)).astype(np.float16).astype(np.float32)
+    k = (rng.standard_normal((1, 1, nk, 128)) + kshift).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((1, 1, nk, 128)).astype(np.float16).astype(np.float32)
+    return q, k, v
+
+
+def test_kitchen_restatement_pins():
+    from oracle import int8_attention as oa
+    assert abs(float(oa.S_U8_OFFSET) - np.log2(255.0)) < 1e-6     # exp2 of the offset is 255
+    rng = np.random.default_rng(23)
+    # identical keys: every non-last tile's probabilities are exactly 255, so
+    # the output is the dequantized mean of V (the last tile sums its FP32
+    # probabilities, 254.9999..., into the denominator: within 1e-6). The key
+    # count is a whole number of blocks: centred identical keys have a zero
+    # score scale, under which the kernel's -1e30 out-of-bound score would no
+    # longer mask a padded key.
+    q, _, v = _qkv_np(rng, 40, 256)
+    k = np.repeat(rng.standard_normal((1, 1, 1, 128)).astype(np.float32), 256, axis=2)
+    prep = oa.kitchen_prepare(q, k, v)
+    out = oa.kitchen_attention(prep)
+    want = (prep['v8'][0, 0, :256].astype(np.float64).mean(0) * prep['vs'][0, 0])[None, :]
+    assert np.abs(out[0, 0] - want).max() <= 1e-5 * np.abs(want).max()
+    # one key far above the rest: the output is that key's dequantized value row
+    q, k, v = _qkv_np(rng, 8, 300)
+    k[0, 0, 137] = q[0, 0, 0] * 40
+    out = oa.kitchen_attention(oa.kitchen_prepare(q[:, :, :1], k, v))
+    prep = oa.kitchen_prepare(q[:, :, :1], k, v)
+    row = prep['v8'][0, 0, 137].astype(np.float64) * prep['vs'][0, 0]
+    assert np.abs(out[0, 0, 0] - row).max() <= 1e-3 * np.abs(row).max()
+    # the scales follow the kernel's thread grouping: rows 32 G + 8 i + j share
+    # a Q scale, keys with the same (key mod 8) // 2 of a block share a K scale
+    q, k, v = _qkv_np(rng, 70, 130)
+    prep = oa.kitchen_prepare(q, k, v)
+    qs, ks = prep['qs'][0, 0], prep['ks'][0, 0]
+    assert qs[3] == qs[11] == qs[19] == qs[27] and qs[3] != qs[4]
+    assert ks[2] == ks[3] == ks[10] == ks[11] and ks[2] != ks[4] and ks[2] != ks[66]
+
+
+def test_kitchen_restatement_and_this_scheme_against_exact():
+    """Both schemes against exact float64 softmax attention, and this build's
+    scheme against the reference restatement (the error the build carries)."""
+    from oracle import int8_attention as oa
+    rng = np.random.default_rng(29)
+    for nq, nk, ref_tol, ours_tol in ((64, 64, 0.02, 0.02), (64, 1000, 0.03, 0.07), (32, 4000, 0.03, 0.10)):
+        q, k, v = _qkv_np(rng, nq, nk)
+        exact = oa.reference_attention(q, k, v)
+        ref = oa.kitchen_attention(oa.kitchen_prepare(q, k, v))
+        ours = oa.attention(oa.prepare(q, k, v))
+        scale = np.abs(exact).max()
+        assert np.abs(ref - exact).max() <= ref_tol * scale, nk
+        assert np.abs(ours - exact).max() <= ours_tol * scale, nk
+        cos = (ref * exact).sum() / np.sqrt((ref * ref).sum() * (exact * exact).sum())
+        assert cos > 0.9998, (nk, cos)
+        # the two CTA_K choices of the reference's launcher agree within its own error
+        if nk >= 128:
+            ref128 = oa.kitchen_attention(oa.kitchen_prepare(q, k, v, cta_k=128))
+            assert np.abs(ref128 - ref).max() <= 2 * ref_tol * scale
