@@ -832,9 +832,61 @@ def run_dit_attention_block(args, torch, dev):
     return res
 
 
+def run_reference_shapes(args, torch, dev):
+    """The reference's own published operator shapes (one TP2 rank): each
+    projection through the API (quantize + GEMM + epilogue; row shards give
+    their FP32 partial) and its GEMM alone, next to the reference's T4 time."""
+    from w8a8 import kernels, workloads
+    from w8a8.dit_column_linear import column_linear
+    from w8a8.tp_dit import RowParallelLinearINT8
+    rows = {}
+    for name, (role, m, n, k, t4_ms, src) in workloads.REFERENCE_SHAPES.items():
+        data = workloads.reference_shape(name)
+        wq, ws = workloads.quantize_weight(data['w'], dev)
+        x = data['x'].to(dev)
+        if role == 'column':
+            full = lambda: column_linear(x, wq, ws)  # noqa: E731
+            q, a = kernels.quantize_rows(x, convrot=True, round_rotated=True)
+            gemm = lambda: kernels.gemm(q, wq, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=ws)  # noqa: E731
+        else:
+            shard = RowParallelLinearINT8(2 * k, n, world_size=2, device=dev)
+            shard.weight.data.copy_(wq)
+            shard.weight_scale.data.copy_(ws)
+            act = 'swiglu' if role == 'fc2' else None
+            full = lambda: shard.partial(x, act)  # noqa: E731
+            if role == 'fc2':
+                r = kernels.swiglu_quantize(x)
+                q, a = r['q'], r['scale']
+            else:
+                q, a = kernels.quantize_rows(x, convrot=True, round_rotated=False)
+            gemm = lambda: kernels.gemm(q, wq, epilogue=kernels.EPI_ROW, row_scale=a, col_scale=ws,  # noqa: E731
+                                        out_dtype=torch.float32)
+        # Interleaved repeats (the clock settles over the first calls); the
+        # faster of two rounds each.
+        tf = tg = float('inf')
+        for _ in range(2):
+            tf = min(tf, timed(torch, full, args.steps, args.warmup))
+            tg = min(tg, timed(torch, gemm, args.steps, args.warmup))
+        ops = 2.0 * m * n * k
+        row = dict(role=role, m=m, n=n, k=k, api_us=round(tf * 1e3, 1), gemm_us=round(tg * 1e3, 1),
+                   gemm_tops=round(ops / (tg * 1e-3) / 1e12, 1),
+                   gemm_frac=round(ops / (tg * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4))
+        if t4_ms is not None:
+            t_ours = tg if name.startswith('dit') else tf
+            row.update(t4_ms=t4_ms, t4_source=f'docs/reports/{src}', speedup_vs_t4=round(t4_ms / t_ours, 1))
+        rows[name] = row
+    total_ops = sum(2.0 * v['m'] * v['n'] * v['k'] for v in rows.values())
+    total_us = sum(v['gemm_us'] for v in rows.values())
+    return dict(metric='reference operator shapes: GEMM us and TOPS (one TP2 rank, one MI355X)',
+                value=round(total_ops / (total_us * 1e-6) / 1e12, 1), unit='TOPS', higher_is_better=True,
+                dtype='int8', data='synthetic (seeded N(0,1) activations with x20 outlier channels, N(0,0.02) '
+                'weights quantized per channel)', config=dict(workload='reference_shapes'), shapes=rows)
+
+
 WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_attention': run_dit_attention, 'dit_attention_block': run_dit_attention_block, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
              'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv, 'dit_qkv_rope': run_dit_qkv_rope,
-             'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard}
+             'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard,
+             'reference_shapes': run_reference_shapes}
 
 
 def main():

@@ -15,6 +15,12 @@ Shapes:
                   activations N(0, 0.5)
   dit_half_shard  M=204336 in 16384-row chunks; QKV 3072 -> 4608, FC1
                   3072 -> 2x4096, FC2 4096 -> 3072 with an FP32 output
+  reference_shapes  the shapes of the reference's own published operator
+                  timings (one TP2 rank of MiniMax-H3): DiT S=6814 with hidden
+                  5376 (QKV 5376 -> 10752, O 3584 -> 5376, FC1 5376 -> 14336,
+                  FC2 7168 -> 5376) and the text encoder at S=353 with hidden
+                  5120 (q 5120 -> 4096, k/v 5120 -> 512, gate/up 5120 -> 12800,
+                  down 12800 -> 5120)
 """
 import torch
 
@@ -191,6 +197,38 @@ def dit_attention_block(m=None, seed=None):
     k_gain = torch.rand(128, generator=g) + 0.5
     return dict(x=x, weight=weight, shift=shift, scale=scale, gate=gate, segments=segments, eps=s['eps'],
                 w_qkv=w_qkv, w_o=w_o, freqs=freqs, q_gain=q_gain, k_gain=k_gain, heads=heads, hidden=hidden)
+
+
+# name: (role, M, N, K, the reference's T4 rank-0 time in ms for the same
+# operator, its source). Roles: 'column' (ConvRot256 quantize + GEMM + column
+# dequant), 'row' (FP32 ConvRot256 quantize of the rank's K slice + GEMM ->
+# FP32 partial), 'fc2' (fused SwiGLU/ConvRot256 prologue on [M, 2K] + GEMM ->
+# FP32 partial). The T4 times are the GEMM alone for the DiT shapes
+# (docs/reports/TP2_OPERATOR_RESULTS.md:132-135) and the complete row
+# projection (prologue, GEMM and scaled-FP16 SUM) for the TE down projection
+# (docs/reports/FP16_FC2_FUSION_VIDEO_SPLIT_20261022.md:149).
+REFERENCE_SHAPES = {
+    'dit_qkv': ('column', 6814, 10752, 5376, 20.02, 'TP2_OPERATOR_RESULTS.md:132'),
+    'dit_o': ('row', 6814, 5376, 3584, 6.51, 'TP2_OPERATOR_RESULTS.md:133'),
+    'dit_fc1': ('column', 6814, 14336, 5376, 28.69, 'TP2_OPERATOR_RESULTS.md:134'),
+    'dit_fc2': ('fc2', 6814, 5376, 7168, 14.23, 'TP2_OPERATOR_RESULTS.md:135'),
+    'te_q': ('column', 353, 4096, 5120, None, None),
+    'te_kv': ('column', 353, 512, 5120, None, None),
+    'te_gate_up': ('column', 353, 12800, 5120, None, None),
+    'te_down': ('fc2', 353, 5120, 12800, 1.906, 'FP16_FC2_FUSION_VIDEO_SPLIT_20261022.md:149'),
+}
+
+
+def reference_shape(name, seed=10):
+    """Seeded inputs of one reference shape: x fp16 [M, K] (N(0,1) with x20
+    outlier channels; [M, 2K] gate|up for the 'fc2' role) and w fp32 [N, K]."""
+    role, m, n, k = REFERENCE_SHAPES[name][:4]
+    g = torch.Generator().manual_seed(seed + sorted(REFERENCE_SHAPES).index(name))
+    if role == 'fc2':
+        x = (torch.randn((m, 2 * k), generator=g)).half()
+    else:
+        x = activations(g, m, k, 8)
+    return dict(role=role, x=x, w=weights(g, n, k))
 
 
 def quantize_weight(w, device):
