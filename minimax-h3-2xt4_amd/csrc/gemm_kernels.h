@@ -1270,16 +1270,6 @@ inline int current_device(int& dev) {
   return W8A8_OK;
 }
 
-// Compute units of device dev (cached per device).
-inline int device_cus(int dev) {
-  static std::atomic<int> cus[64];
-  int n = cus[dev].load(std::memory_order_acquire);
-  if (n > 0) return n;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-  cus[dev].store(n, std::memory_order_release);
-  return n;
-}
-
 template <int EPI, int OUT, int FLAGS>
 int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s) {
   // The LDS ring and staging area exceed the 64 KB default: raise the

@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <stdarg.h>
 
+#include <atomic>
+
 #include "w8a8.h"
 
 namespace w8a8 {
@@ -22,6 +24,23 @@ inline int elem_size(int dt) {
     case W8A8_I8: return 1;
     default: return 0;
   }
+}
+
+// Compute units of device dev (0 <= dev < 64; cached per device).
+inline int device_cus(int dev) {
+  static std::atomic<int> cus[64];
+  int n = cus[dev].load(std::memory_order_acquire);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  cus[dev].store(n, std::memory_order_release);
+  return n;
+}
+
+// Compute units of the current device (256 if it cannot be queried).
+inline int current_device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  return device_cus(dev);
 }
 
 inline int launch_status(const char* what) {
