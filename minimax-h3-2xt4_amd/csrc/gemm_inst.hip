@@ -21,13 +21,21 @@ int launch_gemm_partials(const GemmParams& p, int dev, hipStream_t s) {
   return launch_persistent<kEpiInt32, kI32, 0>(p, tiles, dev, s);
 }
 
-// Split K when the output tiles leave CUs idle. Cost model in units of one
-// K = 128 stage of a 256x256 tile (about 1 us on the power-limited clock):
-// rounds of work items times stages per item, plus the partial sums'
-// write-and-read traffic at about 6.5 TB/s.
+// K split and workspace bytes of an m x n x k GEMM. M <= 64 takes the
+// weight-streaming kernel's split (stream_ksplit). Above, split K when the
+// output tiles leave CUs idle. Cost model in units of one K = 128 stage of a
+// 256x256 tile (about 1 us on the power-limited clock): rounds of work items
+// times stages per item, plus the partial sums' write-and-read traffic at
+// about 6.5 TB/s.
 int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_bytes) {
   *workspace_bytes = 0;
-  if (m <= kSkinnyMaxM || k % kSK != 0) return 1;
+  if (m <= kSkinnyMaxM) {   // the weight-streaming kernel's own split
+    if (!stream_applies(m, k)) return 1;
+    const int ks = stream_ksplit(n, k, device_cus(dev));
+    if (ks > 1) *workspace_bytes = (int64_t)ks * m * n * 4;
+    return ks;
+  }
+  if (k % kSK != 0) return 1;
   if ((m - 1) * k + k >= (1ll << 32) || (n - 1) * k + k >= (1ll << 32)) return 1;
   const int64_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
   const int64_t kstages = k / kSK, cus = device_cus(dev);

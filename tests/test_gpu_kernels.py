@@ -111,6 +111,54 @@ def test_gemm_skinny_epilogues(gpu, m, epi, out_dtype, bias_dtype):
     assert_bits_equal(np_of(got), want, f'skinny m={m} {epi} {out_dtype} {bias_dtype}')
 
 
+STREAM_CASES = [
+    # (m, n, k): 16 < M <= 64 with K % 128 == 0 takes the weight-streaming kernel.
+    # These split K (two or four workgroups per 64-row block, partials in
+    # the workspace) unless the workspace is withheld; ragged N and M.
+    (20, 4096, 14336), (64, 4100, 4096), (17, 203, 14336), (49, 4096, 14336),
+]
+
+
+@pytest.mark.parametrize('m,n,k', STREAM_CASES)
+def test_gemm_stream_split_and_whole(gpu, m, n, k):
+    print(f'stream gemm {m}x{n}x{k}', flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.01 + 1e-4
+    ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
+    bias = (torch.randn((n,), generator=g) * 0.01).half()
+    res = randn16(g, (m, n), 1 / 512)
+    assert kernels.gemm_workspace_bytes(m, n, k, gpu) > 0        # the default call splits K
+    acc = o.int_mm(np_of(a), np_of(b))
+    ag, bg = a.to(gpu), b.to(gpu)
+    none = torch.empty(0, dtype=torch.uint8, device=gpu)
+    for workspace in (None, none):
+        assert_bits_equal(np_of(kernels.gemm(ag, bg, workspace=workspace)), acc, f'int32 ws={workspace is None}')
+        got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                           bias=bias.to(gpu), residual=res.to(gpu), out_dtype=torch.float16, workspace=workspace)
+        want = o.residual_add(np_of(res), o.dequantize_row(acc, np_of(rs), np_of(ws), 'f16', np_of(bias)))
+        assert_bits_equal(np_of(got), want, f'row+bias+residual ws={workspace is None}')
+        got = kernels.gemm(ag, bg, epilogue=kernels.EPI_COLUMN, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                           out_dtype=torch.float32, workspace=workspace)
+        assert_bits_equal(np_of(got), o.dequantize_column(acc, np_of(rs), np_of(ws), 'f32'),
+                          f'column f32 ws={workspace is None}')
+
+
+def test_gemm_stream_strided_weight_and_short_k(gpu):
+    g = torch.Generator().manual_seed(23)
+    wide = randi8(g, (300, 1536))
+    b = wide[:, :1024]                  # weight row stride 1536
+    a = randi8(g, (33, 1024))
+    got = kernels.gemm(a.to(gpu), wide.to(gpu)[:, :1024])
+    assert_bits_equal(np_of(got), o.int_mm(np_of(a), np_of(b).copy()), 'strided weight')
+    # K = 128 and 256: one or two steps, so some of the four waves get none
+    for k in (128, 256, 384):
+        a = randi8(g, (64, k))
+        b = randi8(g, (130, k))
+        assert_bits_equal(np_of(kernels.gemm(a.to(gpu), b.to(gpu))), o.int_mm(np_of(a), np_of(b)), f'k={k}')
+
+
 def test_gemm_scalar_weight_scale_and_residual(gpu):
     g = torch.Generator().manual_seed(12)
     m, n, k = 130, 96, 512

@@ -38,7 +38,8 @@ def _noalloc(args):
 @pytest.mark.parametrize('call', [0, 1])
 def test_noalloc_gemm_equals_gemm_on_two_calls(gpu, call):
     del call   # the whole sequence runs twice: the second time the array holds the last shape's partials
-    for m, n, k in ((512, 4096, 14336), (200, 1000, 4096)):
+    # persistent tiles with split K, then the weight-streaming kernel's split
+    for m, n, k in ((512, 4096, 14336), (200, 1000, 4096), (64, 4096, 14336), (24, 1000, 4096)):
         print(f'noalloc gemm {m}x{n}x{k}', flush=True)
         need = kernels.gemm_workspace_bytes(m, n, k, gpu)
         assert 0 < need <= _abi.GEMM_SCRATCH_BYTES      # the shape splits K and fits the scratch
