@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 10
+#define W8A8_ABI_VERSION 11
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -248,9 +248,10 @@ int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
  *     of channel c for p = 16 h + 4 g + i.
  *   attention: S = q8.k8 (int32); m = the query's largest logit
  *     fp32(max(S) * qs * ks[block]); probabilities
- *     P = rne(exp2(fma(S, qs * ks, log2(127) - m - |m| 2^-22))) in 0..127
- *     (hardware exp2); P.v8 and sum(P) exact in int32 (nk <= 131072);
- *     output fp32(fp32(f32(acc) * vs[c]) / f32(sum P)).
+ *     P = min(255, rne(exp2(fma(S, qs * ks, log2(255) - m)))) in 0..255
+ *     (hardware exp2); acc = P.v8 exact (the MFMA takes P - 128, and
+ *     128 * vsum is added per channel) and sum(P) exact
+ *     (nk <= 131072); output fp32(fp32(f32(acc) * vs[c]) / f32(sum P)).
  * q, k, v: [b, h, nq|nk, d] with element strides {batch, head, token} given
  * per tensor and the d == 128 channels contiguous (e.g. the q, k and v
  * columns of a packed [tokens, 3 * h * d] QKV projection, or contiguous
@@ -278,6 +279,7 @@ typedef struct W8A8AttnPrepareArgs {
   float* ks;               /* [b, h, nkp / 64] */
   int8_t* vt8;             /* [b, h, d, nkp] */
   float* vs;               /* [b, h, d] */
+  int32_t* vsum;           /* [b, h, d]: sum over the keys of vt8, per channel */
   void* workspace;         /* w8a8_attention_workspace_size(b, h, nk) bytes */
   int64_t workspace_bytes;
   void* stream;
@@ -297,6 +299,7 @@ typedef struct W8A8AttentionArgs {
   const float* ks;
   const int8_t* vt8;
   const float* vs;
+  const int32_t* vsum;
   int64_t b;
   int64_t h;
   int64_t nq;

@@ -24,8 +24,8 @@ static_assert(sizeof(W8A8RopeEpilogue) == 48, "W8A8RopeEpilogue layout");
 static_assert(sizeof(W8A8DequantArgs) == 144, "W8A8DequantArgs layout");
 static_assert(sizeof(W8A8NormArgs) == 144, "W8A8NormArgs layout");
 static_assert(sizeof(W8A8RmsRopeArgs) == 104, "W8A8RmsRopeArgs layout");
-static_assert(sizeof(W8A8AttnPrepareArgs) == 216, "W8A8AttnPrepareArgs layout");
-static_assert(sizeof(W8A8AttentionArgs) == 136, "W8A8AttentionArgs layout");
+static_assert(sizeof(W8A8AttnPrepareArgs) == 224, "W8A8AttnPrepareArgs layout");
+static_assert(sizeof(W8A8AttentionArgs) == 144, "W8A8AttentionArgs layout");
 
 extern "C" int w8a8_abi_version(void) { return W8A8_ABI_VERSION; }
 

@@ -2,10 +2,11 @@
 // (key centering, per-token Q scales, per-64-key K scales, per-channel V
 // scales, V transposed) and the attention kernel (S = Q.K^T on INT8 MFMA;
 // a first pass finds each query's largest logit, the second quantizes the
-// exp2-domain probabilities against it to integers 0..127 for an INT8 MFMA
-// P.V product, the denominator being the sum of the same integers, so the
-// whole accumulation is exact in int32). The exponentials use the hardware
-// exp2 (v_exp_f32).
+// exp2-domain probabilities against it to integers P in 0..255 and feeds
+// P - 128 to the signed INT8 MFMA P.V product; the 128 * sum over keys of V
+// it leaves out is one per-channel integer that the preparation sums. The denominator is the sum of the same integers P, so the whole
+// accumulation is exact. The exponentials use the hardware exp2
+// (v_exp_f32).
 //
 // Layout of the attention kernel: a workgroup of eight wavefronts (two per
 // SIMD) takes 256 queries of one (batch, head); a wavefront owns 32. Keys come in
@@ -33,7 +34,7 @@ constexpr int kAttnWaves = 8;     // wavefronts per workgroup
 constexpr int kAttnBQ = kAttnWaves * kAttnWaveQ;   // queries per workgroup
 constexpr int kAttnDma = 8 / kAttnWaves;           // 1 KB DMA instructions per wave and tile
 constexpr float kLog2e = 0x1.715476p+0f;    // fp32(log2(e))
-constexpr float kLog2_127 = 0x1.bf469cp+2f; // fp32(log2(127))
+constexpr float kLog2_255 = 0x1.ffa37cp+2f; // fp32(log2(255))
 
 // Element strides of a [batch, head, token, channel] tensor whose channels
 // are contiguous; at(bh, t) is the offset of token t's row of the flat
@@ -59,6 +60,7 @@ struct AttnPrepParams {
   float* ks;
   int8_t* vt8;
   float* vs;
+  int32_t* vsum;   // sum over the keys of vt8 per channel (int32 atomics)
   float* part_sum;
   float* part_max;
   float* kmean;
@@ -163,6 +165,7 @@ __global__ __launch_bounds__(128) void attn_finalize_kernel(AttnPrepParams p) {
   const float sv = row_scale_of(m);
   p.vs[bh * kAttnD + d] = sv;
   p.vrcp[bh * kAttnD + d] = 1.0f / sv;
+  p.vsum[bh * kAttnD + d] = 0;   // the quant kernel adds each block's codes
 }
 
 // 32 consecutive channels [32 part, 32 part + 32) of token t (16-byte loads).
@@ -306,7 +309,16 @@ __global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
       const int key = 8 * ((pos >> 2) & 3) + 4 * (pos >> 4) + (pos & 3);
       vb[pos] = vtile[(32 * gq + key) * kAttnD + ch];
     }
-    if (k_blk) store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * gq, vb);
+    if (k_blk) {
+      store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * gq, vb);
+      // The block's codes of channel ch, added to its sum over the keys
+      // (integer atomics: exact in any order).
+      int sum = 0;
+#pragma unroll
+      for (int pos = 0; pos < 32; ++pos) sum += vb[pos];
+      sum += __shfl_xor(sum, 1, 64);
+      if (gq == 0) atomicAdd(p.vsum + bh * kAttnD + ch, sum);
+    }
   }
 }
 
@@ -344,6 +356,7 @@ struct AttnParams {
   const float* ks;
   const int8_t* vt8;
   const float* vs;
+  const int32_t* vsum;
   void* out;
   Strides3 ost;
   int nq, nk, nkp, nblk;
@@ -524,12 +537,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     if (u + 6 < npairs) step(u + 6, stage0, stage1, a0, a1, b0, b1);
   }
   const float m = fmaxf(ml, __shfl_xor(ml, 32, 64));
-  // log2(127) - m, lowered by |m| 2^-22 so that the largest exponent cannot
-  // pass log2(127) by more than a few ulps (P <= 127).
-  const float nm = (kLog2_127 - m) - fabsf(m) * 0x1p-22f;
+  const float nm = kLog2_255 - m;
 
-  // Pass 2: P = rne(exp2(fma(S, c_j, nm))) in 0..127, O^T += V^T.P^T and
-  // sum(P), exact in int32.
+  // Pass 2: P = min(255, rne(exp2(fma(S, c_j, nm)))) (v_cvt_pk_u8_f32
+  // rounds to nearest even and saturates), O^T += V^T.(P - 128)^T and
+  // sum(P - 128), exact in int32.
   v16i oi[4];
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) oi[ct] = v16i{};
@@ -544,11 +556,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
         float qv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) qv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)s[t][4 * g + i], c, nm));
-        // v_cvt_pk_u8_f32 rounds to nearest even and packs the byte.
         uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(qv[0], 0, 0u);
         w = __builtin_amdgcn_cvt_pk_u8_f32(qv[1], 1, w);
         w = __builtin_amdgcn_cvt_pk_u8_f32(qv[2], 2, w);
-        pw[t][g] = __builtin_amdgcn_cvt_pk_u8_f32(qv[3], 3, w);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(qv[3], 3, w);
+        pw[t][g] = w ^ 0x80808080u;   // P - 128 as signed bytes
         li = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, li, false);
       }
 #pragma unroll
@@ -605,10 +617,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     if (j + 2 < p.nblk) step(j + 2, stage2, stage3, stage1, sa, sb);
     if (j + 3 < p.nblk) step(j + 3, stage3, stage0, stage2, sb, sa);
   }
-  // Keys past nk in the last block have all-zero K and V^T codes: each
-  // scored 0, added nothing to P.V, and added the same byte
-  // cvt_pk_u8(exp2(fma(0, c, nm))) to this lane's sum (as a signed byte,
-  // like every other); take them out exactly.
+  // Each lane summed P - 128 over its 32 keys of every block: sum(P) puts
+  // the 128s back. Keys past nk in the last block have all-zero K and V^T
+  // codes: each scored 0, added nothing to P.V and the same P =
+  // cvt_pk_u8(exp2(fma(0, c, nm))) to this lane's sum; take them out exactly.
+  li += 128 * 32 * p.nblk;
   {
     const int jl = p.nblk - 1, kl = p.nk - kAttnBK * jl;
     int npad = 0;
@@ -616,13 +629,14 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     for (int x = 0; x < 32; ++x) npad += (32 * (x >> 4) + 8 * ((x >> 2) & 3) + 4 * hh + (x & 3)) >= kl;
     if (npad) {
       const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(0.0f, qscale * ksc[jl], nm));
-      li -= npad * (int)(int8_t)(__builtin_amdgcn_cvt_pk_u8_f32(e, 0, 0u) & 0xffu);
+      li -= npad * (int)(__builtin_amdgcn_cvt_pk_u8_f32(e, 0, 0u) & 0xffu);
     }
   }
   const float l = (float)(li + __shfl_xor(li, 32, 64));
   if (q0 + fr >= p.nq) return;
   const int64_t orow = p.ost.at(bh, q0 + fr);
   const float* vsc = p.vs + bh * kAttnD;
+  const int* vsm = p.vsum + bh * kAttnD;   // O = O' + 128 * vsum, exact in int64
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -630,9 +644,11 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       const int c0 = 32 * ct + 8 * g + 4 * hh;
       const float4 s4 = *reinterpret_cast<const float4*>(vsc + c0);
       const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+      const int4 m4 = *reinterpret_cast<const int4*>(vsm + c0);
+      const int vm[4] = {m4.x, m4.y, m4.z, m4.w};
       float y[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = ((float)oi[ct][4 * g + i] * sv[i]) / l;
+      for (int i = 0; i < 4; ++i) y[i] = ((float)((int64_t)oi[ct][4 * g + i] + 128 * (int64_t)vm[i]) * sv[i]) / l;
       if constexpr (OUT == kF32) {
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + c0) = make_float4(y[0], y[1], y[2], y[3]);
       } else {
@@ -690,10 +706,11 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention_prepare: empty problem");
   W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536,
                "w8a8_attention_prepare: sizes out of range");
-  W8A8_REQUIRE(a->q && a->k && a->v && a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->workspace,
+  W8A8_REQUIRE(a->q && a->k && a->v && a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->vsum &&
+                   a->workspace,
                "w8a8_attention_prepare: null buffer");
   W8A8_REQUIRE(aligned16(a->q) && aligned16(a->k) && aligned16(a->v) && aligned16(a->q8) && aligned16(a->k8) &&
-                   aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->workspace),
+                   aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->vsum) && aligned16(a->workspace),
                "w8a8_attention_prepare: tensors must be 16-byte aligned");
   W8A8_REQUIRE(a->workspace_bytes >= w8a8_attention_workspace_size(a->b, a->h, a->nk),
                "w8a8_attention_prepare: workspace below w8a8_attention_workspace_size()");
@@ -712,7 +729,7 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   p.nkp = p.nblk * kAttnBK;
   p.chunks = (int)attn_chunks(a->nk);
   p.c0 = a->sm_scale * kLog2e;
-  p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs;
+  p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs; p.vsum = a->vsum;
   const int64_t bh = a->b * a->h;
   float* ws = reinterpret_cast<float*>(a->workspace);
   p.part_sum = ws;
@@ -743,19 +760,22 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention: head dimension %d != 128", a->d);
   W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention: empty problem");
   W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536, "w8a8_attention: sizes out of range");
-  if (a->nk > (1 << 17)) {   // the int32 P.V sums hold nk * 127 * 127
+  if (a->nk > (1 << 17)) {   // the int32 sums of (P - 128).V hold nk * 128 * 127
     set_error("w8a8_attention: at most 131072 keys (exact int32 accumulation)");
     return W8A8_ERR_UNSUPPORTED;
   }
-  W8A8_REQUIRE(a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->out, "w8a8_attention: null buffer");
-  W8A8_REQUIRE(aligned16(a->q8) && aligned16(a->k8) && aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->out),
+  W8A8_REQUIRE(a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->vsum && a->out,
+               "w8a8_attention: null buffer");
+  W8A8_REQUIRE(aligned16(a->q8) && aligned16(a->k8) && aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->vsum) &&
+                   aligned16(a->out),
                "w8a8_attention: tensors must be 16-byte aligned");
   const int64_t extents[3] = {a->b, a->h, a->nq};
   W8A8_REQUIRE(strides_aligned(a->out_strides, a->out_dtype == W8A8_F16 ? 2 : 4),
                "w8a8_attention: out strides must be non-negative multiples of 16 bytes");
   W8A8_REQUIRE(strides_disjoint(a->out_strides, extents), "w8a8_attention: out strides make rows overlap");
   AttnParams p;
-  p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs; p.out = a->out;
+  p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs; p.vsum = a->vsum;
+  p.out = a->out;
   p.ost = strides3(a->out_strides, a->h);
   p.nq = (int)a->nq; p.nk = (int)a->nk;
   p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);

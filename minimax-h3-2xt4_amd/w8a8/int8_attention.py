@@ -8,7 +8,7 @@ heads without masks. q, k, v are [batch, heads, tokens, 128] fp16 or fp32; the
 output has q's dtype. Two libw8a8 calls: the preparation (key centering,
 per-token Q and per-64-key K scales, per-channel V scales, INT8 codes, V
 transposed) and the attention kernel (INT8 MFMA for Q.K^T and P.V, two passes:
-the row maxima, then 7-bit probabilities relative to them with FP32 scales).
+the row maxima, then u8 probabilities relative to them with FP32 scales).
 The reference's kernel (kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh)
 is a one-pass online softmax with u8 probabilities relative to each key tile's
 maximum and per-thread Q/K scale groups; this scheme is close to it on short

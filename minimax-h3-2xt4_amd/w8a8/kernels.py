@@ -475,7 +475,7 @@ def attention_prepare(q, k, v, *, sm_scale=None):
     128] (fp16 or fp32). The inputs are read in place when their channels
     are contiguous and their strides 16-byte multiples (e.g. transposed views
     of a packed QKV projection), else from contiguous copies. Returns a dict
-    with q8, qs, k8, ks, vt8, vs (device tensors) and the shape."""
+    with q8, qs, k8, ks, vt8, vs, vsum (device tensors) and the shape."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError('q, k, v must be [batch, heads, tokens, dim]')
     _device(q, k, v)
@@ -504,6 +504,7 @@ def attention_prepare(q, k, v, *, sm_scale=None):
                 ks=torch.empty((b, h, nkp // ATTN_BLOCK_K), dtype=torch.float32, device=dev),
                 vt8=torch.empty((b, h, d, nkp), dtype=torch.int8, device=dev),
                 vs=torch.empty((b, h, d), dtype=torch.float32, device=dev),
+                vsum=torch.empty((b, h, d), dtype=torch.int32, device=dev),
                 shape=(b, h, nq, nk, d))
     with torch.cuda.device(dev):
         nbytes = int(_abi.load().w8a8_attention_workspace_size(b, h, nk))
@@ -513,7 +514,8 @@ def attention_prepare(q, k, v, *, sm_scale=None):
                                 k_strides=_row_strides(k), v_strides=_row_strides(v),
                                 q8=prep['q8'].data_ptr(), qs=prep['qs'].data_ptr(), k8=prep['k8'].data_ptr(),
                                 ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(), vs=prep['vs'].data_ptr(),
-                                workspace=ws.data_ptr(), workspace_bytes=nbytes, stream=_abi.stream_of(q))
+                                vsum=prep['vsum'].data_ptr(), workspace=ws.data_ptr(), workspace_bytes=nbytes,
+                                stream=_abi.stream_of(q))
     _abi.call('w8a8_attention_prepare', args)
     return prep
 
@@ -533,7 +535,8 @@ def attention(prep, *, out_dtype=torch.float16, out=None):
         raise ValueError('out must be a [B, H, Nq, D] view of out_dtype with contiguous, 16-byte aligned rows')
     args = _abi.AttentionArgs(out_dtype=_abi.DTYPE_CODE[out_dtype], q8=q8.data_ptr(), qs=prep['qs'].data_ptr(),
                               k8=prep['k8'].data_ptr(), ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(),
-                              vs=prep['vs'].data_ptr(), b=b, h=h, nq=nq, nk=nk, d=d, out=out.data_ptr(),
+                              vs=prep['vs'].data_ptr(), vsum=prep['vsum'].data_ptr(), b=b, h=h, nq=nq, nk=nk, d=d,
+                              out=out.data_ptr(),
                               out_strides=_row_strides(out),
                               stream=_abi.stream_of(q8))
     _abi.call('w8a8_attention', args)

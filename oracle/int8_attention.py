@@ -12,12 +12,13 @@ the reference (comfy-kitchen is not installed), so the restatement assumes
 the SageAttention quantizer and is **parity unpinned** for those bits and for
 CUDA's approximate exp2 / reciprocal. This build's GPU kernel implements a
 different scheme, restated first (``prepare`` / ``attention``): two passes
-instead of one online pass, 7-bit probabilities relative to the row's
-largest logit instead of u8 probabilities relative to each 64-key tile's
-largest logit, per-token Q and per-64-key K scales instead of the kernel's
-per-thread groups. Its error against exact attention grows with the key
-count (max-abs error over max |output| about 0.04-0.07 at 1000-16384 random
-keys, against 0.014-0.017 for the restated reference scheme):
+instead of one online pass, u8 probabilities relative to the row's largest
+logit instead of relative to each 64-key tile's largest logit, per-token Q
+and per-64-key K scales instead of the kernel's per-thread groups. The GPU
+feeds P - 128 to its signed INT8 MFMA and adds 128 * (sum over keys of v8)
+per channel afterwards, which gives the same integer P . v8. Its error
+against exact attention grows with the key count (max-abs error over max
+|output| in tests/test_oracle.py, against the restated reference scheme):
 
 prepare (exact, checked bit for bit):
   * K is centred per channel: mean[d] = (sum over tokens of k[t][d], fp32,
@@ -29,15 +30,16 @@ prepare (exact, checked bit for bit):
     c0 = fp32(sm_scale * log2(e)), so logits come out in the exp2 domain.
   * K: one scale per 64-key block (amax over the block's 64 x 128 centred
     values), k8 = sat(rne(kc / s)); keys past Nk are zero.
-  * V: one scale per channel (amax over all tokens), v8 = sat(rne(v / s)).
+  * V: one scale per channel (amax over all tokens), v8 = sat(rne(v / s)),
+    and vsum = sum over the keys of v8 per channel (the GPU's P - 128
+    correction).
 
 attention (checked within a tolerance: the GPU's exp2 is the hardware
 approximation), per query:
     S = q8 . k8 (int32, exact) and c_j = fp32(qs * ks[j]) for key block j;
     m = max over blocks of fp32(max(S_j) * c_j), the largest logit;
-    nm = fp32(fp32(log2(127) - m) - fp32(|m| * 2^-22));
-    P = rne(exp2(fma(S, c_j, nm))), integers 0..127 (the 2^-22 margin keeps
-    the largest exponent within a few ulps of log2(127)), 0 past Nk;
+    nm = fp32(log2(255) - m);
+    P = min(255, rne(exp2(fma(S, c_j, nm)))), integers 0..255, 0 past Nk;
     acc = P . v8 and l = sum(P), exact integers;
     out = fp32(fp32(f32(acc) * vs) / f32(l)).
 """
@@ -47,7 +49,7 @@ from .w8a8_oracle import R127, SCALE_FLOOR, quantize_rows
 
 F32 = np.float32
 LOG2E = F32(1.4426950408889634)
-L127 = F32(np.log2(127.0))
+L255 = F32(np.log2(255.0))
 BLOCK_K = 64
 CHUNK = 256
 
@@ -85,8 +87,8 @@ def key_mean(k):
 
 
 def prepare(q, k, v, sm_scale=None):
-    """INT8 operands of the attention: dict of q8, qs, k8, ks, vt8, vs (and
-    kmean), for q [B, H, Nq, D], k, v [B, H, Nk, D] (any float dtype)."""
+    """INT8 operands of the attention: dict of q8, qs, k8, ks, vt8, vs, vsum
+    (and kmean), for q [B, H, Nq, D], k, v [B, H, Nk, D] (any float dtype)."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     b, h, nq, d = q.shape
     nk = k.shape[2]
@@ -111,7 +113,8 @@ def prepare(q, k, v, sm_scale=None):
         v8[:, :, :nk] = np.clip(np.rint(v / vs[:, :, None, :]), -128, 127).astype(np.int8)
     perm = perm32()
     vt8 = v8.reshape(b, h, nkp // 32, 32, d)[:, :, :, perm, :].reshape(b, h, nkp, d).transpose(0, 1, 3, 2).copy()
-    return dict(q8=q8, qs=qs, k8=k8, ks=ks, vt8=vt8, vs=vs, kmean=mean, v8=v8, nk=nk)
+    vsum = v8.astype(np.int64).sum(2).astype(np.int32)     # per channel, exact (|sum| < 2^31)
+    return dict(q8=q8, qs=qs, k8=k8, ks=ks, vt8=vt8, vs=vs, vsum=vsum, kmean=mean, v8=v8, nk=nk)
 
 
 def attention(prep, out_dtype='f32'):
@@ -136,10 +139,10 @@ def attention(prep, out_dtype='f32'):
             with np.errstate(over='ignore', invalid='ignore'):
                 mj = np.where(mblk > np.iinfo(np.int64).min, (mblk.astype(F32) * c).astype(F32), -np.inf)
                 m = mj.max(1).astype(F32)
-                nm = ((L127 - m).astype(F32) - (np.abs(m) * F32(2.0 ** -22)).astype(F32)).astype(F32)
+                nm = (L255 - m).astype(F32)
                 e = (s.astype(np.float64) * cfull.astype(np.float64) + nm[:, None]).astype(F32)
                 p = np.exp2(e).astype(F32)
-            pi = np.where(valid[None, :], np.rint(p), 0).astype(np.int64)
+            pi = np.where(valid[None, :], np.minimum(np.rint(p), 255), 0).astype(np.int64)
             acc = pi @ v8[bi, hi]
             l = pi.sum(1).astype(F32)
             out[bi, hi] = ((acc.astype(F32) * vs[bi, hi][None, :]).astype(F32) / l[:, None]).astype(F32)

@@ -96,7 +96,7 @@ def fixtures():
     ka = (rng.standard_normal((1, 2, 70, 128)) + 0.5).astype(np.float16)
     va = rng.standard_normal((1, 2, 70, 128)).astype(np.float16)
     prep = oa.prepare(qa.astype(np.float32), ka.astype(np.float32), va.astype(np.float32))
-    out['attention'] = dict(q=qa, k=ka, v=va, **{n: prep[n] for n in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs')},
+    out['attention'] = dict(q=qa, k=ka, v=va, **{n: prep[n] for n in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum')},
                             out=oa.attention(prep, out_dtype='f32'))
     return out
 

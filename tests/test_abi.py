@@ -35,7 +35,7 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [96, 96, 192, 144, 144, 104, 216, 136]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [96, 96, 192, 144, 144, 104, 224, 144]
     assert ctypes.sizeof(_abi.RopeEpilogue) == 48   # static_assert'ed in the library too
 
 
@@ -121,7 +121,7 @@ def test_attention_argument_checks():
     assert lib.w8a8_attention_workspace_size(0, 2, 300) == 0
     base = dict(struct_size=ctypes.sizeof(_abi.AttnPrepareArgs), in_dtype=_abi.F16, q=4096, k=8192, v=12288, b=1,
                 h=2, nq=100, nk=300, d=128, sm_scale=0.088, q8=16384, qs=20480, k8=24576, ks=28672, vt8=32768,
-                vs=36864, workspace=40960, workspace_bytes=1 << 20, q_strides=(0, 12800, 128),
+                vs=36864, vsum=38912, workspace=40960, workspace_bytes=1 << 20, q_strides=(0, 12800, 128),
                 k_strides=(0, 38400, 128), v_strides=(0, 38400, 128))
     _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'd': 64}), 'head dimension')
     _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'in_dtype': _abi.BF16}), 'in_dtype')
@@ -134,7 +134,7 @@ def test_attention_argument_checks():
     _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'q_strides': (0, -128, 128)}),
                     'multiples of 16 bytes')
     att = dict(struct_size=ctypes.sizeof(_abi.AttentionArgs), out_dtype=_abi.F16, q8=4096, qs=8192, k8=12288,
-               ks=16384, vt8=20480, vs=24576, b=1, h=2, nq=100, nk=300, d=128, out=28672,
+               ks=16384, vt8=20480, vs=24576, vsum=26624, b=1, h=2, nq=100, nk=300, d=128, out=28672,
                out_strides=(0, 128, 256))
     _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out_dtype': _abi.I32}), 'out_dtype')
     _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out': None}), 'null')

@@ -78,7 +78,7 @@ def test_kernels_reproduce_golden_fixtures_of_the_dit_rows(gpu):
     assert_bits_equal(np_of(k), d['k'], 'golden rms_rope k')
     d = load('attention')
     prep = kernels.attention_prepare(t(d['q']), t(d['k']), t(d['v']))
-    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs'):
+    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum'):
         assert_bits_equal(np_of(prep[name]), d[name], f'golden attention {name}')
     out = np_of(kernels.attention(prep, out_dtype=torch.float32)).astype(np.float64)
     # the GPU takes the hardware exp2: within 2e-3 of the oracle's output

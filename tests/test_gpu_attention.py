@@ -45,7 +45,7 @@ def test_prepare_matches_oracle(gpu, b, h, nq, nk, dtype):
     q, k, v = _qkv(g, b, h, nq, nk, dtype)
     prep = kernels.attention_prepare(q.to(gpu), k.to(gpu), v.to(gpu))
     want = oa.prepare(_np(q), _np(k), _np(v))
-    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs'):
+    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum'):
         got = np_of(prep[name])
         assert got.shape == want[name].shape, name
         if got.dtype == np.float32:
@@ -133,7 +133,7 @@ def test_strided_operands_and_output(gpu, b, h, n, dtype):
     assert kernels._row_strides(q) is not None and not q.is_contiguous()
     prep = kernels.attention_prepare(q, k, v)
     flat = kernels.attention_prepare(q.contiguous(), k.contiguous(), v.contiguous())
-    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs'):
+    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum'):
         assert torch.equal(prep[name], flat[name]), name
     for out_dtype in (torch.float16, torch.float32):
         want = kernels.attention(flat, out_dtype=out_dtype)

@@ -68,7 +68,7 @@ def test_dit_attention_sublayer(gpu, rows, hidden, heads, rot):
     heads_first = [np.ascontiguousarray(t.astype(np.float32).transpose(1, 0, 2))[None] for t in (qo, ko, vo)]
     oprep = oa.prepare(*heads_first)
     prep = kernels.attention_prepare(q.transpose(0, 1)[None], k.transpose(0, 1)[None], v.transpose(0, 1)[None])
-    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs'):
+    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum'):
         got = np_of(prep[name])
         if got.dtype == np.float32:
             assert np.array_equal(got.view(np.uint32), oprep[name].view(np.uint32)), name

@@ -549,7 +549,7 @@ def test_attention_oracle_against_closed_forms():
     exact = oa.reference_attention(q, k, v)
     cos = (out * exact).sum() / np.sqrt((out * out).sum() * (exact * exact).sum())
     assert cos > 0.999
-    # identical keys: every probability is 127, the output is the mean of the quantized values
+    # identical keys: every probability is 255, the output is the mean of the quantized values
     ku = np.repeat(rng.standard_normal((1, 1, 1, 128)).astype(np.float32), 100, axis=2)
     pr = oa.prepare(q[:, :1], ku, v[:, :1, :100])
     mean_v = (pr['v8'][:, :, :100].astype(np.float64) * pr['vs'][:, :, None, :]).mean(2)
@@ -676,7 +676,8 @@ def test_kitchen_restatement_and_this_scheme_against_exact():
     scheme against the reference restatement (the error the build carries)."""
     from oracle import int8_attention as oa
     rng = np.random.default_rng(29)
-    for nq, nk, ref_tol, ours_tol in ((64, 64, 0.02, 0.02), (64, 1000, 0.03, 0.07), (32, 4000, 0.03, 0.10)):
+    # ours: u8 probabilities against the row maximum (7-bit ones measured 0.062 / 0.041 at 1000 / 4000 keys)
+    for nq, nk, ref_tol, ours_tol in ((64, 64, 0.02, 0.03), (64, 1000, 0.03, 0.04), (32, 4000, 0.03, 0.04)):
         q, k, v = _qkv_np(rng, nq, nk)
         exact = oa.reference_attention(q, k, v)
         ref = oa.kitchen_attention(oa.kitchen_prepare(q, k, v))
