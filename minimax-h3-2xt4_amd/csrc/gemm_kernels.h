@@ -247,8 +247,8 @@ __device__ __forceinline__ int readout_col(int nw, int h, int lane) {
 // so the passes need only compiler ordering between the slice writes and
 // reads, and the next pass's writes may issue before this pass's reads
 // return.
-template <int EPI, int OUT, int FLAGS, bool INTERIOR>
-__device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[4][4],
+template <int EPI, int OUT, int FLAGS, bool INTERIOR, int NB = 4>
+__device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16i (&acc)[NB][4],
                                                         const float (&wsc)[2][8], const float (&bsc)[2][8],
                                                         const float (&as)[4], const int (&lbl)[4], int mw, int nw,
                                                         int lane, int8_t* stage, int64_t out_off) {
@@ -264,6 +264,9 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     const int mb = pass >> 1, h = pass & 1;
     const int mrow = mw + mb * 32;
     const int ncol = nw + 64 * h + ocol;
+    // A quadrant 96 columns wide (NB == 3) has only its first 32 in the
+    // second half: the other read-out lanes of those passes store nothing.
+    const bool in_quad = NB == 4 || h == 0 || ocol < 32;
     // INTERIOR: every row and column of the quadrant is inside the output
     // and rows are 16-byte aligned, so no store needs a mask.
     const bool full_cols = INTERIOR || (p.vec16 && ncol + R::CPL <= p.n);
@@ -273,7 +276,9 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       for (int it = 0; it < R::ITERS; ++it) {
         const int m = mrow + it * R::RPI + orow;
         const uint16_t* r = p.residual + (int64_t)m * p.ldr + ncol;
-        if (INTERIOR || (m < p.m && full_cols)) {
+        if (!in_quad) {
+          rres[it] = make_uint4(0, 0, 0, 0);
+        } else if (INTERIOR || (m < p.m && full_cols)) {
           rres[it] = *reinterpret_cast<const uint4*>(r);
         } else {
           uint32_t w[4] = {0, 0, 0, 0};
@@ -294,7 +299,10 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       for (int it = 0; it < R::ITERS; ++it) {
         const int row = it * R::RPI + orow;
         const float* gr = p.gate + (int64_t)__shfl(lbl[mb], row, 64) * p.ldg;
-        if (p.gvec && full_cols) {
+        if (!in_quad) {
+#pragma unroll
+          for (int j = 0; j < R::CPL; ++j) gv[it][j] = 0.0f;
+        } else if (p.gvec && full_cols) {
 #pragma unroll
           for (int q = 0; q < R::CPL / 4; ++q) {
             const float4 g4 = *reinterpret_cast<const float4*>(gr + ncol + 4 * q);
@@ -311,10 +319,12 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     for (int nbl = 0; nbl < 2; ++nbl)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int nb = 2 * h + nbl;
-        const int chunk = nbl * 8 + 2 * g + fh;
-        *reinterpret_cast<v4i*>(stage + fr * RB + ((chunk ^ (fr & 15)) << 4)) =
-            v4i{acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2], acc[nb][mb][4 * g + 3]};
+        const int nb = min(2 * h + nbl, NB - 1);
+        if (NB == 4 || 2 * h + nbl < NB) {
+          const int chunk = nbl * 8 + 2 * g + fh;
+          *reinterpret_cast<v4i*>(stage + fr * RB + ((chunk ^ (fr & 15)) << 4)) =
+              v4i{acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2], acc[nb][mb][4 * g + 3]};
+        }
       }
     asm volatile("" ::: "memory");
     // Row scales of the lane's read-out rows (from the lanes holding them in
@@ -378,7 +388,8 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
         }
       }
       char* o = reinterpret_cast<char*>(p.out) + (out_off + (int64_t)m * p.ldc + ncol) * R::ES;
-      if (INTERIOR || (m < p.m && full_cols)) {
+      if (!in_quad) {
+      } else if (INTERIOR || (m < p.m && full_cols)) {
         *reinterpret_cast<uint4*>(o) = make_uint4(words[0], words[1], words[2], words[3]);
       } else if (!INTERIOR && m < p.m) {
 #pragma unroll
@@ -779,13 +790,27 @@ __device__ __forceinline__ void block_barrier() {
 
 __device__ __forceinline__ int lds_chunk(int row, int c) { return c ^ ((row >> 1) & 7); }
 
-template <int EPI, int OUT, int FLAGS>
+// f(integral_constant<int, I>) for I = LO .. HI - 1.
+template <int LO, int HI, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (LO < HI) {
+    f(std::integral_constant<int, LO>{});
+    static_for<LO + 1, HI>(f);
+  }
+}
+
+template <int EPI, int OUT, int FLAGS, int NB>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_i8_persistent(GemmParams p) {
+  // NB MFMA column blocks per wave: tiles are 256 x 64 NB (256 or 192
+  // columns), a wave's quadrant 128 x 32 NB, and a B unit 2 NB DMA
+  // instructions per wave (8 rows each).
+  static_assert(NB == 4 || (NB == 3 && (FLAGS & kWithRope) == 0), "NB 4, or 3 without the RoPE epilogue");
+  constexpr int BN = 64 * NB, WN = 32 * NB, JB = 2 * NB;
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tiles_m = (p.m + kBM - 1) / kBM, tiles_n = (p.n + kBN - 1) / kBN;
+  const int tiles_m = (p.m + kBM - 1) / kBM, tiles_n = (p.n + BN - 1) / BN;
   // Tile schedule. Workgroup w runs on XCD w % 8 (round-robin dispatch).
   // With a grid that is a multiple of 8, XCD x owns the contiguous raster
   // range [x*T/8, (x+1)*T/8) and its G/8 workgroups walk it in lockstep, so
@@ -808,28 +833,33 @@ void gemm_i8_persistent(GemmParams p) {
   auto ks_end = [&](int item) { return (item % ksplit + 1) * kstages / ksplit; };
 
   // DMA cursor: the (tile, stage) of the next stage to issue. Wave w fills
-  // rows 64 w .. 64 w + 63 of both operand tiles, 8 rows per instruction;
-  // offsets are 32-bit (the host checks that the operands span < 4 GB).
-  uint32_t off_a[8], off_b[8];
+  // rows 64 w .. 64 w + 63 of the A tile and 8 JB w .. 8 JB (w + 1) - 1 of
+  // the B tile, 8 rows per instruction; offsets are 32-bit (the host checks
+  // that the operands span < 4 GB).
+  uint32_t off_a[8], off_b[JB];
   auto point = [&](int i) {
     int tm, tn;
     raster(item_of(i) / ksplit, tiles_m, tiles_n, tm, tn);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int row = (wave * 8 + j) * 8 + (lane >> 3);
-      const int chunk = lds_chunk(row, lane & 7);
-      off_a[j] = (uint32_t)((int64_t)min(tm * kBM + row, p.m - 1) * p.lda + chunk * 16);
-      off_b[j] = (uint32_t)((int64_t)min(tn * kBN + row, p.n - 1) * p.ldb + chunk * 16);
+      off_a[j] = (uint32_t)((int64_t)min(tm * kBM + row, p.m - 1) * p.lda + lds_chunk(row, lane & 7) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < JB; ++j) {
+      const int row = (wave * JB + j) * 8 + (lane >> 3);
+      off_b[j] = (uint32_t)((int64_t)min(tn * BN + row, p.n - 1) * p.ldb + lds_chunk(row, lane & 7) * 16);
     }
   };
   int dma_i = 0, dma_ks = ks_begin(item_of(0)), dma_end = ks_end(item_of(0));
   point(0);
   // The ring: unit h (the A tile of global stage h / 2 for even h, its B
-  // tile for odd h) goes to slot h % kSlots. A unit is 8 DMA instructions
-  // per wave, issued in halves of 4 spread between MFMAs (a burst of them
-  // would stall the issuing wave behind the address unit). The cursor
-  // advances after a B tile's second half; past the last stage of the last
-  // tile it stays put and re-reads that stage into slots never consumed.
+  // tile for odd h) goes to slot h % kSlots. A unit is 8 (A) or JB (B) DMA
+  // instructions per wave, issued in halves spread between MFMAs (a burst
+  // of them would stall the issuing wave behind the address unit). The
+  // cursor advances after a B tile's second half; past the last stage of
+  // the last tile it stays put and re-reads that stage into slots never
+  // consumed.
   // dma_end (the cursor item's last stage + 1) is recomputed only when the
   // cursor moves to the next item, keeping its divisions out of the stages.
   auto advance = [&]() {
@@ -843,23 +873,29 @@ void gemm_i8_persistent(GemmParams p) {
       point(dma_i);
     }
   };
-  // DMA instruction J (0..7) of this wave's part of the cursor stage's A or
-  // B tile into slot.
+  // DMA instruction J (0..7 of A, 0..JB - 1 of B) of this wave's part of
+  // the cursor stage's A or B tile into slot.
   auto dma_one = [&](auto b_tag, auto j_tag, int slot) {
     constexpr bool B = decltype(b_tag)::value;
     constexpr int J = decltype(j_tag)::value;
-    int8_t* st = smem + slot * kSTile + wave * 8 * 1024 + J * 1024;
+    int8_t* st = smem + slot * kSTile + wave * (B ? JB : 8) * 1024 + J * 1024;
     const uint32_t kof = (uint32_t)(dma_ks * kSK);
     if constexpr (B) dma16(p.b + (off_b[J] + kof), st);
     else dma16(p.a + (off_a[J] + kof), st);
-    if constexpr (B && J == 7) advance();
+    if constexpr (B && J == JB - 1) advance();
+  };
+  // Part R (of NB, one per MFMA row) of half H of a unit: instructions
+  // [C H + R C / NB, C H + (R + 1) C / NB) with C the half's length.
+  auto dma_part = [&](auto b_tag, auto h_tag, auto r_tag, int slot) {
+    constexpr bool B = decltype(b_tag)::value;
+    constexpr int H = decltype(h_tag)::value, R = decltype(r_tag)::value;
+    constexpr int C = B ? JB / 2 : 4;
+    static_for<C * H + R * C / NB, C * H + (R + 1) * C / NB>([&](auto j) { dma_one(b_tag, j, slot); });
   };
   auto issue_half = [&](auto b_tag, auto h_tag, int slot) {
-    constexpr int H = decltype(h_tag)::value;
-    dma_one(b_tag, std::integral_constant<int, 4 * H>{}, slot);
-    dma_one(b_tag, std::integral_constant<int, 4 * H + 1>{}, slot);
-    dma_one(b_tag, std::integral_constant<int, 4 * H + 2>{}, slot);
-    dma_one(b_tag, std::integral_constant<int, 4 * H + 3>{}, slot);
+    constexpr bool B = decltype(b_tag)::value;
+    constexpr int H = decltype(h_tag)::value, C = B ? JB / 2 : 4;
+    static_for<C * H, C * H + C>([&](auto j) { dma_one(b_tag, j, slot); });
   };
   using A_ = std::false_type;
   using B_ = std::true_type;
@@ -872,81 +908,49 @@ void gemm_i8_persistent(GemmParams p) {
   // accumulator tiles (its 128x128 quadrant).
   const int wm = wave >> 1, wn = wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
-  const int a_row = wm * 128 * kSK + fr * kSK, b_row = wn * 128 * kSK + fr * kSK;
-  auto read_frags = [&](int slot_a, int slot_b, int u, v4i (&fa)[4], v4i (&fb)[4]) {
+  const int a_row = wm * 128 * kSK + fr * kSK, b_row = wn * WN * kSK + fr * kSK;
+  auto read_frags = [&](int slot_a, int slot_b, int u, v4i (&fa)[NB], v4i (&fb)[4]) {
     const int8_t* sa = smem + slot_a * kSTile;
     const int8_t* sb = smem + slot_b * kSTile;
     const int off = lds_chunk(fr, 2 * u + fh) << 4;   // rows 32 i + fr share (row >> 1) & 7
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      fa[i] = *reinterpret_cast<const v4i*>(sb + b_row + i * 32 * kSK + off);
-      fb[i] = *reinterpret_cast<const v4i*>(sa + a_row + i * 32 * kSK + off);
-    }
+    for (int i = 0; i < NB; ++i) fa[i] = *reinterpret_cast<const v4i*>(sb + b_row + i * 32 * kSK + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fb[i] = *reinterpret_cast<const v4i*>(sa + a_row + i * 32 * kSK + off);
   };
-  // Group k (0..2) of the fragment reads of sub-step u, in the order the
-  // next sub-step's first MFMA row consumes them (all four A fragments fb,
-  // then the B fragments fa): k = 0 reads fb[0..2], k = 1 fb[3], fa[0..1],
-  // k = 2 fa[2..3]. The last MFMA row of a sub-step issues no reads, so the
-  // reads have landed when the next sub-step starts.
-  auto read_group = [&](int slot_a, int slot_b, int u, int k, v4i (&fa)[4], v4i (&fb)[4]) {
+  // Group k (0 .. NB - 2) of the fragment reads of sub-step u, in the order
+  // the next sub-step's first MFMA row consumes them (all four A fragments
+  // fb, then the B fragments fa). NB = 4: k = 0 reads fb[0..2], k = 1
+  // fb[3], fa[0..1], k = 2 fa[2..3]; NB = 3: k = 0 fb[0..3], k = 1
+  // fa[0..2]. The last MFMA row of a sub-step issues no reads, so the reads
+  // have landed when the next sub-step starts.
+  auto read_group = [&](int slot_a, int slot_b, int u, int k, v4i (&fa)[NB], v4i (&fb)[4]) {
     const int off = lds_chunk(fr, 2 * u + fh) << 4;
     const int8_t* sa = smem + slot_a * kSTile + a_row + off;
     const int8_t* sb = smem + slot_b * kSTile + b_row + off;
     auto rd = [](const int8_t* base, int i) { return *reinterpret_cast<const v4i*>(base + i * 32 * kSK); };
-    if (k == 0) {
-      fb[0] = rd(sa, 0); fb[1] = rd(sa, 1); fb[2] = rd(sa, 2);
-    } else if (k == 1) {
-      fb[3] = rd(sa, 3); fa[0] = rd(sb, 0); fa[1] = rd(sb, 1);
+    if constexpr (NB == 4) {
+      if (k == 0) {
+        fb[0] = rd(sa, 0); fb[1] = rd(sa, 1); fb[2] = rd(sa, 2);
+      } else if (k == 1) {
+        fb[3] = rd(sa, 3); fa[0] = rd(sb, 0); fa[1] = rd(sb, 1);
+      } else {
+        fa[2] = rd(sb, 2); fa[3] = rd(sb, 3);
+      }
     } else {
-      fa[2] = rd(sb, 2); fa[3] = rd(sb, 3);
+      if (k == 0) {
+        fb[0] = rd(sa, 0); fb[1] = rd(sa, 1); fb[2] = rd(sa, 2); fb[3] = rd(sa, 3);
+      } else {
+        fa[0] = rd(sb, 0); fa[1] = rd(sb, 1); fa[2] = rd(sb, 2);
+      }
     }
   };
-  v16i acc[4][4];
-  auto mfma16 = [&](const v4i (&fa)[4], const v4i (&fb)[4]) {
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[nb], fb[mb], acc[nb][mb], 0, 0, 0);
-  };
-  // Block row nb of the 4x4 MFMA grid (4 MFMAs).
-  auto mfma_row = [&](int nb, const v4i (&fa)[4], const v4i (&fb)[4]) {
+  v16i acc[NB][4];
+  // Block row nb of the NB x 4 MFMA grid (4 MFMAs).
+  auto mfma_row = [&](int nb, const v4i (&fa)[NB], const v4i (&fb)[4]) {
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
       acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[nb], fb[mb], acc[nb][mb], 0, 0, 0);
-  };
-  // 16 MFMAs with 8 fragment reads spread between them.
-  auto interleave = [&]() {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-  };
-  // 12 MFMAs with 8 fragment reads.
-  auto interleave12 = [&]() {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-    }
-  };
-  // The same with 4 DMA instructions between them.
-  auto interleave_dma = [&]() {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
-  };
-  auto interleave12_dma = [&]() {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-    }
   };
 
   // Stage g computes from units 2g, 2g + 1 (slots c, c + 1 with
@@ -960,9 +964,9 @@ void gemm_i8_persistent(GemmParams p) {
   issue_half(A_{}, H0{}, 2);
   issue_half(A_{}, H1{}, 2);
   issue_half(B_{}, H0{}, 3);
-  wait_vmcnt<12>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
+  wait_vmcnt<8 + JB / 2>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
   block_barrier();
-  v4i fa0[4], fb0[4], fa1[4], fb1[4];
+  v4i fa0[NB], fb0[4], fa1[NB], fb1[4];
   read_frags(0, 1, 0, fa0, fb0);
   auto next_slot = [](int slot) { return slot == kSlots - 1 ? 0 : slot + 1; };
   int cur_a = 0;   // slot of the current stage's A tile; its B tile is the next slot
@@ -970,7 +974,7 @@ void gemm_i8_persistent(GemmParams p) {
     const int item = item_of(i);
     int tm, tn;
     raster(item / ksplit, tiles_m, tiles_n, tm, tn);
-    const int mw = tm * kBM + wm * 128, nw = tn * kBN + wn * 128;
+    const int mw = tm * kBM + wm * 128, nw = tn * BN + wn * WN;
     // Row scales in the MFMA layout, the column scales (and biases) of the
     // staged read-out and the gate labels, fetched before the K loop so the
     // epilogue never waits on them.
@@ -993,37 +997,31 @@ void gemm_i8_persistent(GemmParams p) {
       load_readout_scales<EPI, OUT, (FLAGS & kWithBias) != 0>(p, nw, lane, wsc, braw);
     }
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < NB; ++a)
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
     const int nks = ks_end(item) - ks_begin(item);   // >= 1
-    // One stage: 64 MFMAs, 32 fragment reads and 16 DMA instructions.
+    // One stage: 16 NB MFMAs, 4 (NB + 4) fragment reads and 8 + JB DMA
+    // instructions.
     int stg = 0;   // the last stage's B slot: the epilogue's staging area
     int ks = 0;
-    // A sub-step in fixed order: each MFMA row of the current fragments is
-    // followed by one fragment pair of the next sub-step and one DMA
-    // instruction (sched_barrier keeps the compiler from regrouping them).
-    auto substep = [&](const v4i (&ca)[4], const v4i (&cb)[4], int ra, int rb, int u, v4i (&na)[4],
+    // A sub-step in fixed order: each MFMA row of the current fragments but
+    // the last is followed by one group of the next sub-step's fragment
+    // reads, and every row by its part of the half-unit of DMA
+    // (sched_barrier keeps the compiler from regrouping them).
+    auto substep = [&](const v4i (&ca)[NB], const v4i (&cb)[4], int ra, int rb, int u, v4i (&na)[NB],
                        v4i (&nb)[4], auto b_tag, auto h_tag, int dslot) {
-      constexpr int H = decltype(h_tag)::value;
-      mfma_row(0, ca, cb);
-      __builtin_amdgcn_sched_barrier(0);
-      read_group(ra, rb, u, 0, na, nb);
-      dma_one(b_tag, std::integral_constant<int, 4 * H>{}, dslot);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_row(1, ca, cb);
-      __builtin_amdgcn_sched_barrier(0);
-      read_group(ra, rb, u, 1, na, nb);
-      dma_one(b_tag, std::integral_constant<int, 4 * H + 1>{}, dslot);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_row(2, ca, cb);
-      __builtin_amdgcn_sched_barrier(0);
-      read_group(ra, rb, u, 2, na, nb);
-      dma_one(b_tag, std::integral_constant<int, 4 * H + 2>{}, dslot);
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_row(3, ca, cb);
-      dma_one(b_tag, std::integral_constant<int, 4 * H + 3>{}, dslot);
-      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NB>([&](auto r_tag) {
+        constexpr int R = decltype(r_tag)::value;
+        mfma_row(R, ca, cb);
+        // (The last row's DMA may rise among its MFMAs.)
+        if constexpr (R + 1 < NB) {
+          __builtin_amdgcn_sched_barrier(0);
+          read_group(ra, rb, u, R, na, nb);
+        }
+        dma_part(b_tag, h_tag, r_tag, dslot);
+        __builtin_amdgcn_sched_barrier(0);
+      });
     };
     do {  // nks >= 1
       // At a tile's last stage the next tile's first fragments are read
@@ -1043,27 +1041,25 @@ void gemm_i8_persistent(GemmParams p) {
       // this stage returned;
       wait_vm_lgkm<8>();
       block_barrier();   // ... for every wave: both slots are released.
-      if (!last) read_group(nxt_a, nxt_b, 0, 0, fa0, fb0);
-      dma_one(B_{}, std::integral_constant<int, 0>{}, cur_a);
-      mfma_row(1, fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      if (!last) read_group(nxt_a, nxt_b, 0, 1, fa0, fb0);
-      dma_one(B_{}, std::integral_constant<int, 1>{}, cur_a);
-      mfma_row(2, fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      if (!last) read_group(nxt_a, nxt_b, 0, 2, fa0, fb0);
-      dma_one(B_{}, std::integral_constant<int, 2>{}, cur_a);
-      mfma_row(3, fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      dma_one(B_{}, std::integral_constant<int, 3>{}, cur_a);
-      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NB>([&](auto r_tag) {
+        constexpr int R = decltype(r_tag)::value;
+        if constexpr (R > 0) {
+          mfma_row(R, fa1, fb1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (R + 1 < NB) {
+          if (!last) read_group(nxt_a, nxt_b, 0, R, fa0, fb0);
+        }
+        dma_part(B_{}, H0{}, r_tag, cur_a);
+        __builtin_amdgcn_sched_barrier(0);
+      });
       stg = cur_b;
       cur_a = nxt_a;
     } while (++ks < nks);
     // The tile's scale and bias loads have landed: at most unit 2g + 4 and
     // the first half of unit 2g + 5 are younger and in flight. (The
-    // epilogue's residual loads queue behind those 12 instructions.)
-    wait_vmcnt<12>();
+    // epilogue's residual loads queue behind those 8 + JB / 2 instructions.)
+    wait_vmcnt<8 + JB / 2>();
     float bsc[2][8];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -1090,20 +1086,19 @@ void gemm_i8_persistent(GemmParams p) {
       } else {
         store_quadrant_rope<EPI, kF16, false>(p, acc, wsc, as, mw, nw, lane, stage_w);
       }
-    } else if ((FLAGS & kWithGate) == 0 && p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
-      store_quadrant32_passes<EPI, OUT, FLAGS, (FLAGS & kWithGate) == 0>(p, acc, wsc, bsc, as, lbl, mw, nw, lane,
-                                                                        stage_w, out_off);
+    } else if ((FLAGS & kWithGate) == 0 && p.vec16 && mw + 128 <= p.m && nw + WN <= p.n)
+      store_quadrant32_passes<EPI, OUT, FLAGS, (FLAGS & kWithGate) == 0, NB>(p, acc, wsc, bsc, as, lbl, mw, nw,
+                                                                            lane, stage_w, out_off);
     else
-      store_quadrant32_passes<EPI, OUT, FLAGS, false>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
+      store_quadrant32_passes<EPI, OUT, FLAGS, false, NB>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w,
+                                                          out_off);
     // The staging slot's next unit (2g + 6) is issued during the next
     // stage; a wave's DMA into a slot writes the same 8 KB it used for
     // staging, so its own staging reads returning is all that unit waits for.
     wait_lgkm();
     // The next tile's first fragments (its stage 0 landed before the last
     // barrier, in the slots cur_a and the one after).
-    read_group(cur_a, next_slot(cur_a), 0, 0, fa0, fb0);
-    read_group(cur_a, next_slot(cur_a), 0, 1, fa0, fb0);
-    read_group(cur_a, next_slot(cur_a), 0, 2, fa0, fb0);
+    static_for<0, NB - 1>([&](auto k) { read_group(cur_a, next_slot(cur_a), 0, decltype(k)::value, fa0, fb0); });
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }
@@ -1434,14 +1429,14 @@ inline int current_device(int& dev) {
   return W8A8_OK;
 }
 
-template <int EPI, int OUT, int FLAGS>
+template <int EPI, int OUT, int FLAGS, int NB>
 int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s) {
   // The LDS ring and staging area exceed the 64 KB default: raise the
   // kernel's dynamic LDS limit once per device.
   static DeviceOnce lds_enabled;
   const uint64_t bit = 1ull << dev;
   if (!(lds_enabled.done.load(std::memory_order_acquire) & bit)) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_persistent<EPI, OUT, FLAGS>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_persistent<EPI, OUT, FLAGS, NB>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, kPersistentLds);
     if (e != hipSuccess) {
       set_error("w8a8_gemm: cannot enable %d bytes of LDS: %s", kPersistentLds, hipGetErrorString(e));
@@ -1450,12 +1445,25 @@ int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s
     lds_enabled.done.fetch_or(bit, std::memory_order_acq_rel);
   }
   // One workgroup per CU (the ring takes the whole LDS); a multiple of 8 so
-  // every XCD holds the same number of them.
+  // every XCD holds the same number of them, unless that would take one
+  // more round of work items (150 items on 144 workgroups).
   const int64_t items = tiles * (p.ksplit > 1 ? p.ksplit : 1);
   int64_t grid = items < device_cus(dev) ? items : device_cus(dev);
-  if (grid >= 8) grid &= ~7ll;
-  hipLaunchKernelGGL((gemm_i8_persistent<EPI, OUT, FLAGS>), dim3((unsigned)grid), dim3(256), kPersistentLds, s, p);
+  const int64_t grid8 = grid & ~7ll;
+  if (grid8 >= 8 && (items + grid8 - 1) / grid8 == (items + grid - 1) / grid) grid = grid8;
+  hipLaunchKernelGGL((gemm_i8_persistent<EPI, OUT, FLAGS, NB>), dim3((unsigned)grid), dim3(256), kPersistentLds, s,
+                     p);
   return W8A8_OK;
+}
+
+// The persistent kernel with 256 x 64 nb tiles.
+template <int EPI, int OUT, int FLAGS>
+int launch_persistent_nb(const GemmParams& p, const GemmPlan& plan, int dev, hipStream_t s) {
+  const int64_t tiles = plan_tiles(p.m, p.n, plan);
+  if constexpr ((FLAGS & kWithRope) == 0) {
+    if (plan.nb == 3) return launch_persistent<EPI, OUT, FLAGS, 3>(p, tiles, dev, s);
+  }
+  return launch_persistent<EPI, OUT, FLAGS, 4>(p, tiles, dev, s);
 }
 
 template <int EPI, int OUT, int MB>
@@ -1509,21 +1517,25 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     else launch_skinny<EPI, OUT, 4>(p, s);
     return W8A8_OK;
   }
-  const int64_t tiles = (int64_t)((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
   // The persistent kernel streams whole K = 128 stages and addresses the
   // operands with 32-bit offsets; anything else takes the register-staged
   // kernel.
   const bool offsets32 = (int64_t)(p.m - 1) * p.lda + p.k < (1ll << 32) && (int64_t)(p.n - 1) * p.ldb + p.k < (1ll << 32);
   if (p.k % kSK != 0 || !offsets32) {
+    const int64_t tiles = (int64_t)((p.m + kBM - 1) / kBM) * ((p.n + kBN - 1) / kBN);
     hipLaunchKernelGGL((gemm_i8_256x256<EPI, OUT>), dim3((unsigned)tiles), dim3(256), 0, s, p);
     return W8A8_OK;
   }
   int dev = 0;
   int rc = current_device(dev);
   if (rc != W8A8_OK) return rc;
-  int64_t ws_need = 0;
-  const int ksplit = p.ws && !p.rope_heads ? gemm_ksplit(p.m, p.n, p.k, dev, &ws_need) : 1;
-  if (ksplit > 1 && p.ws_bytes >= ws_need) {
+  // Tile width and K split (the RoPE epilogue takes neither: one head per
+  // 128-column quadrant, whole K).
+  GemmPlan plan = p.rope_heads ? GemmPlan{4, 1} : gemm_plan(p.m, p.n, p.k, device_cus(dev));
+  const int64_t ws_need = plan.ksplit > 1 ? (int64_t)plan.ksplit * p.m * p.n * 4 : 0;
+  if (plan.ksplit > 1 && (p.ws == nullptr || p.ws_bytes < ws_need)) plan = gemm_plan(p.m, p.n, p.k, device_cus(dev), 1);
+  const int ksplit = plan.ksplit;
+  if (ksplit > 1) {
     GemmParams q = p;
     q.out = p.ws;
     q.ldc = p.n;
@@ -1533,7 +1545,7 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     q.bias_dtype = 0;
     q.ksplit = ksplit;
     q.split_stride = (int64_t)p.m * p.n;
-    rc = launch_gemm_partials(q, dev, s);
+    rc = launch_gemm_partials(q, plan, dev, s);
     if (rc != W8A8_OK) return rc;
     const int64_t threads = (int64_t)p.m * ((p.n + 3) / 4);
     hipLaunchKernelGGL((splitk_reduce_kernel<EPI, OUT>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
@@ -1541,20 +1553,20 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     return W8A8_OK;
   }
   if constexpr (EPI == kEpiInt32) {
-    return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
+    return launch_persistent_nb<EPI, OUT, 0>(p, plan, dev, s);
   } else if constexpr (OUT != kF16) {  // a residual requires FP16 output
-    return p.bias_dtype ? launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s)
-                        : launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
+    return p.bias_dtype ? launch_persistent_nb<EPI, OUT, kWithBias>(p, plan, dev, s)
+                        : launch_persistent_nb<EPI, OUT, 0>(p, plan, dev, s);
   } else {
     // The host admits the RMS-RoPE epilogue only without bias, residual or gate.
-    if (p.rope_heads) return launch_persistent<EPI, OUT, kWithRope>(p, tiles, dev, s);
+    if (p.rope_heads) return launch_persistent_nb<EPI, OUT, kWithRope>(p, plan, dev, s);
     switch ((p.bias_dtype ? kWithBias : 0) | (p.residual ? kWithResidual : 0) | (p.gate ? kWithGate : 0)) {
-      case 0: return launch_persistent<EPI, OUT, 0>(p, tiles, dev, s);
-      case kWithBias: return launch_persistent<EPI, OUT, kWithBias>(p, tiles, dev, s);
-      case kWithResidual: return launch_persistent<EPI, OUT, kWithResidual>(p, tiles, dev, s);
-      case kWithBias | kWithResidual: return launch_persistent<EPI, OUT, kWithBias | kWithResidual>(p, tiles, dev, s);
-      case kWithResidual | kWithGate: return launch_persistent<EPI, OUT, kWithResidual | kWithGate>(p, tiles, dev, s);
-      default: return launch_persistent<EPI, OUT, kWithBias | kWithResidual | kWithGate>(p, tiles, dev, s);
+      case 0: return launch_persistent_nb<EPI, OUT, 0>(p, plan, dev, s);
+      case kWithBias: return launch_persistent_nb<EPI, OUT, kWithBias>(p, plan, dev, s);
+      case kWithResidual: return launch_persistent_nb<EPI, OUT, kWithResidual>(p, plan, dev, s);
+      case kWithBias | kWithResidual: return launch_persistent_nb<EPI, OUT, kWithBias | kWithResidual>(p, plan, dev, s);
+      case kWithResidual | kWithGate: return launch_persistent_nb<EPI, OUT, kWithResidual | kWithGate>(p, plan, dev, s);
+      default: return launch_persistent_nb<EPI, OUT, kWithBias | kWithResidual | kWithGate>(p, plan, dev, s);
     }
   }
 }

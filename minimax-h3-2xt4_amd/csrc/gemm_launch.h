@@ -60,8 +60,48 @@ void launch_dequant(const GemmParams& p, const int32_t* acc, int64_t ldacc, hipS
 // (1: none) and the workspace bytes it needs.
 int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_bytes);
 
+// Tile width and K split of the persistent kernel: 256 x 64 nb output tiles
+// (nb 4: 256 x 256, nb 3: 256 x 192), K split ksplit ways.
+struct GemmPlan {
+  int nb;
+  int ksplit;
+};
+
+inline int64_t plan_tiles(int64_t m, int64_t n, const GemmPlan& plan) {
+  return ((m + 255) / 256) * ((n + 64 * plan.nb - 1) / (64 * plan.nb));
+}
+
+// The plan of least modelled time for an m x n x k GEMM (k a multiple of
+// 128) on cus CUs, with at most max_split K splits. The cost is counted in
+// K = 128 stages of a 256 x 256 tile (about 1 us on the power-limited
+// clock): rounds of work items x (stages per item x the tile's relative
+// cost, 0.85 for 192-wide tiles whose stages take 0.80 of the cycles, + 8
+// for the tile's epilogue and the launch's fill and drain), plus the split
+// partials' write-and-read traffic at about 6.5 TB/s. A plan replaces the
+// one before it only when it is 10% faster (256-wide and unsplit first).
+inline GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k, int cus, int max_split = 8) {
+  const int64_t kst = k / 128;
+  GemmPlan best{4, 1};
+  double best_t = -1.0;
+  for (int nb = 4; nb >= 3; --nb) {
+    const int64_t tiles = plan_tiles(m, n, GemmPlan{nb, 1});
+    const double f = nb == 4 ? 1.0 : 0.85;
+    for (int ks = 1; ks <= max_split; ks *= 2) {
+      if (ks > 1 && (tiles >= cus || kst / ks < 2)) break;
+      const int64_t rounds = (tiles * ks + cus - 1) / cus;
+      double t = (double)rounds * ((double)((kst + ks - 1) / ks) * f + 8.0);
+      if (ks > 1) t += (double)ks * m * n * 8 / 6.5e12 * 1e6;
+      if (best_t < 0.0 || t < 0.9 * best_t) {
+        best = GemmPlan{nb, ks};
+        best_t = t;
+      }
+    }
+  }
+  return best;
+}
+
 // The int32 partial-sum pass of a split-K GEMM (the persistent kernel with
 // the raw int32 epilogue, defined with the int32 instantiation).
-int launch_gemm_partials(const GemmParams& p, int dev, hipStream_t s);
+int launch_gemm_partials(const GemmParams& p, const GemmPlan& plan, int dev, hipStream_t s);
 
 }  // namespace w8a8

@@ -159,6 +159,43 @@ def test_gemm_stream_strided_weight_and_short_k(gpu):
         assert_bits_equal(np_of(kernels.gemm(a.to(gpu), b.to(gpu))), o.int_mm(np_of(a), np_of(b)), f'k={k}')
 
 
+@pytest.mark.parametrize('m,n,k', [(4096, 3072, 3072), (2000, 2900, 3072), (1000, 1000, 2048)])
+def test_gemm_192_wide_tiles(gpu, m, n, k):
+    # Shapes the host plans with 256 x 192 tiles: 16 x 16 = 256 of them fill
+    # the GPU where 256 x 256 leaves 64 CUs idle (4096 x 3072); ragged edges
+    # in M and N (2000 x 2900: last tiles of 208 rows and 20 columns); and K
+    # split four ways over 4 x 6 tiles (1000 x 1000). Every epilogue variant.
+    print(f'192-wide tiles {m}x{n}x{k}', flush=True)
+    g = torch.Generator().manual_seed(m + n + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.01 + 1e-4
+    ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
+    bias = (torch.randn((n,), generator=g) * 0.01).half()
+    res = randn16(g, (m, n), 1 / 512)
+    gate = torch.randn((5, n), generator=g)
+    labels = torch.randint(0, 5, (m,), generator=g, dtype=torch.int32)
+    acc = o.int_mm(np_of(a), np_of(b))
+    ag, bg = a.to(gpu), b.to(gpu)
+    assert_bits_equal(np_of(kernels.gemm(ag, bg)), acc, 'int32')
+    row16 = o.dequantize_row(acc, np_of(rs), np_of(ws), 'f16', np_of(bias))
+    got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       bias=bias.to(gpu), out_dtype=torch.float16)
+    assert_bits_equal(np_of(got), row16, 'row + bias')
+    got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       bias=bias.to(gpu), residual=res.to(gpu), out_dtype=torch.float16)
+    assert_bits_equal(np_of(got), o.residual_add(np_of(res), row16), 'row + bias + residual')
+    got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       out_dtype=torch.float16, residual=res.to(gpu), gate=gate.to(gpu), gate_labels=labels.to(gpu))
+    branch = o.dequantize_row(acc, np_of(rs), np_of(ws), 'f16')
+    assert_bits_equal(np_of(got), o.gated_residual_add(np_of(res), branch, np_of(gate), np_of(labels)), 'gated')
+    for out_dtype in (torch.float32, torch.bfloat16):
+        got = kernels.gemm(ag, bg, epilogue=kernels.EPI_COLUMN, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                           out_dtype=out_dtype)
+        assert_bits_equal(np_of(got), o.dequantize_column(acc, np_of(rs), np_of(ws), tname(out_dtype)),
+                          f'column {out_dtype}')
+
+
 def test_gemm_scalar_weight_scale_and_residual(gpu):
     g = torch.Generator().manual_seed(12)
     m, n, k = 130, 96, 512
