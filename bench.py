@@ -161,6 +161,13 @@ def run_dit_ffn(args, torch, dev):
                                            gate_labels=labels), args.steps, args.warmup)
     kernels_out['fc2_gemm_gated'] = dict(us=tg * 1e3, tops=ops_fc2 / (tg * 1e-3) / 1e12)
     kernels_out['fc2_gemm_gated']['frac'] = kernels_out['fc2_gemm_gated']['tops'] / PEAK_INT8_TOPS
+    # The vendor library on the same FC1 operand bytes, for comparison:
+    # hipBLASLt behind torch._int_mm (int32 out, no epilogue).
+    qa1 = kernels.quantize_rows(h, convrot=True, round_rotated=True)[0]
+    tv = timed(torch, lambda: torch._int_mm(qa1, w1.t()), args.steps, args.warmup)
+    kernels_out['fc1_hipblaslt_int32'] = dict(us=tv * 1e3, tops=ops_fc1 / (tv * 1e-3) / 1e12)
+    kernels_out['fc1_hipblaslt_int32']['frac'] = kernels_out['fc1_hipblaslt_int32']['tops'] / PEAK_INT8_TOPS
+    del qa1
     fc1 = kernels_out['fc1_gemm']
     traffic = traffic_from_profiles('fc1_gemm')
     roofline = dict(bound='mfma', achieved=round(fc1['tops'], 1), peak=PEAK_INT8_TOPS, unit='TOPS',
@@ -355,6 +362,118 @@ def run_copy(args, torch, dev):
     ms = timed(torch, lambda: dst.copy_(src), args.steps, args.warmup)
     return dict(metric='device copy bandwidth (calibration)', value=round(2 * nbytes / (ms * 1e-3) / 1e9, 1),
                 unit='GB/s', bytes_read=nbytes, bytes_written=nbytes, ms=round(ms, 4))
+
+
+def _board_sensors():
+    """sysfs files of the GPU's board power (uW), its cap and the shader clock table."""
+    import glob
+    found = {}
+    for hw in sorted(glob.glob('/sys/class/drm/card*/device/hwmon/hwmon*')):
+        for name in ('power1_input', 'power1_average', 'power1_cap'):
+            path = os.path.join(hw, name)
+            if name not in found and os.path.exists(path):
+                found[name] = path
+    for path in sorted(glob.glob('/sys/class/drm/card*/device/pp_dpm_sclk')):
+        found.setdefault('sclk', path)
+    return found
+
+
+def _read_sensor(path):
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    if path.endswith('pp_dpm_sclk'):   # the active level is marked with '*'
+        for line in text.splitlines():
+            if line.rstrip().endswith('*'):
+                digits = ''.join(c for c in line.split(':', 1)[-1] if c.isdigit())
+                return float(digits) if digits else None
+        return None
+    try:
+        return float(text.strip())
+    except ValueError:
+        return None
+
+
+def run_gemm_power(args, torch, dev):
+    """The FC1 GEMM (16384 x 16384 x 3072, the DiT FFN block's operands)
+    sustained for a few seconds per variant while the board power is
+    sampled: this build's GEMM with the column epilogue (fp16 out) and with
+    int32 output, and the vendor library (hipBLASLt behind torch._int_mm,
+    int32 out, no epilogue) on the same operand bytes, then on uniformly
+    random int8 operands. Shows whether the GEMMs run at the board's power
+    cap and how this kernel compares with the library at equal power."""
+    import threading
+    from w8a8 import kernels, workloads
+    m, hidden, ffn = 16384, 3072, 8192
+    data = workloads.dit_ffn(m=m, hidden=hidden, ffn=ffn)
+    w1, s1 = workloads.quantize_weight(data['w1'], dev)
+    qa, a = kernels.quantize_rows(data['h'].to(dev), convrot=True, round_rotated=True)
+    g = torch.Generator(device=dev).manual_seed(5)
+    ua = torch.randint(-128, 128, qa.shape, dtype=torch.int8, device=dev, generator=g)
+    uw = torch.randint(-128, 128, w1.shape, dtype=torch.int8, device=dev, generator=g)
+    ops = 2.0 * m * 2 * ffn * hidden
+    # Both int32 routes must agree before anything is timed.
+    if not torch.equal(kernels.gemm(qa[:512], w1, epilogue=kernels.EPI_INT32), torch._int_mm(qa[:512], w1.t())):
+        raise RuntimeError('int32 GEMM differs from torch._int_mm')
+    cases = {
+        'fc1_column_fp16': lambda: kernels.gemm(qa, w1, epilogue=kernels.EPI_COLUMN, row_scale=a, col_scale=s1,
+                                                out_dtype=torch.float16),
+        'fc1_int32': lambda: kernels.gemm(qa, w1, epilogue=kernels.EPI_INT32),
+        'hipblaslt_int32': lambda: torch._int_mm(qa, w1.t()),
+        'uniform_fc1_int32': lambda: kernels.gemm(ua, uw, epilogue=kernels.EPI_INT32),
+        'uniform_hipblaslt_int32': lambda: torch._int_mm(ua, uw.t()),
+    }
+    sensors = _board_sensors()
+    samples, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            samples.append((time.perf_counter(), {k: _read_sensor(p) for k, p in sensors.items()}))
+            time.sleep(0.05)
+
+    thread = threading.Thread(target=sample, daemon=True)
+    thread.start()
+    rows = {}
+    try:
+        for name, fn in cases.items():
+            for _ in range(args.warmup):
+                fn()
+            torch.cuda.synchronize()
+            t_begin = time.perf_counter()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            calls = 0
+            start.record()
+            while time.perf_counter() - t_begin < args.seconds:
+                for _ in range(20):
+                    fn()
+                calls += 20
+                torch.cuda.synchronize()
+            end.record()
+            torch.cuda.synchronize()
+            t_end = time.perf_counter()
+            us = start.elapsed_time(end) / calls * 1e3
+            # Sensor means over the run after its first second (steady state).
+            window = [s for t, s in samples if t_begin + 1.0 <= t <= t_end]
+            row = dict(us=round(us, 1), tops=round(ops / us / 1e6, 1), frac=round(ops / us / 1e6 / PEAK_INT8_TOPS, 4),
+                       calls=calls)
+            for key, unit, scale in (('power1_input', 'board_w', 1e-6), ('power1_average', 'board_avg_w', 1e-6),
+                                     ('power1_cap', 'cap_w', 1e-6), ('sclk', 'sclk_mhz', 1.0)):
+                vals = [s[key] for s in window if s.get(key) is not None]
+                if vals:
+                    row[unit] = round(sum(vals) / len(vals) * scale, 1)
+            rows[name] = row
+            time.sleep(1.0)
+    finally:
+        stop.set()
+        thread.join()
+    ours, lib = rows['fc1_column_fp16'], rows['hipblaslt_int32']
+    return dict(metric='FC1 GEMM 16384x16384x3072 sustained: TOPS and board power', value=ours['tops'], unit='TOPS',
+                higher_is_better=True, dtype='int8', seconds_per_case=args.seconds,
+                data='synthetic (the DiT FFN block FC1 operands; uniform int8 for the uniform_* cases)',
+                config=dict(workload='gemm_power', m=m, n=2 * ffn, k=hidden),
+                vs_hipblaslt=round(lib['us'] / ours['us'], 3), cases=rows,
+                sensors={k: v for k, v in sensors.items()})
 
 
 def _cpu_rows_timing(fn, reps=3):
@@ -886,7 +1005,7 @@ def run_reference_shapes(args, torch, dev):
 WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_attention': run_dit_attention, 'dit_attention_block': run_dit_attention_block, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
              'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv, 'dit_qkv_rope': run_dit_qkv_rope,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard,
-             'reference_shapes': run_reference_shapes}
+             'reference_shapes': run_reference_shapes, 'gemm_power': run_gemm_power}
 
 
 def main():
@@ -897,6 +1016,7 @@ def main():
     ap.add_argument('--workload', default='dit_ffn', choices=sorted(WORKLOADS))
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--cpu-rows', type=int, default=4096)
+    ap.add_argument('--seconds', type=float, default=4.0, help='gemm_power: sustained seconds per case')
     args = ap.parse_args()
     if args.gpus != 1:
         print(f'bench.py: this W8A8 path runs on one GPU; --gpus {args.gpus} is not supported '
