@@ -352,29 +352,31 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       // words[i]: output elements 2 i, 2 i + 1 (2-byte outputs) or element i.
       uint32_t words[4];
       if constexpr (OUT == kF16) {
-        // FP16 pairs convert in one packed instruction; with a residual the
-        // rounded branch is widened again, added and rounded per pair.
+        // FP16 pairs convert in packed instructions, the row's eight values
+        // behind one opaque step; with a residual the rounded branch is
+        // widened again, added and rounded the same way.
+        float y[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float y0 = dequant1<EPI>(c[it][2 * i], a, wsc[h][2 * i]);
-          float y1 = dequant1<EPI>(c[it][2 * i + 1], a, wsc[h][2 * i + 1]);
-          if constexpr (has_bias) {
-            y0 = y0 + bsc[h][2 * i];
-            y1 = y1 + bsc[h][2 * i + 1];
-          }
-          words[i] = f2h2_of_f32(y0, y1);
+        for (int j = 0; j < 8; ++j) {
+          y[j] = dequant1<EPI>(c[it][j], a, wsc[h][j]);
+          if constexpr (has_bias) y[j] = y[j] + bsc[h][j];
         }
+        f2h8_of_f32(y, words);
         if constexpr (has_res) {
           const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float r0 = h2f((uint16_t)(rw[i] & 0xffffu)), r1 = h2f((uint16_t)(rw[i] >> 16));
             const float b0 = h2f((uint16_t)(words[i] & 0xffffu)), b1 = h2f((uint16_t)(words[i] >> 16));
-            if constexpr (has_gate)
-              words[i] = f2h2_of_f32(__builtin_fmaf(b0, gv[it][2 * i], r0), __builtin_fmaf(b1, gv[it][2 * i + 1], r1));
-            else
-              words[i] = f2h2_of_f32(r0 + b0, r1 + b1);
+            if constexpr (has_gate) {
+              y[2 * i] = __builtin_fmaf(b0, gv[it][2 * i], r0);
+              y[2 * i + 1] = __builtin_fmaf(b1, gv[it][2 * i + 1], r1);
+            } else {
+              y[2 * i] = r0 + b0;
+              y[2 * i + 1] = r1 + b1;
+            }
           }
+          f2h8_of_f32(y, words);
         }
       } else {
         uint32_t bits[R::CPL];
@@ -390,7 +392,10 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
       char* o = reinterpret_cast<char*>(p.out) + (out_off + (int64_t)m * p.ldc + ncol) * R::ES;
       if (!in_quad) {
       } else if (INTERIOR || (m < p.m && full_cols)) {
-        *reinterpret_cast<uint4*>(o) = make_uint4(words[0], words[1], words[2], words[3]);
+        // Streaming store: the output is not read again by this kernel, so it
+        // should not push the operand lines out of L2.
+        __builtin_nontemporal_store(v4i{(int)words[0], (int)words[1], (int)words[2], (int)words[3]},
+                                    reinterpret_cast<v4i*>(o));
       } else if (!INTERIOR && m < p.m) {
 #pragma unroll
         for (int j = 0; j < R::CPL; ++j) {

@@ -48,6 +48,15 @@ __device__ __forceinline__ uint32_t f2h2_of_f32(float a, float b) {
   __asm__("" : "+v"(b));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{a, b}, v2h));
 }
+// Eight fp32 -> fp16 conversions into four packed words (y[2 i] in the low
+// half of w[i]), each value first existing as a rounded fp32. One opaque
+// step covers all eight, so the compiler may interleave their producers.
+__device__ __forceinline__ void f2h8_of_f32(float (&y)[8], uint32_t (&w)[4]) {
+  __asm__("" : "+v"(y[0]), "+v"(y[1]), "+v"(y[2]), "+v"(y[3]), "+v"(y[4]), "+v"(y[5]), "+v"(y[6]), "+v"(y[7]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{y[2 * i], y[2 * i + 1]}, v2h));
+}
 __device__ __forceinline__ float bf2f(uint16_t b) {
   return __builtin_bit_cast(float, (uint32_t)b << 16);
 }
