@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
     load16<DT>(xrow + ((int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), gv);
     load16<DT>(xrow + (width + (int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), uv);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = swiglu(gv[i], uv[i]);
+    for (int i = 0; i < 16; ++i) v[i] = DT == kF16 ? swiglu_fp16_gate(gv[i], uv[i]) : swiglu(gv[i], uv[i]);
     convrot256_lanes<true>(v, buf, t);
   };
   auto group_absmax = [&](int g, const float (&v)[16]) {

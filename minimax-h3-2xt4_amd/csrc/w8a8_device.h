@@ -135,6 +135,30 @@ __device__ __forceinline__ float swiglu(float g, float u) {
   return act * u;
 }
 
+// The same for a gate g that is an fp16 value. For -44 < g < 2^16 (finite
+// fp16 gates above -44: then 1 <= 1 + exp(-g) < 2^64) the division takes the
+// reciprocal refined by one Newton step and two residual corrections, each a
+// single-rounding FMA; the reciprocal, the quotient and the residuals stay
+// normal, so no operand scaling or special-case fix-up is needed. The
+// quotient equals the IEEE one for every such gate: the GPU parity tests run
+// every finite fp16 gate through the kernel. Other gates (below -44, inf,
+// NaN) take the IEEE division. The range test |g - 32746| < 32790 is exact
+// for fp16 g (the difference fits in 24 bits) and false for inf and NaN.
+__device__ __forceinline__ float swiglu_fp16_gate(float g, float u) {
+  const float den = 1.0f + exp_f32(-g);
+  float act;
+  if (__builtin_expect(fabsf(g - 32746.0f) < 32790.0f, 1)) {
+    float r = __builtin_amdgcn_rcpf(den);
+    r = __builtin_fmaf(__builtin_fmaf(-den, r, 1.0f), r, r);
+    const float q0 = g * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-den, q0, g), r, q0);
+    act = __builtin_fmaf(__builtin_fmaf(-den, q1, g), r, q1);
+  } else {
+    act = g / den;
+  }
+  return act * u;
+}
+
 // ------------------------------------------------------------- quantizer
 // q = clamp(rne(x / s), -128, 127) with the IEEE quotient x / s.
 // rcp = 1/s (IEEE). The product x*rcp is within 2^-15 of the quotient for

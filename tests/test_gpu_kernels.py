@@ -431,6 +431,42 @@ def test_swiglu_external_max_fp32_input_and_phases(gpu):
                       'maximum phase')
 
 
+def test_swiglu_every_finite_fp16_gate(gpu):
+    """One row per finite fp16 gate value (W = 256, up = 1). With a single
+    nonzero gate every rotated element is +-a / 16 for a = g / (1 + exp(-g)),
+    so the group maximum is |a| / 16 exactly: every gate's activation, from
+    the reciprocal division or the IEEE one, is compared bit for bit."""
+    bits = np.arange(65536, dtype=np.uint32)
+    finite = bits[(bits & 0x7C00) != 0x7C00].astype(np.uint16)
+    print(f'swiglu: {finite.size} finite fp16 gates', flush=True)
+    x = torch.zeros((finite.size, 512), dtype=torch.float16)
+    x[:, 256:] = 1.0
+    x[:, 0] = torch.from_numpy(finite.view(np.float16))
+    res = kernels.swiglu_quantize(x.to(gpu), want_row_max=True, want_group_max=True)
+    gates = finite.view(np.float16).astype(np.float32)
+    want = (np.abs(o.swiglu_f32(gates, np.ones_like(gates))) * np.float32(1.0 / 16.0)).astype(np.float32)
+    assert_bits_equal(np_of(res['group_max'])[:, 0], want, 'group max = |silu(g)| / 16, every finite gate')
+    idx = np.arange(0, finite.size, 97)
+    wq, ws, wg = o.fc2_prologue(np_of(x)[idx])
+    assert_bits_equal(np_of(res['q'])[idx], wq, 'codes of sampled gate rows')
+    assert_bits_equal(np_of(res['scale']).reshape(-1)[idx], ws, 'scales of sampled gate rows')
+
+
+def test_swiglu_infinite_gate(gpu):
+    # A +inf gate is outside the reciprocal division's range: inf / (1 + 0)
+    # is inf, and the group maximum with it.
+    x = torch.zeros((2, 512), dtype=torch.float16)
+    x[:, 256:] = 1.0
+    x[0, 3] = float('inf')
+    x[1, 3] = 60000.0
+    res = kernels.swiglu_quantize(x.to(gpu), want_group_max=True)
+    xs = np_of(x).astype(np.float32)
+    with np.errstate(invalid='ignore'):
+        rot = o.convrot256(o.swiglu_f32(xs[:, :256], xs[:, 256:]))
+    assert_bits_equal(np_of(res['group_max']), np.abs(rot).max(-1, keepdims=True), 'group max with an infinite gate')
+    assert np.isinf(np_of(res['group_max'])[0, 0])
+
+
 # ------------------------------------------------------------------ DiT gated residual update
 GATE_CASES = [
     # (m, n, k): persistent tiles with ragged edges, the skinny path, split K
