@@ -1215,20 +1215,24 @@ void launch_skinny(const GemmParams& p, hipStream_t s) {
 
 // Weight streaming for M <= 64 with K a multiple of 128 (text-encoder
 // decode and short prefill). A workgroup of 4 waves owns 64 weight rows and
-// one of ksplit contiguous K ranges (one workgroup per CU); its waves split
-// that range into contiguous runs of 128-byte K steps. Each wave streams its
-// run through its own ring of R LDS slots with LDS DMA only: a step is the
-// 64 weight rows (8 global_load_lds_dwordx4 of 8 rows x 128 bytes) and the
-// MB 16-row blocks of activation rows (2 MB more). In each 128-byte row,
-// 16-byte chunk c lands at c ^ ((r >> 1) & 7), so the DMA writes and the
-// fragment reads are free of bank conflicts. Keeping every load of the loop
-// an LDS DMA makes the counted waits exact: DMA loads complete in issue
-// order among themselves, but not with respect to ordinary loads into
-// registers. The slot is read back as v_mfma_i32_16x16x64_i8 fragments
-// (weights as A, activations as B; two 64-byte sub-steps per step). The
-// waves' sums meet in LDS (reusing the ring); with ksplit == 1 the shared
-// epilogue writes the outputs, otherwise plane ks of the caller's workspace
-// receives the workgroup's int32 sums and splitk_reduce_kernel finishes.
+// one of ksplit contiguous K ranges (one workgroup per CU). A step is 128
+// bytes of K: the 64 weight rows and the MB 16-row blocks of activation rows
+// (8 rows per global_load_lds_dwordx4). The workgroup streams its range
+// through one LDS ring of S steps with S - 1 steps in flight, so a CU keeps
+// ~120-140 KB of loads outstanding (the latency of the memory system, not the
+// bandwidth, bounds a shallower ring). Each wave issues a quarter of every
+// step's DMA; one barrier per step makes the step visible to all waves and
+// frees the slot read in the step before for the next refill. In each
+// 128-byte row, 16-byte chunk c lands at c ^ ((r >> 1) & 7), so the DMA
+// writes and the fragment reads are free of bank conflicts. Every load of
+// the loop is an LDS DMA, and every iteration issues the same number of them
+// (past the range's end the last step is loaded again into the freed slot,
+// which is never read), so the counted waits are exact. Wave w multiplies
+// weight rows 16 w .. 16 w + 15 with every activation block
+// (v_mfma_i32_16x16x64_i8, two 64-byte sub-steps per step) and finishes its
+// own outputs: with ksplit == 1 the shared epilogue writes them, otherwise
+// plane ks of the caller's workspace receives the int32 sums and
+// splitk_reduce_kernel finishes.
 constexpr int kStreamRows = 64;      // weight rows per workgroup
 constexpr int kStreamStep = 128;     // K bytes per step
 constexpr int kStreamWaves = 4;
@@ -1236,17 +1240,16 @@ constexpr int kStreamWaves = 4;
 template <int MB>
 struct StreamRing {
   static constexpr int kRows = kStreamRows + 16 * MB;             // weight + activation rows of a step
-  static constexpr int kDma = kRows / 8;                          // DMA instructions per step
-  static constexpr int kSlot = kRows * kStreamStep;
-  static constexpr int kSlots = MB <= 2 ? 3 : 2;
-  static constexpr int kLds = kStreamWaves * kSlots * kSlot;      // 120, 144, 112, 128 KB
+  static constexpr int kDpw = (kRows / 8 + kStreamWaves - 1) / kStreamWaves;   // DMA per wave and step
+  static constexpr int kSlot = 8 * kStreamWaves * kDpw * kStreamStep;          // padded to whole DMA groups
+  static constexpr int kSlots = (160 * 1024) / kSlot;             // 13 (MB 1, 2), 10 (MB 3, 4)
+  static constexpr int kLds = kSlots * kSlot;                     // 156, 156, 160, 160 KB
 };
 
 template <int EPI, int OUT, int MB, bool PARTIAL>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm_i8_stream(GemmParams p, int nblocks, int ksplit) {
   using R = StreamRing<MB>;
-  static_assert(kStreamWaves * kStreamRows * MB * 16 * 4 <= R::kLds, "the partial sums reuse the ring");
-  static_assert(R::kLds <= 160 * 1024 && (R::kSlots - 1) * R::kDma < 64, "LDS and vmcnt range");
+  static_assert(R::kLds <= 160 * 1024 && (R::kSlots - 2) * R::kDpw < 64, "LDS and vmcnt range");
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1254,103 +1257,77 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_i8_stream(GemmParams p
   const int n0 = nblk * kStreamRows;
   const int steps = p.k / kStreamStep;
   const int g0 = (int)((int64_t)ks * steps / ksplit), g1 = (int)((int64_t)(ks + 1) * steps / ksplit);
-  const int s0 = g0 + (g1 - g0) * wave / kStreamWaves, s1 = g0 + (g1 - g0) * (wave + 1) / kStreamWaves;
-  const int nsteps = s1 - s0;
-  int8_t* const ring = lds + wave * R::kSlots * R::kSlot;
+  const int nsteps = g1 - g0;
 
-  // DMA instruction d of a step: slot row 8 d + lane / 8 - weight row n0 +
-  // that (rows 0..63, clamped to the last weight row) or activation row
-  // that - 64 (clamped to the last of the m rows; clamped rows are never
-  // stored) - and the logical chunk that lands on physical chunk lane % 8.
-  const int8_t* src[R::kDma];
+  // This wave's DMA instruction i of a step: slot rows 8 d .. 8 d + 7 with
+  // d = kDpw * wave + i; lane -> row 8 d + lane / 8 and the logical chunk
+  // that lands on physical chunk lane % 8. Rows 0..63 are weight rows n0 +
+  // r (clamped to the last weight row), the next 16 MB activation rows
+  // (clamped to the last of the m rows; clamped rows are never stored), the
+  // padding rows past them load a weight row that is never read.
+  const int8_t* src[R::kDpw];
 #pragma unroll
-  for (int d = 0; d < R::kDma; ++d) {
-    const int r = 8 * d + (lane >> 3);
+  for (int i = 0; i < R::kDpw; ++i) {
+    const int r = 8 * (R::kDpw * wave + i) + (lane >> 3);
     const int c = (lane & 7) ^ ((r >> 1) & 7);
-    src[d] = r < kStreamRows ? p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb + c * 16
-                             : p.a + (int64_t)min(r - kStreamRows, p.m - 1) * p.lda + c * 16;
+    src[i] = r >= kStreamRows && r < R::kRows
+                 ? p.a + (int64_t)min(r - kStreamRows, p.m - 1) * p.lda + c * 16
+                 : p.b + (int64_t)min(n0 + (r < kStreamRows ? r : 0), p.n - 1) * p.ldb + c * 16;
   }
   const int fr = lane & 15, fc = lane >> 4;
-
-  v4i acc[4][MB];
+  v4i acc[MB];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = v4i{0, 0, 0, 0};
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = v4i{0, 0, 0, 0};
 
   if (nsteps > 0) {
-    // Step t of the wave's run into a slot (past the run's end the last step
-    // is loaded again, into a slot that is never read, so every iteration
-    // issues the same instructions and the wait count below is exact).
     auto dma_step = [&](int t, int slot) {
-      const int64_t kof = (int64_t)(s0 + min(t, nsteps - 1)) * kStreamStep;
+      const int64_t kof = (int64_t)(g0 + min(t, nsteps - 1)) * kStreamStep;
 #pragma unroll
-      for (int d = 0; d < R::kDma; ++d) dma16(src[d] + kof, ring + slot * R::kSlot + d * 1024);
+      for (int i = 0; i < R::kDpw; ++i)
+        dma16(src[i] + kof, lds + slot * R::kSlot + (R::kDpw * wave + i) * 1024);
     };
     // Fragment (slot rows row0 + fr, K bytes 64 j + 16 fc .. + 16).
     auto frag = [&](int slot, int row0, int j) {
       const int r = row0 + fr;
       const int c = (4 * j + fc) ^ ((r >> 1) & 7);
-      return *reinterpret_cast<const v4i*>(ring + slot * R::kSlot + r * kStreamStep + c * 16);
+      return *reinterpret_cast<const v4i*>(lds + slot * R::kSlot + r * kStreamStep + c * 16);
     };
 #pragma unroll
-    for (int i = 0; i < R::kSlots; ++i) dma_step(i, i);
-    // Iteration t waits until only the R - 1 younger steps' DMA may be in
-    // flight, reads step t's fragments, refills the slot with step t + R,
-    // then multiplies.
-    int slot = 0;
+    for (int i = 0; i < R::kSlots - 1; ++i) dma_step(i, i);
+    int slot = 0;                      // slot of step t
+    int refill = R::kSlots - 1;        // slot of step t + S - 1 (read in step t - 1)
     for (int t = 0; t < nsteps; ++t) {
-      constexpr int kWait = (R::kSlots - 1) * R::kDma;
-      __builtin_amdgcn_s_waitcnt((kWait & 0xF) | ((kWait >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-      v4i w[2][4], x[2][MB];
+      // This wave's loads of step t landed (only the S - 2 younger steps'
+      // may be in flight); after the barrier every wave's have, and every
+      // wave is done reading the slot of step t - 1.
+      wait_vmcnt<(R::kSlots - 2) * R::kDpw>();
+      block_barrier();
+      dma_step(t + R::kSlots - 1, refill);
+      v4i w[2], x[2][MB];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) w[j][nb] = frag(slot, nb * 16, j);
+        w[j] = frag(slot, 16 * wave, j);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) x[j][mb] = frag(slot, kStreamRows + mb * 16, j);
       }
-      // The compiler does not order the DMA's LDS write after these reads:
-      // the wait and the fences do.
-      wait_lgkm();
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      dma_step(t + R::kSlots, slot);
-      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j][nb], x[j][mb], acc[nb][mb], 0, 0, 0);
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], x[j][mb], acc[mb], 0, 0, 0);
+      refill = slot;
       slot = slot + 1 == R::kSlots ? 0 : slot + 1;
     }
   }
-  wait_vmcnt<0>();   // no DMA may still target the ring when it is reused below
-  __syncthreads();
-  // Lane holds C[m][n..n+3] for m = 16 mb + fr, n = 16 nb + 4 fc (local);
-  // the waves' sums meet in LDS as red[wave][n][m].
-  int* red = reinterpret_cast<int*>(lds);
-  constexpr int RM = MB * 16;
+  wait_vmcnt<0>();   // no DMA may still target the ring at exit
+  // Lane holds C[m][n .. n + 3] for m = 16 mb + fr, n = n0 + 16 wave + 4 fc.
+  const int n = n0 + 16 * wave + 4 * fc;
+  const int valid = min(4, p.n - n);
+  if (valid <= 0) return;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) red[(wave * kStreamRows + nb * 16 + 4 * fc + v) * RM + mb * 16 + fr] = acc[nb][mb][v];
-  __syncthreads();
-  for (int idx = tid; idx < p.m * (kStreamRows / 4); idx += kStreamWaves * 64) {
-    const int m = idx / (kStreamRows / 4);
-    const int nl = (idx % (kStreamRows / 4)) * 4;
-    const int n = n0 + nl;
-    const int valid = min(4, p.n - n);
-    if (valid <= 0) continue;
-    int c[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int w = 0; w < kStreamWaves; ++w)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) c[v] += red[(w * kStreamRows + nl + v) * RM + m];
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = 16 * mb + fr;
+    if (m >= p.m) continue;
+    const int c[4] = {acc[mb][0], acc[mb][1], acc[mb][2], acc[mb][3]};
     if constexpr (PARTIAL) {
       int* o = reinterpret_cast<int*>(p.ws) + (int64_t)ks * p.m * p.n + (int64_t)m * p.n + n;
       if (valid == 4 && (p.n & 3) == 0) *reinterpret_cast<int4*>(o) = make_int4(c[0], c[1], c[2], c[3]);
@@ -1369,11 +1346,11 @@ inline bool stream_applies(int64_t m, int64_t k) {
 }
 
 // K split of the streaming kernel: the largest power of two up to 8 that
-// keeps one workgroup per CU and at least two steps per wave.
+// keeps one workgroup per CU and at least eight steps per workgroup.
 inline int stream_ksplit(int64_t n, int64_t k, int cus) {
   const int64_t nblocks = (n + kStreamRows - 1) / kStreamRows, steps = k / kStreamStep;
   int ks = 1;
-  while (ks < 8 && nblocks * ks * 2 <= cus && steps / (ks * 2) >= 2 * kStreamWaves) ks *= 2;
+  while (ks < 8 && nblocks * ks * 2 <= cus && steps / (ks * 2) >= 8) ks *= 2;
   return ks;
 }
 
