@@ -1108,9 +1108,10 @@ void gemm_i8_persistent(GemmParams p) {
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }
 
-// Skinny GEMM for M <= 64 (text-encoder decode / short prefill): weight
-// streaming. A workgroup of W wavefronts owns NR weight rows (NR = 16 with
-// W = 8, or NR = 32 with W = 4 when N / 32 still fills the GPU); the waves
+// Skinny GEMM for 2 <= M <= 16, and 17 <= M <= 64 where K is not a multiple
+// of 128 (text-encoder short prefill): weight streaming. A workgroup of W
+// wavefronts owns NR weight rows (NR = 16 with W = 8, or NR = 32 with W = 4
+// when N / 32 still fills the GPU); the waves
 // split K into contiguous ranges and multiply with v_mfma_i32_16x16x64_i8
 // (weight rows as the MFMA A operand, MB 16-row activation blocks as B),
 // loading both operands straight from memory into registers in batches of U
@@ -1201,6 +1202,74 @@ __global__ __launch_bounds__(NR == 16 ? 512 : 256) void gemm_i8_skinny(GemmParam
     const float a = EPI != kEpiInt32 ? p.row_scale[m] : 0.0f;
     epilogue4<EPI, OUT>(p, m, n, valid, c, a);
   }
+}
+
+// GEMV (M == 1, decode): wave w owns R consecutive weight rows; lane l
+// reads the 16-byte K chunks l, l + 64, ... of each, so every load
+// instruction covers 1 KB of one row, and multiplies them with the matching
+// activation chunk by v_dot4_i32_i8 (exact int32 sums in any order). A batch
+// is C = 16 / R chunks of each row: 16 KB per wave in flight. Each row's
+// partial sums meet by a cross-lane reduction; lane 0 stores the R outputs
+// through the shared epilogue.
+template <int EPI, int OUT, int R>
+__global__ __launch_bounds__(256) void gemv_i8(GemmParams p) {
+  constexpr int C = R == 4 ? 4 : 8;
+  const int lane = threadIdx.x & 63;
+  const int n0 = (int)(((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * R);
+  if (n0 >= p.n) return;
+  const int chunks = p.k >> 4;
+  const int8_t* wr[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) wr[r] = p.b + (int64_t)min(n0 + r, p.n - 1) * p.ldb;
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0;
+  for (int c0 = 0; c0 < chunks; c0 += 64 * C) {
+    v4i w[R][C], x[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      const int c = c0 + 64 * i + lane;
+      const bool ok = c < chunks;
+      x[i] = ok ? *reinterpret_cast<const v4i*>(p.a + (int64_t)c * 16) : v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        w[r][i] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(wr[r] + (int64_t)c * 16))
+                     : v4i{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int i = 0; i < C; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[r] = __builtin_amdgcn_sdot4(w[r][i][e], x[i][e], acc[r], false);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+  if (lane != 0) return;
+  const float a = EPI != kEpiInt32 ? p.row_scale[0] : 0.0f;
+#pragma unroll
+  for (int g = 0; g < R; g += 4) {
+    const int n = n0 + g;
+    const int valid = min(min(4, R - g), p.n - n);
+    if (valid <= 0) break;
+    int c[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int v = 0; v < 4 && g + v < R; ++v) c[v] = acc[g + v];
+    epilogue4<EPI, OUT>(p, 0, n, valid, c, a);
+  }
+}
+
+// Rows per wave of the GEMV: the most (4, 2, 1) that still give every SIMD
+// of the GPU four waves.
+template <int EPI, int OUT>
+void launch_gemv(const GemmParams& p, int cus, hipStream_t s) {
+  const int64_t want = (int64_t)cus * 16;   // 4 SIMDs x 4 waves
+  auto grid = [&](int r) { return dim3((unsigned)(((p.n + r - 1) / r + 3) / 4)); };
+  if ((p.n + 3) / 4 >= want) hipLaunchKernelGGL((gemv_i8<EPI, OUT, 4>), grid(4), dim3(256), 0, s, p);
+  else if ((p.n + 1) / 2 >= want) hipLaunchKernelGGL((gemv_i8<EPI, OUT, 2>), grid(2), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemv_i8<EPI, OUT, 1>), grid(1), dim3(256), 0, s, p);
 }
 
 template <int EPI, int OUT, int MB>
@@ -1482,6 +1551,13 @@ int launch_stream(const GemmParams& p, int ksplit, int dev, hipStream_t s) {
 
 template <int EPI, int OUT>
 int launch_gemm(const GemmParams& p, hipStream_t s) {
+  if (p.m == 1 && p.k % 16 == 0) {
+    int dev = 0;
+    const int rc = current_device(dev);
+    if (rc != W8A8_OK) return rc;
+    launch_gemv<EPI, OUT>(p, device_cus(dev), s);
+    return W8A8_OK;
+  }
   if (stream_applies(p.m, p.k)) {
     int dev = 0;
     const int rc = current_device(dev);

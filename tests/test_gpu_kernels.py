@@ -111,6 +111,49 @@ def test_gemm_skinny_epilogues(gpu, m, epi, out_dtype, bias_dtype):
     assert_bits_equal(np_of(got), want, f'skinny m={m} {epi} {out_dtype} {bias_dtype}')
 
 
+GEMV_CASES = [
+    # (n, k): M == 1 takes the GEMV. On 256 CUs a wave owns 4 weight rows
+    # when N >= 16381, 2 when N >= 8191, else 1; ragged N leaves the last wave
+    # fewer rows, and K that is not a multiple of a batch (64 lanes x 4 or 8
+    # chunks of 16 bytes) leaves lanes without a chunk.
+    (16386, 1040), (8194, 4096), (4097, 14336), (1001, 1040), (3, 16),
+]
+
+
+@pytest.mark.parametrize('n,k', GEMV_CASES)
+def test_gemv(gpu, n, k):
+    print(f'gemv 1x{n}x{k}', flush=True)
+    g = torch.Generator().manual_seed(n + k)
+    a = randi8(g, (1, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((1, 1), generator=g) * 0.01 + 1e-4
+    ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
+    bias = (torch.randn((n,), generator=g) * 0.01).half()
+    res = randn16(g, (1, n), 1 / 512)
+    acc = o.int_mm(np_of(a), np_of(b))
+    ag, bg = a.to(gpu), b.to(gpu)
+    assert_bits_equal(np_of(kernels.gemm(ag, bg)), acc, f'gemv int32 1x{n}x{k}')
+    got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       bias=bias.to(gpu), residual=res.to(gpu), out_dtype=torch.float16)
+    want = o.residual_add(np_of(res), o.dequantize_row(acc, np_of(rs), np_of(ws), 'f16', np_of(bias)))
+    assert_bits_equal(np_of(got), want, f'gemv row+bias+residual 1x{n}x{k}')
+    got = kernels.gemm(ag, bg, epilogue=kernels.EPI_COLUMN, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       out_dtype=torch.float32)
+    assert_bits_equal(np_of(got), o.dequantize_column(acc, np_of(rs), np_of(ws), 'f32'), f'gemv column 1x{n}x{k}')
+
+
+def test_gemv_extremes(gpu):
+    # |sum| reaches K * 128 * 128 = 2^31 * 0.109 at K = 14336: exact in int32.
+    k = 14336
+    a = torch.full((1, k), -128, dtype=torch.int8)
+    b = torch.full((9, k), -128, dtype=torch.int8)
+    b[3] = 127
+    b[5, 1::2] = 127
+    got = np_of(kernels.gemm(a.to(gpu), b.to(gpu)))
+    assert_bits_equal(got, o.int_mm(np_of(a), np_of(b)), 'gemv extremes')
+    assert got[0, 0] == k * 128 * 128 and got[0, 3] == -k * 128 * 127
+
+
 STREAM_CASES = [
     # (m, n, k): 16 < M <= 64 with K % 128 == 0 takes the weight-streaming kernel.
     # These split K (two or four workgroups per 64-row block, partials in
