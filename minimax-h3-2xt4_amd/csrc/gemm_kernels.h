@@ -233,8 +233,9 @@ __device__ __forceinline__ int readout_col(int nw, int h, int lane) {
   return nw + 64 * h + (lane % R::LPR) * R::CPL;
 }
 
-// Staged epilogue of one 128x128 quadrant through an 8 KB wave-private LDS
-// slice, in 8 passes of 32 rows x 64 columns. Each pass writes the raw int32
+// Staged epilogue of one 128 x 32 NB quadrant (NB = 4, 3 or 2) through an
+// 8 KB wave-private LDS slice, in passes of 32 rows x 64 columns (8, or 4
+// for NB = 2). Each pass writes the raw int32
 // accumulators into the slice (16-byte chunks XOR-swizzled by row), then
 // each lane reads CPL consecutive columns of one row back, dequantizes them
 // in the reference's order (ROW (C*a)*w, COLUMN C*(a*w), then + bias, then
@@ -262,11 +263,13 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
 #pragma unroll
   for (int pass = 0; pass < 8; ++pass) {
     const int mb = pass >> 1, h = pass & 1;
+    // A quadrant 64 columns wide (NB == 2) has no second half.
+    if (NB == 2 && h == 1) continue;
     const int mrow = mw + mb * 32;
     const int ncol = nw + 64 * h + ocol;
     // A quadrant 96 columns wide (NB == 3) has only its first 32 in the
     // second half: the other read-out lanes of those passes store nothing.
-    const bool in_quad = NB == 4 || h == 0 || ocol < 32;
+    const bool in_quad = NB != 3 || h == 0 || ocol < 32;
     // INTERIOR: every row and column of the quadrant is inside the output
     // and rows are 16-byte aligned, so no store needs a mask.
     const bool full_cols = INTERIOR || (p.vec16 && ncol + R::CPL <= p.n);
@@ -745,13 +748,13 @@ __device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw,
   }
 }
 
-// Persistent 256x256 GEMM fed by gfx950 direct global->LDS loads
-// (global_load_lds_dwordx4). One workgroup per CU walks its tiles; the
-// operand stream runs across tile boundaries.
+// Persistent GEMM (256 x 256, 256 x 192 or 128 x 256 output tiles) fed by
+// gfx950 direct global->LDS loads (global_load_lds_dwordx4). One workgroup
+// per CU walks its tiles; the operand stream runs across tile boundaries.
 //
-// A stage holds K = 128 of both operand tiles (256 rows x 128 bytes each):
-// every row segment is a whole 128-byte line, which streams from L2 about
-// 1.6x faster per CU than half lines. The 160 KB of LDS is a ring of five
+// A stage holds K = 128 of both operand tiles (up to 256 rows x 128 bytes
+// each): every row segment is a whole 128-byte line, which streams from L2
+// about 1.6x faster per CU than half lines. The 160 KB of LDS is a ring of five
 // 32 KB slots, one operand tile of one stage each: unit h (the A tile of
 // stage h / 2 for even h, its B tile for odd h) lives in slot h % 5. While
 // stage g computes from units 2g and 2g + 1, units 2g + 2 .. 2g + 4 stream
@@ -807,15 +810,19 @@ __device__ __forceinline__ void static_for(F&& f) {
 template <int EPI, int OUT, int FLAGS, int NB>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_i8_persistent(GemmParams p) {
-  // NB MFMA column blocks per wave: tiles are 256 x 64 NB (256 or 192
-  // columns), a wave's quadrant 128 x 32 NB, and a B unit 2 NB DMA
-  // instructions per wave (8 rows each).
-  static_assert(NB == 4 || (NB == 3 && (FLAGS & kWithRope) == 0), "NB 4, or 3 without the RoPE epilogue");
-  constexpr int BN = 64 * NB, WN = 32 * NB, JB = 2 * NB;
+  // NB MFMA column blocks per wave. NB = 4 or 3: tiles are 256 x 64 NB
+  // (256 or 192 columns), the waves 2 x 2 quadrants of 128 x 32 NB. NB = 2:
+  // tiles are 128 x 256 (for M of a few hundred rows), the waves 1 x 4
+  // quadrants of 128 x 64 sharing the A tile, which fills half its slot. An
+  // A unit is NA, a B unit JB DMA instructions per wave (8 rows each).
+  static_assert(NB == 4 || ((NB == 3 || NB == 2) && (FLAGS & kWithRope) == 0),
+                "NB 4, or 3 or 2 without the RoPE epilogue");
+  constexpr int BM = NB == 2 ? 128 : 256, BN = NB == 2 ? 256 : 64 * NB, WN = 32 * NB;
+  constexpr int NA = BM / 32, JB = BN / 32;
   extern __shared__ __attribute__((aligned(16))) int8_t smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tiles_m = (p.m + kBM - 1) / kBM, tiles_n = (p.n + BN - 1) / BN;
+  const int tiles_m = (p.m + BM - 1) / BM, tiles_n = (p.n + BN - 1) / BN;
   // Tile schedule. Workgroup w runs on XCD w % 8 (round-robin dispatch).
   // With a grid that is a multiple of 8, XCD x owns the contiguous raster
   // range [x*T/8, (x+1)*T/8) and its G/8 workgroups walk it in lockstep, so
@@ -838,17 +845,17 @@ void gemm_i8_persistent(GemmParams p) {
   auto ks_end = [&](int item) { return (item % ksplit + 1) * kstages / ksplit; };
 
   // DMA cursor: the (tile, stage) of the next stage to issue. Wave w fills
-  // rows 64 w .. 64 w + 63 of the A tile and 8 JB w .. 8 JB (w + 1) - 1 of
-  // the B tile, 8 rows per instruction; offsets are 32-bit (the host checks
-  // that the operands span < 4 GB).
-  uint32_t off_a[8], off_b[JB];
+  // rows 8 NA w .. 8 NA (w + 1) - 1 of the A tile and 8 JB w .. 8 JB (w + 1)
+  // - 1 of the B tile, 8 rows per instruction; offsets are 32-bit (the host
+  // checks that the operands span < 4 GB).
+  uint32_t off_a[NA], off_b[JB];
   auto point = [&](int i) {
     int tm, tn;
     raster(item_of(i) / ksplit, tiles_m, tiles_n, tm, tn);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = (wave * 8 + j) * 8 + (lane >> 3);
-      off_a[j] = (uint32_t)((int64_t)min(tm * kBM + row, p.m - 1) * p.lda + lds_chunk(row, lane & 7) * 16);
+    for (int j = 0; j < NA; ++j) {
+      const int row = (wave * NA + j) * 8 + (lane >> 3);
+      off_a[j] = (uint32_t)((int64_t)min(tm * BM + row, p.m - 1) * p.lda + lds_chunk(row, lane & 7) * 16);
     }
 #pragma unroll
     for (int j = 0; j < JB; ++j) {
@@ -859,7 +866,7 @@ void gemm_i8_persistent(GemmParams p) {
   int dma_i = 0, dma_ks = ks_begin(item_of(0)), dma_end = ks_end(item_of(0));
   point(0);
   // The ring: unit h (the A tile of global stage h / 2 for even h, its B
-  // tile for odd h) goes to slot h % kSlots. A unit is 8 (A) or JB (B) DMA
+  // tile for odd h) goes to slot h % kSlots. A unit is NA (A) or JB (B) DMA
   // instructions per wave, issued in halves spread between MFMAs (a burst
   // of them would stall the issuing wave behind the address unit). The
   // cursor advances after a B tile's second half; past the last stage of
@@ -878,12 +885,12 @@ void gemm_i8_persistent(GemmParams p) {
       point(dma_i);
     }
   };
-  // DMA instruction J (0..7 of A, 0..JB - 1 of B) of this wave's part of
-  // the cursor stage's A or B tile into slot.
+  // DMA instruction J (0..NA - 1 of A, 0..JB - 1 of B) of this wave's part
+  // of the cursor stage's A or B tile into slot.
   auto dma_one = [&](auto b_tag, auto j_tag, int slot) {
     constexpr bool B = decltype(b_tag)::value;
     constexpr int J = decltype(j_tag)::value;
-    int8_t* st = smem + slot * kSTile + wave * (B ? JB : 8) * 1024 + J * 1024;
+    int8_t* st = smem + slot * kSTile + wave * (B ? JB : NA) * 1024 + J * 1024;
     const uint32_t kof = (uint32_t)(dma_ks * kSK);
     if constexpr (B) dma16(p.b + (off_b[J] + kof), st);
     else dma16(p.a + (off_a[J] + kof), st);
@@ -894,12 +901,12 @@ void gemm_i8_persistent(GemmParams p) {
   auto dma_part = [&](auto b_tag, auto h_tag, auto r_tag, int slot) {
     constexpr bool B = decltype(b_tag)::value;
     constexpr int H = decltype(h_tag)::value, R = decltype(r_tag)::value;
-    constexpr int C = B ? JB / 2 : 4;
+    constexpr int C = B ? JB / 2 : NA / 2;
     static_for<C * H + R * C / NB, C * H + (R + 1) * C / NB>([&](auto j) { dma_one(b_tag, j, slot); });
   };
   auto issue_half = [&](auto b_tag, auto h_tag, int slot) {
     constexpr bool B = decltype(b_tag)::value;
-    constexpr int H = decltype(h_tag)::value, C = B ? JB / 2 : 4;
+    constexpr int H = decltype(h_tag)::value, C = B ? JB / 2 : NA / 2;
     static_for<C * H, C * H + C>([&](auto j) { dma_one(b_tag, j, slot); });
   };
   using A_ = std::false_type;
@@ -911,7 +918,7 @@ void gemm_i8_persistent(GemmParams p) {
   // stage), lane (r = lane % 32, h = lane / 32) supplies row r, logical
   // chunk 2 u + h of both operands. Each wave holds a 4x4 grid of 32x32
   // accumulator tiles (its 128x128 quadrant).
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = NB == 2 ? 0 : wave >> 1, wn = NB == 2 ? wave : wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
   const int a_row = wm * 128 * kSK + fr * kSK, b_row = wn * WN * kSK + fr * kSK;
   auto read_frags = [&](int slot_a, int slot_b, int u, v4i (&fa)[NB], v4i (&fb)[4]) {
@@ -927,8 +934,8 @@ void gemm_i8_persistent(GemmParams p) {
   // the next sub-step's first MFMA row consumes them (all four A fragments
   // fb, then the B fragments fa). NB = 4: k = 0 reads fb[0..2], k = 1
   // fb[3], fa[0..1], k = 2 fa[2..3]; NB = 3: k = 0 fb[0..3], k = 1
-  // fa[0..2]. The last MFMA row of a sub-step issues no reads, so the reads
-  // have landed when the next sub-step starts.
+  // fa[0..2]; NB = 2: k = 0 all six. The last MFMA row of a sub-step issues
+  // no reads, so the reads have landed when the next sub-step starts.
   auto read_group = [&](int slot_a, int slot_b, int u, int k, v4i (&fa)[NB], v4i (&fb)[4]) {
     const int off = lds_chunk(fr, 2 * u + fh) << 4;
     const int8_t* sa = smem + slot_a * kSTile + a_row + off;
@@ -942,12 +949,15 @@ void gemm_i8_persistent(GemmParams p) {
       } else {
         fa[2] = rd(sb, 2); fa[3] = rd(sb, 3);
       }
-    } else {
+    } else if constexpr (NB == 3) {
       if (k == 0) {
         fb[0] = rd(sa, 0); fb[1] = rd(sa, 1); fb[2] = rd(sa, 2); fb[3] = rd(sa, 3);
       } else {
         fa[0] = rd(sb, 0); fa[1] = rd(sb, 1); fa[2] = rd(sb, 2);
       }
+    } else {
+      fb[0] = rd(sa, 0); fb[1] = rd(sa, 1); fb[2] = rd(sa, 2); fb[3] = rd(sa, 3);
+      fa[0] = rd(sb, 0); fa[1] = rd(sb, 1);
     }
   };
   v16i acc[NB][4];
@@ -969,7 +979,7 @@ void gemm_i8_persistent(GemmParams p) {
   issue_half(A_{}, H0{}, 2);
   issue_half(A_{}, H1{}, 2);
   issue_half(B_{}, H0{}, 3);
-  wait_vmcnt<8 + JB / 2>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
+  wait_vmcnt<NA + JB / 2>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
   block_barrier();
   v4i fa0[NB], fb0[4], fa1[NB], fb1[4];
   read_frags(0, 1, 0, fa0, fb0);
@@ -979,7 +989,7 @@ void gemm_i8_persistent(GemmParams p) {
     const int item = item_of(i);
     int tm, tn;
     raster(item / ksplit, tiles_m, tiles_n, tm, tn);
-    const int mw = tm * kBM + wm * 128, nw = tn * BN + wn * WN;
+    const int mw = tm * BM + wm * 128, nw = tn * BN + wn * WN;
     // Row scales in the MFMA layout, the column scales (and biases) of the
     // staged read-out and the gate labels, fetched before the K loop so the
     // epilogue never waits on them.
@@ -1006,7 +1016,7 @@ void gemm_i8_persistent(GemmParams p) {
 #pragma unroll
       for (int b = 0; b < 4; ++b) acc[a][b] = v16i{};
     const int nks = ks_end(item) - ks_begin(item);   // >= 1
-    // One stage: 16 NB MFMAs, 4 (NB + 4) fragment reads and 8 + JB DMA
+    // One stage: 16 NB MFMAs, 4 (NB + 4) fragment reads and NA + JB DMA
     // instructions.
     int stg = 0;   // the last stage's B slot: the epilogue's staging area
     int ks = 0;
@@ -1044,7 +1054,7 @@ void gemm_i8_persistent(GemmParams p) {
       // The next stage (units 2g + 2, 2g + 3) landed - only unit 2g + 4,
       // issued after them, may still be in flight - and this wave's reads of
       // this stage returned;
-      wait_vm_lgkm<8>();
+      wait_vm_lgkm<NA>();
       block_barrier();   // ... for every wave: both slots are released.
       static_for<0, NB>([&](auto r_tag) {
         constexpr int R = decltype(r_tag)::value;
@@ -1063,8 +1073,8 @@ void gemm_i8_persistent(GemmParams p) {
     } while (++ks < nks);
     // The tile's scale and bias loads have landed: at most unit 2g + 4 and
     // the first half of unit 2g + 5 are younger and in flight. (The
-    // epilogue's residual loads queue behind those 8 + JB / 2 instructions.)
-    wait_vmcnt<8 + JB / 2>();
+    // epilogue's residual loads queue behind those NA + JB / 2 instructions.)
+    wait_vmcnt<NA + JB / 2>();
     float bsc[2][8];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -1513,6 +1523,7 @@ int launch_persistent_nb(const GemmParams& p, const GemmPlan& plan, int dev, hip
   const int64_t tiles = plan_tiles(p.m, p.n, plan);
   if constexpr ((FLAGS & kWithRope) == 0) {
     if (plan.nb == 3) return launch_persistent<EPI, OUT, FLAGS, 3>(p, tiles, dev, s);
+    if (plan.nb == 2) return launch_persistent<EPI, OUT, FLAGS, 2>(p, tiles, dev, s);
   }
   return launch_persistent<EPI, OUT, FLAGS, 4>(p, tiles, dev, s);
 }

@@ -60,36 +60,40 @@ void launch_dequant(const GemmParams& p, const int32_t* acc, int64_t ldacc, hipS
 // (1: none) and the workspace bytes it needs.
 int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_bytes);
 
-// Tile width and K split of the persistent kernel: 256 x 64 nb output tiles
-// (nb 4: 256 x 256, nb 3: 256 x 192), K split ksplit ways.
+// Tile shape and K split of the persistent kernel: nb 4: 256 x 256, nb 3:
+// 256 x 192, nb 2: 128 x 256 output tiles; K split ksplit ways.
 struct GemmPlan {
   int nb;
   int ksplit;
 };
 
 inline int64_t plan_tiles(int64_t m, int64_t n, const GemmPlan& plan) {
-  return ((m + 255) / 256) * ((n + 64 * plan.nb - 1) / (64 * plan.nb));
+  const int64_t bm = plan.nb == 2 ? 128 : 256, bn = plan.nb == 2 ? 256 : 64 * plan.nb;
+  return ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
 }
 
 // The plan of least modelled time for an m x n x k GEMM (k a multiple of
 // 128) on cus CUs, with at most max_split K splits. The cost is counted in
 // K = 128 stages of a 256 x 256 tile (about 1 us on the power-limited
 // clock): rounds of work items x (stages per item x the tile's relative
-// cost, 0.85 for 192-wide tiles whose stages take 0.80 of the cycles, + 8
-// for the tile's epilogue and the launch's fill and drain), plus the split
-// partials' write-and-read traffic at about 6.5 TB/s. A plan replaces the
-// one before it only when it is 10% faster (256-wide and unsplit first).
+// cost + the tile's epilogue and the launch's fill and drain), plus the
+// split partials' write-and-read traffic at about 6.5 TB/s. A 256 x 192
+// stage costs 0.85 (0.80 of the cycles), a 128 x 256 stage 0.6 with an
+// epilogue of 6 instead of 8: fitted to the fastest measured plan of eight
+// shapes with M of 300..700 rows, where 256-row tiles leave most CUs idle
+// or need large split partials. A plan replaces the one before it only
+// when it is 10% faster (256 x 256 and unsplit first).
 inline GemmPlan gemm_plan(int64_t m, int64_t n, int64_t k, int cus, int max_split = 8) {
   const int64_t kst = k / 128;
   GemmPlan best{4, 1};
   double best_t = -1.0;
-  for (int nb = 4; nb >= 3; --nb) {
+  for (int nb = 4; nb >= 2; --nb) {
     const int64_t tiles = plan_tiles(m, n, GemmPlan{nb, 1});
-    const double f = nb == 4 ? 1.0 : 0.85;
+    const double f = nb == 4 ? 1.0 : nb == 3 ? 0.85 : 0.6, e = nb == 2 ? 6.0 : 8.0;
     for (int ks = 1; ks <= max_split; ks *= 2) {
       if (ks > 1 && (tiles >= cus || kst / ks < 2)) break;
       const int64_t rounds = (tiles * ks + cus - 1) / cus;
-      double t = (double)rounds * ((double)((kst + ks - 1) / ks) * f + 8.0);
+      double t = (double)rounds * ((double)((kst + ks - 1) / ks) * f + e);
       if (ks > 1) t += (double)ks * m * n * 8 / 6.5e12 * 1e6;
       if (best_t < 0.0 || t < 0.9 * best_t) {
         best = GemmPlan{nb, ks};

@@ -72,7 +72,7 @@ def test_gemm_strided_operands_and_empty(gpu):
 @pytest.mark.parametrize('bias_dtype', [None, torch.float16, torch.float32])
 def test_gemm_fused_epilogue(gpu, epi, out_dtype, bias_dtype):
     g = torch.Generator().manual_seed(11)
-    # 521 x 300: full 256x256 tiles (staged epilogue) and ragged edge tiles
+    # 521 x 300: full tiles (staged epilogue) and ragged edge tiles (128 x 256 tiles on 256 CUs)
     m, n, k = 521, 300, 256
     a = randi8(g, (m, k))
     b = randi8(g, (n, k))
@@ -202,13 +202,17 @@ def test_gemm_stream_strided_weight_and_short_k(gpu):
         assert_bits_equal(np_of(kernels.gemm(a.to(gpu), b.to(gpu))), o.int_mm(np_of(a), np_of(b)), f'k={k}')
 
 
-@pytest.mark.parametrize('m,n,k', [(4096, 3072, 3072), (2000, 2900, 3072), (1000, 1000, 2048)])
-def test_gemm_192_wide_tiles(gpu, m, n, k):
-    # Shapes the host plans with 256 x 192 tiles: 16 x 16 = 256 of them fill
-    # the GPU where 256 x 256 leaves 64 CUs idle (4096 x 3072); ragged edges
-    # in M and N (2000 x 2900: last tiles of 208 rows and 20 columns); and K
-    # split four ways over 4 x 6 tiles (1000 x 1000). Every epilogue variant.
-    print(f'192-wide tiles {m}x{n}x{k}', flush=True)
+@pytest.mark.parametrize('m,n,k', [(4096, 3072, 3072), (2000, 2900, 16384), (700, 3000, 1024), (353, 5120, 12800),
+                                   (353, 512, 5120)])
+def test_gemm_tile_shapes(gpu, m, n, k):
+    # Shapes the host plans with the narrower tiles, on 256 CUs: 256 x 192
+    # tiles, 16 x 16 = 256 of them filling the GPU where 256 x 256 leaves 64
+    # CUs idle (4096 x 3072), and with K split two ways and ragged edges in M
+    # and N (2000 x 2900: last tiles of 208 rows and 20 columns); 128 x 256
+    # tiles for M of a few hundred rows, unsplit (700 x 3000: last tile of 60
+    # rows), K split four (353 x 5120) and eight ways (353 x 512: two tile
+    # columns, the second of 256). Every epilogue variant.
+    print(f'tile shapes {m}x{n}x{k}', flush=True)
     g = torch.Generator().manual_seed(m + n + k)
     a = randi8(g, (m, k))
     b = randi8(g, (n, k))
@@ -299,7 +303,7 @@ def test_gemm_more_tiles_than_cus_epilogues(gpu, epi, out_dtype, bias_dtype, res
 
 SPLITK_CASES = [
     # (m, n, k, epilogue, out dtype, bias dtype, residual): grids smaller than the CU count
-    (512, 4096, 14336, 'int32', None, None, False),     # text-encoder down at M=512: 32 tiles
+    (512, 4096, 14336, 'int32', None, None, False),     # text-encoder down at M=512: 64 tiles of 128 x 256
     (300, 520, 2048, 'row', torch.float16, None, True),  # ragged rows and columns
     (300, 520, 2048, 'column', torch.bfloat16, torch.float16, False),
     (257, 1000, 1024, 'row', torch.float32, torch.float32, False),
