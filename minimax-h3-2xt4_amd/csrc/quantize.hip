@@ -5,6 +5,8 @@
 // 128-bit int8 store, so each wave instruction touches a contiguous span.
 // With ConvRot256 a 256-column group is owned by 16 consecutive lanes and
 // rotated through a wave-private LDS transpose (w8a8_device.h).
+#include <atomic>
+
 #include "w8a8_device.h"
 #include "w8a8_host.h"
 
@@ -104,15 +106,20 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   }
 }
 
-// Few rows (decode / short prefill): one 256-thread workgroup per row, thread
-// t owning units u = t + 256 j (J units, kept in registers), so a row is
-// spread over four wavefronts instead of one.
-template <int DT, int ROT, int J>
-__global__ __launch_bounds__(256) void quantize_row_wg_kernel(
+// Few rows (decode / short prefill): one workgroup of W wavefronts per row,
+// thread t owning units u = t + 64 W j (J units, kept in registers), so a
+// row is spread over W wavefronts instead of one: W = 16 for up to one row
+// per CU (four waves per SIMD), W = 4 beyond.
+template <int ROT, int W>
+constexpr int row_wg_lds_bytes() { return ((ROT ? W * kRotWave : 0) + W) * 4; }
+
+template <int DT, int ROT, int J, int W>
+__global__ __launch_bounds__(64 * W) void quantize_row_wg_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t cols, const float* __restrict__ row_max,
     int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, float* __restrict__ row_max_out) {
-  __shared__ float lds[ROT ? 4 * kRotWave : 1];
-  __shared__ float wmax[4];
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* const lds = smem;
+  float* const wmax = smem + (ROT ? W * kRotWave : 0);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const int units = (int)(cols >> 4);
@@ -123,7 +130,7 @@ __global__ __launch_bounds__(256) void quantize_row_wg_kernel(
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int u = tid + 256 * j;
+    const int u = tid + 64 * W * j;
     if (u < units) {
       load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v[j]);
       if constexpr (ROT != 0) {
@@ -140,14 +147,20 @@ __global__ __launch_bounds__(256) void quantize_row_wg_kernel(
   amax = wave_max(amax);
   if (lane == 0) wmax[wave] = amax;
   __syncthreads();
-  amax = row_max ? row_max[row] : fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (row_max) {
+    amax = row_max[row];
+  } else {
+    amax = wmax[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) amax = fmaxf(amax, wmax[w]);
+  }
   if (row_max_out != nullptr && tid == 0) row_max_out[row] = amax;
   if (q == nullptr) return;  // maximum phase only
   const float s = row_scale_of(amax);
   const float rcp = 1.0f / s;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const int u = tid + 256 * j;
+    const int u = tid + 64 * W * j;
     if (u < units) *reinterpret_cast<uint4*>(q + row * ldq + (int64_t)u * 16) = quant16(v[j], s, rcp);
   }
   if (tid == 0) scale[row] = s;
@@ -158,10 +171,36 @@ static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
   // Below 1024 rows a wavefront per row leaves most of the GPU idle: spread
   // each row over a workgroup (up to 16384 columns).
   if (a->rows < 1024 && a->cols <= 16384) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+      set_error("w8a8_quantize_rows: hipGetDevice failed");
+      return W8A8_ERR_LAUNCH;
+    }
+    const dim3 g((unsigned)a->rows);
+    if (a->rows <= (int64_t)device_cus(dev)) {
+      // 16 waves, one unit per thread. With the rotation the LDS exceeds the
+      // 64 KB default: raise the limit once per device.
+      constexpr int kLds = row_wg_lds_bytes<ROT, 16>();
+      static std::atomic<uint64_t> enabled{0};
+      const uint64_t bit = 1ull << dev;
+      if (!(enabled.load(std::memory_order_acquire) & bit)) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&quantize_row_wg_kernel<DT, ROT, 1, 16>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
+        if (e != hipSuccess) {
+          set_error("w8a8_quantize_rows: cannot enable %d bytes of LDS: %s", kLds, hipGetErrorString(e));
+          return W8A8_ERR_LAUNCH;
+        }
+        enabled.fetch_or(bit, std::memory_order_acq_rel);
+      }
+      hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, 1, 16>), g, dim3(1024), kLds, stream, a->x, a->ldx,
+                         a->cols, a->row_max, a->q, a->ldq, a->scale, a->row_max_out);
+      return launch_status("w8a8_quantize_rows");
+    }
     const int jw = (int)((a->cols / 16 + 255) / 256);
-    const dim3 g((unsigned)a->rows), b(256);
-#define W8A8_WLAUNCH(JJ)                                                                              \
-  hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, JJ>), g, b, 0, stream, a->x, a->ldx, a->cols, \
+    const dim3 b(256);
+    constexpr int kLds4 = row_wg_lds_bytes<ROT, 4>();
+#define W8A8_WLAUNCH(JJ)                                                                                    \
+  hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, JJ, 4>), g, b, kLds4, stream, a->x, a->ldx, a->cols, \
                      a->row_max, a->q, a->ldq, a->scale, a->row_max_out)
     switch (jw) {
       case 1: W8A8_WLAUNCH(1); break;

@@ -1,33 +1,45 @@
 // FC2 prologue: FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8, fused.
 //
-// One 256-thread workgroup per row. Sixteen 16-lane slots each own one
+// One workgroup of W wavefronts per row: 4 W 16-lane slots each own one
 // 256-column group per pass (lane t of a slot loads gate/up elements
 // [16t, 16t + 16) of the group with 128-bit loads). The rotated FP32 values
 // stay in registers until the row maximum is known, so the only HBM traffic
 // is the FP16 gate|up row in and the int8 row out (plus the fp32 scale).
-// (Timed on one box: at width 8192 two passes of 4-wave workgroups run
-// 220 us against 262 us for one pass of 8-wave workgroups.)
+// Many rows take W = 4 (timed on one box: at width 8192 two passes of 4-wave
+// workgroups run 220 us against 262 us for one pass of 8-wave workgroups);
+// up to one row per CU takes W = 16, so a lane transforms a quarter of the
+// groups with four waves per SIMD issuing (one row of width 14336: 13.0 ->
+// 8.6 us; at two rows per CU the 16-wave workgroups no longer gain).
+#include <atomic>
+
 #include "w8a8_device.h"
 #include "w8a8_host.h"
 
 namespace w8a8 {
 
-constexpr int kSwigluMaxPasses = 4;  // register-resident up to width 16384
+constexpr int kSwigluMaxPasses = 4;  // register-resident up to width 16384 (W = 4)
 
 template <int DT>
 constexpr int sw_bytes() { return DT == kF32 ? 4 : 2; }
 
-// P > 0: the row's rotated values stay in registers (P passes of 16 groups).
-// P == 0: streaming, the row is transformed twice (maximum, then quantize).
-template <int DT, int P>
-__global__ __launch_bounds__(256) void swiglu_quant_kernel(
+// Dynamic LDS of a W-wave workgroup: the rotation slots, then the waves'
+// maxima.
+template <int W>
+constexpr int swiglu_lds_bytes() { return (W * kRotWave + W) * 4; }
+
+// P > 0: the row's rotated values stay in registers (P passes of 4 W
+// groups). P == 0: streaming, the row is transformed twice (maximum, then
+// quantize).
+template <int DT, int P, int W>
+__global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t width,
     const float* __restrict__ row_max_in, float* __restrict__ row_max_out,
     float* __restrict__ group_max, int8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale) {
-  constexpr int kWaves = 4, kSlots = 4 * kWaves;
-  __shared__ float lds[kWaves * kRotWave];
-  __shared__ float wmax[kWaves];
+  constexpr int kWaves = W, kSlots = 4 * kWaves;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* const lds = smem;
+  float* const wmax = smem + kWaves * kRotWave;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const int groups = (int)(width >> 8);
@@ -114,14 +126,14 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(
   }
 }
 
-template <int DT>
-static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
+template <int DT, int W>
+static void launch_swiglu_w(const W8A8SwigluArgs* a, hipStream_t stream) {
   const int groups = (int)(a->width >> 8);
-  const int passes = (groups + 15) / 16;
-  const dim3 grid((unsigned)a->rows), block(256);
-#define W8A8_SLAUNCH(PP)                                                                     \
-  hipLaunchKernelGGL((swiglu_quant_kernel<DT, PP>), grid, block, 0, stream, a->x, a->ldx,     \
-                     a->rows, a->width, a->row_max, a->row_max_out, a->group_max, a->q, a->ldq, \
+  const int passes = (groups + 4 * W - 1) / (4 * W);
+  const dim3 grid((unsigned)a->rows), block(64 * W);
+#define W8A8_SLAUNCH(PP)                                                                                 \
+  hipLaunchKernelGGL((swiglu_quant_kernel<DT, PP, W>), grid, block, swiglu_lds_bytes<W>(), stream, a->x, \
+                     a->ldx, a->rows, a->width, a->row_max, a->row_max_out, a->group_max, a->q, a->ldq,  \
                      a->scale)
   switch (passes) {
     case 1: W8A8_SLAUNCH(1); break;
@@ -132,6 +144,46 @@ static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
   }
 #undef W8A8_SLAUNCH
   static_assert(kSwigluMaxPasses == 4, "dispatch covers P = 1..4");
+}
+
+// The 16-wave variants' LDS exceeds the 64 KB default: raise their limit once
+// per device.
+template <int DT>
+static int enable_wide_swiglu(int dev) {
+  static std::atomic<uint64_t> done{0};
+  const uint64_t bit = 1ull << dev;
+  if (done.load(std::memory_order_acquire) & bit) return W8A8_OK;
+  const void* fns[] = {reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 0, 16>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 1, 16>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 2, 16>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 3, 16>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 4, 16>)};
+  for (const void* f : fns) {
+    const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, swiglu_lds_bytes<16>());
+    if (e != hipSuccess) {
+      set_error("w8a8_swiglu_quantize: cannot enable %d bytes of LDS: %s", swiglu_lds_bytes<16>(),
+                hipGetErrorString(e));
+      return W8A8_ERR_LAUNCH;
+    }
+  }
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return W8A8_OK;
+}
+
+template <int DT>
+static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error("w8a8_swiglu_quantize: hipGetDevice failed");
+    return W8A8_ERR_LAUNCH;
+  }
+  if (a->rows <= (int64_t)device_cus(dev)) {
+    const int rc = enable_wide_swiglu<DT>(dev);
+    if (rc != W8A8_OK) return rc;
+    launch_swiglu_w<DT, 16>(a, stream);
+  } else {
+    launch_swiglu_w<DT, 4>(a, stream);
+  }
   return launch_status("w8a8_swiglu_quantize");
 }
 
