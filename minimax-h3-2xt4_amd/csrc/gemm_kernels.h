@@ -1451,7 +1451,11 @@ __global__ __launch_bounds__(256) void dequant_kernel(GemmParams p, const int32_
 }
 
 // Split-K finish: thread -> 4 consecutive columns of one row; adds the
-// ksplit int32 partial tiles (exact), then the shared epilogue.
+// ksplit int32 partial tiles (exact), then the shared epilogue. Every plan
+// splits K at most kMaxSplit ways; the planes' loads are all issued before
+// the first add, so their latencies overlap instead of adding up.
+constexpr int kMaxSplit = 8;
+
 template <int EPI, int OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, const int32_t* __restrict__ ws,
                                                             int ksplit, int64_t stride) {
@@ -1463,7 +1467,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, const 
   const int valid = min(4, p.n - n);
   const int32_t* src = ws + (int64_t)m * p.n + n;
   int c[4] = {0, 0, 0, 0};
-  if (valid == 4 && (p.n & 3) == 0) {
+  if (valid == 4 && (p.n & 3) == 0 && ksplit <= kMaxSplit) {
+    int4 v[kMaxSplit];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp)
+      v[sp] = sp < ksplit ? *reinterpret_cast<const int4*>(src + sp * stride) : make_int4(0, 0, 0, 0);
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp) {
+      c[0] += v[sp].x; c[1] += v[sp].y; c[2] += v[sp].z; c[3] += v[sp].w;
+    }
+  } else if (valid == 4 && (p.n & 3) == 0) {
     for (int sp = 0; sp < ksplit; ++sp) {
       const int4 v = *reinterpret_cast<const int4*>(src + sp * stride);
       c[0] += v.x; c[1] += v.y; c[2] += v.z; c[3] += v.w;
