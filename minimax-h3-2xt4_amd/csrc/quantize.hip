@@ -168,9 +168,13 @@ __global__ __launch_bounds__(64 * W) void quantize_row_wg_kernel(
 
 template <int DT, int ROT>
 static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
-  // Below 1024 rows a wavefront per row leaves most of the GPU idle: spread
-  // each row over a workgroup (up to 16384 columns).
-  if (a->rows < 1024 && a->cols <= 16384) {
+  // Below 2048 rows a wavefront per row leaves most of the GPU idle, and
+  // rows wider than 4096 columns hold too many registers per wave (or, past
+  // 8192, read the row twice): spread each row over a workgroup (up to 16384
+  // columns). Timed on one box: 1024 x 3072 7.5 -> 5.6 us, 4096 x 8192
+  // 34.2 -> 25.6 us, 1024 x 14336 36.6 -> 14.4 us; 4096 x 3072 stays on a
+  // wavefront per row (12.6 against 17.1 us).
+  if (a->cols <= 16384 && (a->rows < 2048 || (a->cols > 4096 && a->rows < 8192))) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
       set_error("w8a8_quantize_rows: hipGetDevice failed");

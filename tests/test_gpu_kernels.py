@@ -393,8 +393,11 @@ QUANT_CASES = [
     (1, 16, False), (7, 3072, False), (33, 4096, False), (5, 5120, False), (9, 8192, False),
     (3, 16384, False), (2, 2064, False),
     (1, 256, True), (7, 3072, True), (33, 4096, True), (4, 8192, True), (3, 12800, True), (2, 16384, True),
-    # >= 1024 rows: one wavefront per row (registers, then the streaming path past 8192 columns)
+    # 1024..2047 rows: a 4-wave workgroup per row
     (1100, 512, False), (1030, 3072, True), (1024, 9216, False), (1050, 12800, True),
+    # one wavefront per row: 2048 rows or more up to 4096 columns, 8192 rows or more past that (registers),
+    # and rows wider than 16384 columns (the streaming path, each row read twice)
+    (2100, 512, False), (2050, 3072, True), (8200, 4352, False), (2100, 16400, False),
 ]
 
 
