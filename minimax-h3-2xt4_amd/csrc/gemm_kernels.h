@@ -235,8 +235,8 @@ __device__ __forceinline__ int readout_col(int nw, int h, int lane) {
 
 // Staged epilogue of one 128 x 32 NB quadrant (NB = 4, 3 or 2) through an
 // 8 KB wave-private LDS slice, in passes of 32 rows x 64 columns (8, or 4
-// for NB = 2). Each pass writes the raw int32
-// accumulators into the slice (16-byte chunks XOR-swizzled by row), then
+// for NB = 2). Each pass writes the raw int32 accumulators into the slice
+// (16-byte chunks XOR-swizzled by row), then
 // each lane reads CPL consecutive columns of one row back, dequantizes them
 // in the reference's order (ROW (C*a)*w, COLUMN C*(a*w), then + bias, then
 // the cast), adds the FP16 residual read with the same coalesced pattern
@@ -260,6 +260,38 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
   constexpr bool has_gate = (FLAGS & kWithGate) != 0;
   const int fr = lane & 31, fh = lane >> 5;
   const int orow = lane / R::LPR, ocol = (lane % R::LPR) * R::CPL;
+  // The FP16 residual rows of pass `pass` (this lane's read-out columns).
+  // Without the gate, pass + 1's rows are loaded while pass is dequantized,
+  // so their latency is hidden; the gate variants have no registers to spare
+  // for a second set and load each pass's rows at its start.
+  auto load_res = [&](int pass, uint4 (&rr)[R::ITERS]) {
+    const int mb = pass >> 1, h = pass & 1;
+    const int mrow = mw + mb * 32;
+    const int ncol = nw + 64 * h + ocol;
+    const bool in_quad = NB != 3 || h == 0 || ocol < 32;
+    const bool full_cols = INTERIOR || (p.vec16 && ncol + R::CPL <= p.n);
+#pragma unroll
+    for (int it = 0; it < R::ITERS; ++it) {
+      const int m = mrow + it * R::RPI + orow;
+      const uint16_t* r = p.residual + (int64_t)m * p.ldr + ncol;
+      if (!in_quad) {
+        rr[it] = make_uint4(0, 0, 0, 0);
+      } else if (INTERIOR || (m < p.m && full_cols)) {
+        rr[it] = *reinterpret_cast<const uint4*>(r);
+      } else {
+        uint32_t w[4] = {0, 0, 0, 0};
+        if (m < p.m) {
+#pragma unroll
+          for (int j = 0; j < R::CPL; ++j)
+            if (ncol + j < p.n) w[j >> 1] |= (uint32_t)r[j] << (16 * (j & 1));
+        }
+        rr[it] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  };
+  constexpr bool kResAhead = has_res && !has_gate;
+  uint4 rbuf[2][R::ITERS];
+  if constexpr (kResAhead) load_res(0, rbuf[0]);
 #pragma unroll
   for (int pass = 0; pass < 8; ++pass) {
     const int mb = pass >> 1, h = pass & 1;
@@ -273,27 +305,16 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     // INTERIOR: every row and column of the quadrant is inside the output
     // and rows are 16-byte aligned, so no store needs a mask.
     const bool full_cols = INTERIOR || (p.vec16 && ncol + R::CPL <= p.n);
-    uint4 rres[R::ITERS];
-    if constexpr (has_res) {
-#pragma unroll
-      for (int it = 0; it < R::ITERS; ++it) {
-        const int m = mrow + it * R::RPI + orow;
-        const uint16_t* r = p.residual + (int64_t)m * p.ldr + ncol;
-        if (!in_quad) {
-          rres[it] = make_uint4(0, 0, 0, 0);
-        } else if (INTERIOR || (m < p.m && full_cols)) {
-          rres[it] = *reinterpret_cast<const uint4*>(r);
-        } else {
-          uint32_t w[4] = {0, 0, 0, 0};
-          if (m < p.m) {
-#pragma unroll
-            for (int j = 0; j < R::CPL; ++j)
-              if (ncol + j < p.n) w[j >> 1] |= (uint32_t)r[j] << (16 * (j & 1));
-          }
-          rres[it] = make_uint4(w[0], w[1], w[2], w[3]);
-        }
-      }
+    // Buffer of pass q: the parity of its index among the passes that run
+    // (NB == 2 runs every other pass).
+    auto buf_of = [](int q) { return NB == 2 ? (q >> 1) & 1 : q & 1; };
+    if constexpr (kResAhead) {
+      const int next = NB == 2 ? pass + 2 : pass + 1;
+      if (next < 8) load_res(next, rbuf[buf_of(next)]);
+    } else if constexpr (has_res) {
+      load_res(pass, rbuf[0]);
     }
+    const uint4 (&rres)[R::ITERS] = rbuf[kResAhead ? buf_of(pass) : 0];
     // Gate values of the lane's columns for each of its rows (the row's
     // table row comes from the lane holding its label in the MFMA layout).
     float gv[R::ITERS][R::CPL];
