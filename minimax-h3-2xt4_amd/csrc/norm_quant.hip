@@ -125,12 +125,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
     }
   };
   auto store_q = [&](int u, const float (&v)[16], float s, float rcp) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = pack4(quant1(v[4 * i], s, rcp), quant1(v[4 * i + 1], s, rcp), quant1(v[4 * i + 2], s, rcp),
-                   quant1(v[4 * i + 3], s, rcp));
-    *reinterpret_cast<uint4*>(p.q + row * p.ldq + (int64_t)u * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(p.q + row * p.ldq + (int64_t)u * 16) = quant16(v, s, rcp);
   };
   // ss + x*x with one rounding: the square of a 16-bit float is exact in
   // fp32 (at most 22 significant bits, no overflow or underflow), so the FMA

@@ -19,10 +19,13 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 __device__ constexpr float kR127 = 1.0f / 127.0f;
 __device__ constexpr float kScaleFloor = 1e-30f;
 __device__ constexpr float kInv16 = 1.0f / 16.0f;
-// Fast-path bound of quant1: |y - rint(y)| below this means the reciprocal
-// product and the IEEE quotient round to the same integer (their distance is
-// below 2^-15 for |y| < 128, the margin here is 2^-12).
-__device__ constexpr float kTieGuard = 0.5f - 1.0f / 4096.0f;
+// Fast-path bound of quant1 / quant16: |y - rint(y)| below this means the
+// reciprocal product y = x * rcp and the IEEE quotient x / s round to the
+// same integer. rcp = 1/s is correctly rounded and the product is rounded
+// once, so |y - x/s| <= |x/s| (2^-23 + 2^-48) < 2^-16 for |x/s| < 128 (every
+// scale here is at least the absmax / 127); a margin of 2^-15 leaves
+// |x/s - rint(y)| < 0.5.
+__device__ constexpr float kTieGuard = 0.5f - 1.0f / 32768.0f;
 
 // ---------------------------------------------------------- conversions
 __device__ __forceinline__ float h2f(uint16_t h) {
@@ -161,9 +164,9 @@ __device__ __forceinline__ float swiglu_fp16_gate(float g, float u) {
 
 // ------------------------------------------------------------- quantizer
 // q = clamp(rne(x / s), -128, 127) with the IEEE quotient x / s.
-// rcp = 1/s (IEEE). The product x*rcp is within 2^-15 of the quotient for
-// |quotient| < 128, so away from half-integers both round to the same
-// integer; near a half-integer (or for NaN / inf) the exact quotient is
+// rcp = 1/s (IEEE). The product x*rcp is within 2^-16 of the quotient for
+// |quotient| < 128 (kTieGuard), so away from half-integers both round to the
+// same integer; near a half-integer (or for NaN / inf) the exact quotient is
 // computed. Beyond |quotient| >= 128 both saturate to the same code (they
 // share the sign, and neither can land on the other side of the clamp).
 __device__ __forceinline__ int quant1(float x, float s, float rcp) {
