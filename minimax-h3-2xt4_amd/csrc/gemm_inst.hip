@@ -26,7 +26,7 @@ int launch_gemm_partials(const GemmParams& p, const GemmPlan& plan, int dev, hip
 int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_bytes) {
   *workspace_bytes = 0;
   if (m <= kSkinnyMaxM) {   // the weight-streaming kernel's own split
-    if (!stream_applies(m, k)) return 1;
+    if (!stream_applies(m, n, k, device_cus(dev))) return 1;
     const int ks = stream_ksplit(n, k, device_cus(dev));
     if (ks > 1) *workspace_bytes = (int64_t)ks * m * n * 4;
     return ks;

@@ -1139,8 +1139,9 @@ void gemm_i8_persistent(GemmParams p) {
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }
 
-// Skinny GEMM for 2 <= M <= 16, and 17 <= M <= 64 where K is not a multiple
-// of 128 (text-encoder short prefill): weight streaming. A workgroup of W
+// Skinny GEMM for 2 <= M <= 64 where K is not a multiple of 128, and for
+// 2 <= M <= 8 where its 16-row grid fills the GPU in one wave (the streaming
+// kernel below takes the rest): weight streaming. A workgroup of W
 // wavefronts owns NR weight rows (NR = 16 with W = 8, or NR = 32 with W = 4
 // when N / 32 still fills the GPU); the waves
 // split K into contiguous ranges and multiply with v_mfma_i32_16x16x64_i8
@@ -1313,14 +1314,12 @@ void launch_skinny(const GemmParams& p, hipStream_t s) {
   }
 }
 
-// Weight streaming for M <= 64 with K a multiple of 128 (text-encoder
+// Weight streaming for 2 <= M <= 64 with K a multiple of 128 (text-encoder
 // decode and short prefill). A workgroup of 4 waves owns 64 weight rows and
-// one of ksplit contiguous K ranges (one workgroup per CU). A step is 128
-// bytes of K: the 64 weight rows and the MB 16-row blocks of activation rows
-// (8 rows per global_load_lds_dwordx4). The workgroup streams its range
-// through one LDS ring of S steps with S - 1 steps in flight, so a CU keeps
-// ~120-140 KB of loads outstanding (the latency of the memory system, not the
-// bandwidth, bounds a shallower ring). Each wave issues a quarter of every
+// one of ksplit contiguous K ranges. A step is 128 bytes of K: the 64
+// weight rows and the MB 16-row blocks of activation rows (8 rows per
+// global_load_lds_dwordx4). The workgroup streams its range through one LDS
+// ring of S steps with S - 1 steps in flight. Each wave issues a quarter of every
 // step's DMA; one barrier per step makes the step visible to all waves and
 // frees the slot read in the step before for the next refill. In each
 // 128-byte row, 16-byte chunk c lands at c ^ ((r >> 1) & 7), so the DMA
@@ -1337,19 +1336,26 @@ constexpr int kStreamRows = 64;      // weight rows per workgroup
 constexpr int kStreamStep = 128;     // K bytes per step
 constexpr int kStreamWaves = 4;
 
+// 48 KB per workgroup, up to three workgroups per CU: 3 slots for MB 1, 3,
+// 4 (16 KB slots), 4 for MB 2 (12 KB). Two steps in flight per workgroup
+// stream as fast as deeper rings at every measured shape, and the shallow
+// ring lets CUs hold more than one workgroup when the grid exceeds the CUs.
+constexpr int kStreamRingBytes = 48 * 1024;
+
 template <int MB>
 struct StreamRing {
   static constexpr int kRows = kStreamRows + 16 * MB;             // weight + activation rows of a step
   static constexpr int kDpw = (kRows / 8 + kStreamWaves - 1) / kStreamWaves;   // DMA per wave and step
   static constexpr int kSlot = 8 * kStreamWaves * kDpw * kStreamStep;          // padded to whole DMA groups
-  static constexpr int kSlots = (160 * 1024) / kSlot;             // 13 (MB 1, 2), 10 (MB 3, 4)
-  static constexpr int kLds = kSlots * kSlot;                     // 156, 156, 160, 160 KB
+  static constexpr int kSlots = kStreamRingBytes / kSlot;
+  static constexpr int kLds = kSlots * kSlot;
 };
 
 template <int EPI, int OUT, int MB, bool PARTIAL>
 __global__ __launch_bounds__(kStreamWaves * 64) void gemm_i8_stream(GemmParams p, int nblocks, int ksplit) {
   using R = StreamRing<MB>;
-  static_assert(R::kLds <= 160 * 1024 && (R::kSlots - 2) * R::kDpw < 64, "LDS and vmcnt range");
+  static_assert(R::kLds <= kStreamRingBytes && R::kSlots >= 3 && (R::kSlots - 2) * R::kDpw < 64,
+                "LDS and vmcnt range");
   extern __shared__ __attribute__((aligned(16))) int8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1438,19 +1444,24 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_i8_stream(GemmParams p
   }
 }
 
-// Shapes the streaming kernel takes: 17..64 rows (single 16-row blocks
-// stream faster through the register-batched kernel below, which needs no
-// split-K finish) and whole 128-byte K steps.
-inline bool stream_applies(int64_t m, int64_t k) {
-  return m > 16 && m <= kSkinnyMaxM && k >= kStreamStep && k % kStreamStep == 0;
+// Shapes the streaming kernel takes: 2..64 rows and whole 128-byte K steps,
+// except up to 8 rows where the register-batched kernel's grid of 16-row
+// workgroups fills more than half of the CUs in a single wave (N = 3072 and
+// 4096 on 256 CUs): there it finishes first, with no split-K partials.
+inline bool stream_applies(int64_t m, int64_t n, int64_t k, int cus) {
+  if (m < 2 || m > kSkinnyMaxM || k < kStreamStep || k % kStreamStep != 0) return false;
+  const int64_t skinny_wgs = (n + 15) / 16;
+  return !(m <= 8 && 2 * skinny_wgs > cus && skinny_wgs <= cus);
 }
 
 // K split of the streaming kernel: the largest power of two up to 8 that
-// keeps one workgroup per CU and at least eight steps per workgroup.
+// keeps at most 4/3 workgroups per CU and at least four steps per
+// workgroup. Measured at M = 2..64: more workgroups than that lose more to
+// the split-K finish than they gain, fewer leave CUs idle.
 inline int stream_ksplit(int64_t n, int64_t k, int cus) {
   const int64_t nblocks = (n + kStreamRows - 1) / kStreamRows, steps = k / kStreamStep;
   int ks = 1;
-  while (ks < 8 && nblocks * ks * 2 <= cus && steps / (ks * 2) >= 8) ks *= 2;
+  while (ks < 8 && nblocks * ks * 2 * 3 <= 4 * (int64_t)cus && steps / (ks * 2) >= 4) ks *= 2;
   return ks;
 }
 
@@ -1563,31 +1574,16 @@ int launch_persistent_nb(const GemmParams& p, const GemmPlan& plan, int dev, hip
 }
 
 template <int EPI, int OUT, int MB>
-int launch_stream(const GemmParams& p, int ksplit, int dev, hipStream_t s) {
-  // The ring exceeds the 64 KB default: raise both variants' dynamic LDS
-  // limit once per device.
-  static DeviceOnce lds_enabled;
-  const uint64_t bit = 1ull << dev;
-  if (!(lds_enabled.done.load(std::memory_order_acquire) & bit)) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_stream<EPI, OUT, MB, false>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, StreamRing<MB>::kLds);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_stream<EPI, OUT, MB, true>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, StreamRing<MB>::kLds);
-    if (e != hipSuccess) {
-      set_error("w8a8_gemm: cannot enable %d bytes of LDS: %s", StreamRing<MB>::kLds, hipGetErrorString(e));
-      return W8A8_ERR_LAUNCH;
-    }
-    lds_enabled.done.fetch_or(bit, std::memory_order_acq_rel);
-  }
+int launch_stream(const GemmParams& p, int ksplit, hipStream_t s) {
+  using R = StreamRing<MB>;
+  static_assert(R::kLds <= 64 * 1024, "the ring fits the default dynamic LDS limit");
   const int nblocks = (p.n + kStreamRows - 1) / kStreamRows;
   const dim3 grid((unsigned)(nblocks * ksplit)), block(kStreamWaves * 64);
   if (ksplit == 1) {
-    hipLaunchKernelGGL((gemm_i8_stream<EPI, OUT, MB, false>), grid, block, StreamRing<MB>::kLds, s, p, nblocks, 1);
+    hipLaunchKernelGGL((gemm_i8_stream<EPI, OUT, MB, false>), grid, block, R::kLds, s, p, nblocks, 1);
     return W8A8_OK;
   }
-  hipLaunchKernelGGL((gemm_i8_stream<EPI, OUT, MB, true>), grid, block, StreamRing<MB>::kLds, s, p, nblocks,
-                     ksplit);
+  hipLaunchKernelGGL((gemm_i8_stream<EPI, OUT, MB, true>), grid, block, R::kLds, s, p, nblocks, ksplit);
   const int64_t threads = (int64_t)p.m * ((p.n + 3) / 4);
   hipLaunchKernelGGL((splitk_reduce_kernel<EPI, OUT>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, p,
                      reinterpret_cast<const int32_t*>(p.ws), ksplit, (int64_t)p.m * p.n);
@@ -1603,16 +1599,20 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
     launch_gemv<EPI, OUT>(p, device_cus(dev), s);
     return W8A8_OK;
   }
-  if (stream_applies(p.m, p.k)) {
+  if (p.m <= kSkinnyMaxM) {
     int dev = 0;
     const int rc = current_device(dev);
     if (rc != W8A8_OK) return rc;
-    int ks = stream_ksplit(p.n, p.k, device_cus(dev));
-    if (ks > 1 && (p.ws == nullptr || p.ws_bytes < (int64_t)ks * p.m * p.n * 4)) ks = 1;
-    switch ((p.m + 15) / 16) {
-      case 2: return launch_stream<EPI, OUT, 2>(p, ks, dev, s);
-      case 3: return launch_stream<EPI, OUT, 3>(p, ks, dev, s);
-      default: return launch_stream<EPI, OUT, 4>(p, ks, dev, s);
+    const int cus = device_cus(dev);
+    if (stream_applies(p.m, p.n, p.k, cus)) {
+      int ks = stream_ksplit(p.n, p.k, cus);
+      if (ks > 1 && (p.ws == nullptr || p.ws_bytes < (int64_t)ks * p.m * p.n * 4)) ks = 1;
+      switch ((p.m + 15) / 16) {
+        case 1: return launch_stream<EPI, OUT, 1>(p, ks, s);
+        case 2: return launch_stream<EPI, OUT, 2>(p, ks, s);
+        case 3: return launch_stream<EPI, OUT, 3>(p, ks, s);
+        default: return launch_stream<EPI, OUT, 4>(p, ks, s);
+      }
     }
   }
   if (p.m <= kSkinnyMaxM && p.k % 64 == 0) {

@@ -22,7 +22,11 @@ GEMM_SHAPES = [(1, 16, 16), (13, 48, 64), (64, 64, 128), (256, 256, 64), (300, 5
                # weight-streaming (M <= 64) shapes: text-encoder up/down, ragged N
                (1, 14336, 4096), (64, 4096, 14336), (37, 1000, 1024), (5, 520, 192), (65, 4096, 512),
                # 64 weight rows per workgroup (M 49..64, N >= 12288), ragged last workgroup
-               (64, 14336, 4096), (50, 12352, 256)]
+               (64, 14336, 4096), (50, 12352, 256),
+               # up to 8 rows: the register-batched kernel where its 16-row grid fills 128..256 CUs
+               # (N = 4000), the streaming kernel elsewhere (one 16-row block; N = 16 below one
+               # 64-row block, N = 5000 past the CUs)
+               (6, 4000, 1024), (2, 16, 128), (8, 5000, 1024)]
 
 
 @pytest.mark.parametrize('m,n,k', GEMM_SHAPES)
@@ -155,10 +159,17 @@ def test_gemv_extremes(gpu):
 
 
 STREAM_CASES = [
-    # (m, n, k): 16 < M <= 64 with K % 128 == 0 takes the weight-streaming kernel.
-    # These split K (two or four workgroups per 64-row block, partials in
-    # the workspace) unless the workspace is withheld; ragged N and M.
-    (20, 4096, 14336), (64, 4100, 4096), (17, 203, 14336), (49, 4096, 14336),
+    # (m, n, k): 2 <= M <= 64 with K % 128 == 0 takes the weight-streaming kernel
+    # (up to 8 rows only where the register-batched kernel's grid would not fill the CUs).
+    # On 256 CUs these split K two (40 x 10750: 168 row blocks of 64), four
+    # (64 x 4100 and the text-encoder down shapes) or eight ways (17 x 203,
+    # 33 x 512 x 5120: five steps per workgroup), partials in the workspace,
+    # unless the workspace is withheld; ragged N and M. 33 x 20500 x 640 has
+    # more row blocks (321) than CUs and does not split.
+    (20, 4096, 14336), (64, 4100, 4096), (17, 203, 14336), (49, 4096, 14336), (40, 10750, 1024),
+    (33, 512, 5120), (33, 20500, 640),
+    # one 16-row activation block: 3 rows (K split two ways), 12 rows (four ways, ragged N)
+    (3, 5120, 1280), (12, 4000, 2048),
 ]
 
 
@@ -172,7 +183,7 @@ def test_gemm_stream_split_and_whole(gpu, m, n, k):
     ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
     bias = (torch.randn((n,), generator=g) * 0.01).half()
     res = randn16(g, (m, n), 1 / 512)
-    assert kernels.gemm_workspace_bytes(m, n, k, gpu) > 0        # the default call splits K
+    assert (kernels.gemm_workspace_bytes(m, n, k, gpu) > 0) == (n <= 16384)   # the default call splits K
     acc = o.int_mm(np_of(a), np_of(b))
     ag, bg = a.to(gpu), b.to(gpu)
     none = torch.empty(0, dtype=torch.uint8, device=gpu)
