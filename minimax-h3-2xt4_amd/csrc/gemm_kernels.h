@@ -1336,9 +1336,10 @@ constexpr int kStreamRows = 64;      // weight rows per workgroup
 constexpr int kStreamStep = 128;     // K bytes per step
 constexpr int kStreamWaves = 4;
 
-// 48 KB per workgroup, up to three workgroups per CU: 3 slots for MB 1, 3,
-// 4 (16 KB slots), 4 for MB 2 (12 KB). Two steps in flight per workgroup
-// stream as fast as deeper rings at every measured shape, and the shallow
+// 48 KB per workgroup, up to three workgroups per CU: 3 slots for MB 3, 4
+// (16 KB slots), 4 for MB 1, 2 (12 KB). Two or three steps in flight per
+// workgroup stream as fast as deeper rings at every measured shape (a sweep
+// of 48 to 120 KB rings at M = 17..64), and the shallow
 // ring lets CUs hold more than one workgroup when the grid exceeds the CUs.
 constexpr int kStreamRingBytes = 48 * 1024;
 
