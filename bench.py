@@ -9,12 +9,16 @@ M=16384 tokens, hidden 3072, FFN 8192:
      weight scale and the FP16 residual add
 Inputs and weights are seeded synthetic tensors already resident in HBM.
 
-  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline]
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline] [--no-other-configs]
 
 Prints one JSON line: INT8 TOPS of the whole block, ms per step, the
 roofline of the dominant kernel (the FC1 GEMM, timed with HIP events on the
 launch stream), per-kernel times, and the CPU oracle timed on a bounded row
-sample of the same workload on this host.
+sample of the same workload on this host. The default run then appends the
+other configurations' figures to the same line under "other_configs" (the
+W8A8 linear 4096x3072x3072, the DiT QKV projection at 53504 rows, the
+text-encoder skinny projections and the half-shard block projections at
+204336 rows), timed with fewer steps after the block's timed steps.
 """
 import argparse
 import json
@@ -1002,6 +1006,37 @@ def run_reference_shapes(args, torch, dev):
                 'weights quantized per channel)', config=dict(workload='reference_shapes'), shapes=rows)
 
 
+def _compact(name, res):
+    """The figures of one config's result worth carrying on the default line."""
+    keep = {k: res[k] for k in ('metric', 'value', 'unit', 'us', 'ms') if k in res}
+    if 'kernels' in res:
+        keep['kernels'] = res['kernels']
+    if name == 'te_skinny':
+        keep['lines'] = [{k: l[k] for k in ('m', 'proj', 'gemm_us', 'gemm_frac')} for l in res['lines']]
+    return keep
+
+
+# The other configurations, run after the default workload with fewer steps
+# and no CPU baseline so that one default run records every configuration.
+OTHER_CONFIGS = (('c0', 'w8a8_linear'), ('c2', 'dit_qkv'), ('c3', 'te_skinny'), ('c4', 'dit_half_shard'))
+
+
+def run_other_configs(args, torch, dev):
+    sub = argparse.Namespace(**{**vars(args), 'steps': min(args.steps, 20), 'warmup': min(args.warmup, 5),
+                                'no_cpu_baseline': True})
+    out = {}
+    for tag, name in OTHER_CONFIGS:
+        t0 = time.time()
+        try:
+            out[tag] = _compact(name, WORKLOADS[name](sub, torch, dev))
+        except Exception as e:   # a failing secondary config must not cost the default line
+            out[tag] = dict(error=f'{type(e).__name__}: {e}')
+        out[tag]['workload'] = name
+        out[tag]['wall_s'] = round(time.time() - t0, 1)
+        torch.cuda.empty_cache()
+    return out
+
+
 WORKLOADS = {'dit_ffn': run_dit_ffn, 'dit_attention': run_dit_attention, 'dit_attention_block': run_dit_attention_block, 'dit_norm': run_dit_norm, 'dit_rms_rope': run_dit_rms_rope, 'copy': run_copy,
              'w8a8_linear': run_w8a8_linear, 'dit_qkv': run_dit_qkv, 'dit_qkv_rope': run_dit_qkv_rope,
              'te_skinny': run_te_skinny, 'dit_half_shard': run_dit_half_shard,
@@ -1015,6 +1050,8 @@ def main():
     ap.add_argument('--warmup', type=int, default=10)
     ap.add_argument('--workload', default='dit_ffn', choices=sorted(WORKLOADS))
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--no-other-configs', action='store_true',
+                    help='default workload only: skip the c0/c2/c3/c4 figures appended to its line')
     ap.add_argument('--cpu-rows', type=int, default=4096)
     ap.add_argument('--seconds', type=float, default=4.0, help='gemm_power: sustained seconds per case')
     args = ap.parse_args()
@@ -1030,6 +1067,8 @@ def main():
     from w8a8 import _abi
     _abi.load()
     result = WORKLOADS[args.workload](args, torch, dev)
+    if args.workload == 'dit_ffn' and not args.no_other_configs:
+        result['other_configs'] = run_other_configs(args, torch, dev)
     print(json.dumps(result), flush=True)
 
 
