@@ -38,6 +38,43 @@ def test_gemm_int32_exact(gpu, m, n, k):
     assert_bits_equal(np_of(got), o.int_mm(np_of(a), np_of(b)), f'gemm {m}x{n}x{k}')
 
 
+def _dispatch_sweep_shapes(count=48, seed=2024):
+    """Seeded shapes spread over every kernel choice of the GEMM dispatch:
+    M = 1 (GEMV), 2..8 and 9..16 (register-batched or weight-streaming by N),
+    17..64 (weight streaming, split K or not), 65..3000 (persistent tiles of
+    each shape, split K or not), ragged N from one partial tile to past the
+    CU count in 64-row blocks, and K from 16 (multiples of 16, 64, 128, 256)."""
+    rng = np.random.default_rng(seed)
+    shapes = []
+    while len(shapes) < count:
+        m = int(rng.choice([1, rng.integers(2, 9), rng.integers(9, 17), rng.integers(17, 65),
+                            rng.integers(65, 701), rng.integers(701, 3001)]))
+        n = int(rng.choice([rng.integers(1, 600), rng.integers(2049, 4097), rng.integers(4097, 22000)]))
+        k = int(rng.choice([16, 64, 128, 256]) * rng.integers(1, 48))
+        if m * n * k <= 4e9:
+            shapes.append((m, n, k))
+    return shapes
+
+
+@pytest.mark.parametrize('m,n,k', _dispatch_sweep_shapes())
+def test_gemm_dispatch_sweep(gpu, m, n, k):
+    print(f'sweep gemm {m}x{n}x{k}', flush=True)
+    g = torch.Generator().manual_seed(m * 131 + n * 17 + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    acc = o.int_mm(np_of(a), np_of(b))
+    ag, bg = a.to(gpu), b.to(gpu)
+    assert_bits_equal(np_of(kernels.gemm(ag, bg)), acc, f'int32 {m}x{n}x{k}')
+    rs = torch.rand((m, 1), generator=g) * 0.01 + 1e-4
+    ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
+    want = o.dequantize_row(acc, np_of(rs), np_of(ws), 'f16')
+    none = torch.empty(0, dtype=torch.uint8, device=gpu)
+    for workspace in (None, none):     # the split the shape plans, and unsplit
+        got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                           out_dtype=torch.float16, workspace=workspace)
+        assert_bits_equal(np_of(got), want, f'row f16 {m}x{n}x{k} ws={workspace is None}')
+
+
 def test_gemm_signed_extremes_and_layout(gpu):
     k = 5120
     a = torch.full((33, k), -128, dtype=torch.int8)
