@@ -1325,11 +1325,15 @@ void launch_skinny(const GemmParams& p, hipStream_t s) {
 // 128-byte row, 16-byte chunk c lands at c ^ ((r >> 1) & 7), so the DMA
 // writes and the fragment reads are free of bank conflicts. Every load of
 // the loop is an LDS DMA, and every iteration issues the same number of them
-// (past the range's end the last step is loaded again into the freed slot,
-// which is never read), so the counted waits are exact. Wave w multiplies
-// weight rows 16 w .. 16 w + 15 with every activation block
-// (v_mfma_i32_16x16x64_i8, two 64-byte sub-steps per step) and finishes its
-// own outputs: with ksplit == 1 the shared epilogue writes them, otherwise
+// (past the range's end the walk's last step is loaded again into the freed slot,
+// which is never read), so the counted waits are exact. With four
+// activation blocks (M 49..64) wave w multiplies a 32 x 32 block, weight rows
+// 32 (w >> 1) .. + 31 with activation rows 32 (w & 1) .. + 31: four fragment
+// reads per four MFMAs instead of five, which the LDS read rate rewards
+// (64 x 14336 x 4096 16.0 -> 14.1 us). With fewer blocks wave w multiplies
+// weight rows 16 w .. 16 w + 15 with every activation block. The MFMA is
+// v_mfma_i32_16x16x64_i8, two 64-byte sub-steps per step. Each wave finishes
+// its own outputs: with ksplit == 1 the shared epilogue writes them, otherwise
 // plane ks of the caller's workspace receives the int32 sums and
 // splitk_reduce_kernel finishes.
 constexpr int kStreamRows = 64;      // weight rows per workgroup
@@ -1382,13 +1386,25 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_i8_stream(GemmParams p
                  : p.b + (int64_t)min(n0 + (r < kStreamRows ? r : 0), p.n - 1) * p.ldb + c * 16;
   }
   const int fr = lane & 15, fc = lane >> 4;
+  // MB == 4: wave w takes weight rows 32 (w >> 1) .. + 31 against activation
+  // rows 32 (w & 1) .. + 31 (2 x 2 blocks); otherwise weight rows 16 w .. +15
+  // against every activation block.
+  constexpr bool kQuad = MB == 4;
+  const int wi = wave >> 1, wj = wave & 1;
   v4i acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = v4i{0, 0, 0, 0};
 
   if (nsteps > 0) {
+    // Workgroup nblk walks its K range starting at step nblk % nsteps and
+    // wraps around (integer sums do not depend on the order), so the
+    // workgroups of one K range read different columns of their rows at any
+    // moment instead of all the same one: 64 x 4096 x 14336 15.8 -> 14.5 us.
+    const int rot = nblk % nsteps;
     auto dma_step = [&](int t, int slot) {
-      const int64_t kof = (int64_t)(g0 + min(t, nsteps - 1)) * kStreamStep;
+      int u = min(t, nsteps - 1) + rot;
+      u = u >= nsteps ? u - nsteps : u;
+      const int64_t kof = (int64_t)(g0 + u) * kStreamStep;
 #pragma unroll
       for (int i = 0; i < R::kDpw; ++i)
         dma16(src[i] + kof, lds + slot * R::kSlot + (R::kDpw * wave + i) * 1024);
@@ -1410,29 +1426,49 @@ __global__ __launch_bounds__(kStreamWaves * 64) void gemm_i8_stream(GemmParams p
       wait_vmcnt<(R::kSlots - 2) * R::kDpw>();
       block_barrier();
       dma_step(t + R::kSlots - 1, refill);
-      v4i w[2], x[2][MB];
+      if constexpr (kQuad) {
+        v4i w[2][2], x[2][2];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        w[j] = frag(slot, 16 * wave, j);
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) x[j][mb] = frag(slot, kStreamRows + mb * 16, j);
+          for (int h = 0; h < 2; ++h) {
+            w[j][h] = frag(slot, 32 * wi + 16 * h, j);
+            x[j][h] = frag(slot, kStreamRows + 32 * wj + 16 * h, j);
+          }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+              acc[2 * a + b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j][a], x[j][b], acc[2 * a + b], 0, 0, 0);
+      } else {
+        v4i w[2], x[2][MB];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          w[j] = frag(slot, 16 * wave, j);
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) x[j][mb] = frag(slot, kStreamRows + mb * 16, j);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], x[j][mb], acc[mb], 0, 0, 0);
       }
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[j], x[j][mb], acc[mb], 0, 0, 0);
       refill = slot;
       slot = slot + 1 == R::kSlots ? 0 : slot + 1;
     }
   }
   wait_vmcnt<0>();   // no DMA may still target the ring at exit
-  // Lane holds C[m][n .. n + 3] for m = 16 mb + fr, n = n0 + 16 wave + 4 fc.
-  const int n = n0 + 16 * wave + 4 * fc;
-  const int valid = min(4, p.n - n);
-  if (valid <= 0) return;
+  // Lane holds C[m][n .. n + 3] for m = 16 mb + fr, n = n0 + 16 wave + 4 fc
+  // (MB == 4: block 2 a + b holds m = 32 wj + 16 b + fr, n = n0 + 32 wi +
+  // 16 a + 4 fc).
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
-    const int m = 16 * mb + fr;
+    const int n = kQuad ? n0 + 32 * wi + 16 * (mb >> 1) + 4 * fc : n0 + 16 * wave + 4 * fc;
+    const int valid = min(4, p.n - n);
+    if (valid <= 0) continue;
+    const int m = kQuad ? 32 * wj + 16 * (mb & 1) + fr : 16 * mb + fr;
     if (m >= p.m) continue;
     const int c[4] = {acc[mb][0], acc[mb][1], acc[mb][2], acc[mb][3]};
     if constexpr (PARTIAL) {
