@@ -86,12 +86,46 @@ __device__ __forceinline__ void modulate16(float (&v)[16], uint32_t (&bits)[8], 
   }
 }
 
-template <int DT, int MODE, int J, int TB>
-__global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
+// Waves per workgroup of the norm-only kernel with AdaLN tables: the
+// workgroup stages the gain and its first row's shift and scale rows in LDS,
+// and its waves whose row carries that label read them there (the rows of a
+// segment share the label). 16384 x 3072: 55 -> 41 us. With the rotation the
+// tables' LDS costs more occupancy than the loads they save (61 -> 73 us).
+constexpr int kNormStageWaves = 8;
+constexpr int kNormStageMaxCols = 4096;   // 48 KB of tables
+
+// Dynamic LDS of a W-wave workgroup: the rotation slots, then (STAGE) the
+// gain, scale and shift rows.
+template <int MODE, int W, bool STAGE>
+constexpr int norm_lds_floats(int cols) { return (rot_of<MODE>() ? W * kRotWave : 0) + (STAGE ? 3 * cols : 0); }
+
+template <int DT, int MODE, int J, int TB, int W = kNormWaves, bool STAGE = false>
+__global__ __launch_bounds__(64 * W) void norm_quant_kernel(NormParams p) {
   constexpr int ROT = rot_of<MODE>();
-  __shared__ float lds[ROT ? kNormWaves * kRotWave : 1];
+  static_assert(!STAGE || (TB == (kGain | kMod) && ROT == 0), "staged tables: norm-only DiT form");
+  extern __shared__ __attribute__((aligned(16))) float dsm[];
+  float* const lds = dsm;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kNormWaves + wave;
+  const int64_t row0 = (int64_t)blockIdx.x * W;
+  const int64_t row = row0 + wave;
+  float* const tw = dsm + (ROT ? W * kRotWave : 0);
+  float* const tsc = tw + p.cols;
+  float* const tsh = tsc + p.cols;
+  int l0 = -1;
+  if constexpr (STAGE) {
+    // Every thread reaches the barrier before any row bound is applied.
+    l0 = min(max(p.labels[row0], 0), p.mod_rows - 1);
+    const float4* gw = reinterpret_cast<const float4*>(p.weight);
+    const float4* gsc = reinterpret_cast<const float4*>(p.mscale + (int64_t)l0 * p.ld_mod);
+    const float4* gsh = reinterpret_cast<const float4*>(p.shift + (int64_t)l0 * p.ld_mod);
+    const int n4 = (int)(p.cols >> 2);
+    for (int i = threadIdx.x; i < n4; i += 64 * W) {
+      reinterpret_cast<float4*>(tw)[i] = gw[i];
+      reinterpret_cast<float4*>(tsc)[i] = gsc[i];
+      reinterpret_cast<float4*>(tsh)[i] = gsh[i];
+    }
+    __syncthreads();
+  }
   if (row >= p.rows) return;
   const int units = (int)(p.cols >> 4);
   const int jcount = (units + 63) >> 6;
@@ -99,8 +133,10 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
   uint16_t* yrow = p.y ? reinterpret_cast<uint16_t*>(p.y) + row * p.ldy : nullptr;
   const float* sh = nullptr;
   const float* sc = nullptr;
+  bool staged = false;
   if ((TB & kMod) || ((TB & kAnyTables) && p.shift)) {
     const int l = min(max(p.labels[row], 0), p.mod_rows - 1);
+    staged = STAGE && l == l0;
     sh = p.shift + (int64_t)l * p.ld_mod;
     sc = p.mscale + (int64_t)l * p.ld_mod;
   }
@@ -110,7 +146,8 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
   // Normalize one unit (v holds x), store y, rotate for the quantizer.
   auto finish = [&](int u, float (&v)[16], float inv, bool store_y) {
     uint32_t bits[8];
-    modulate16<DT, TB>(v, bits, inv, p.weight, sh, sc, (int64_t)u * 16);
+    if (STAGE && staged) modulate16<DT, TB>(v, bits, inv, tw, tsh, tsc, (int64_t)u * 16);
+    else modulate16<DT, TB>(v, bits, inv, p.weight, sh, sc, (int64_t)u * 16);
     if (store_y && yrow) {
       uint4* dst = reinterpret_cast<uint4*>(yrow + (int64_t)u * 16);
       dst[0] = make_uint4(bits[0], bits[1], bits[2], bits[3]);
@@ -223,10 +260,12 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(NormParams p) {
   }
 }
 
-template <int DT, int MODE, int TB>
-static void launch_norm_j(const NormParams& p, dim3 grid, dim3 block, hipStream_t stream) {
+template <int DT, int MODE, int TB, int W = kNormWaves, bool STAGE = false>
+static void launch_norm_j(const NormParams& p, hipStream_t stream) {
   const int jneed = (int)(((p.cols >> 4) + 63) / 64);
-#define W8A8_NLAUNCH(JJ) hipLaunchKernelGGL((norm_quant_kernel<DT, MODE, JJ, TB>), grid, block, 0, stream, p)
+  const dim3 grid((unsigned)((p.rows + W - 1) / W)), block(64 * W);
+  const size_t lds = 4 * (size_t)max(norm_lds_floats<MODE, W, STAGE>((int)p.cols), 1);
+#define W8A8_NLAUNCH(JJ) hipLaunchKernelGGL((norm_quant_kernel<DT, MODE, JJ, TB, W, STAGE>), grid, block, lds, stream, p)
   switch (jneed) {
     case 1: W8A8_NLAUNCH(1); break;
     case 2: W8A8_NLAUNCH(2); break;
@@ -244,13 +283,16 @@ static void launch_norm_j(const NormParams& p, dim3 grid, dim3 block, hipStream_
 // kernel with the tables decided per call.
 template <int DT, int MODE>
 static int launch_norm(const NormParams& p, hipStream_t stream) {
-  const dim3 grid((unsigned)((p.rows + kNormWaves - 1) / kNormWaves)), block(64 * kNormWaves);
-  if (p.weight && p.shift) {
-    launch_norm_j<DT, MODE, kGain | kMod>(p, grid, block, stream);
+  if (MODE == 0 && p.weight && p.shift && p.cols <= kNormStageMaxCols) {
+    if constexpr (MODE == 0) launch_norm_j<DT, MODE, kGain | kMod, kNormStageWaves, true>(p, stream);
+  } else if (p.weight && p.shift) {
+    launch_norm_j<DT, MODE, kGain | kMod>(p, stream);
   } else if (p.weight) {
-    launch_norm_j<DT, MODE, kGain>(p, grid, block, stream);
+    launch_norm_j<DT, MODE, kGain>(p, stream);
   } else {
-    hipLaunchKernelGGL((norm_quant_kernel<DT, MODE, 0, kAnyTables>), grid, block, 0, stream, p);
+    const dim3 grid((unsigned)((p.rows + kNormWaves - 1) / kNormWaves)), block(64 * kNormWaves);
+    hipLaunchKernelGGL((norm_quant_kernel<DT, MODE, 0, kAnyTables>), grid, block,
+                       4 * (size_t)max(norm_lds_floats<MODE, kNormWaves, false>(0), 1), stream, p);
   }
   return launch_status("w8a8_norm_quantize");
 }

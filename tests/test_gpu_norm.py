@@ -84,6 +84,25 @@ def test_norm_optional_gain_and_modulation(gpu, with_weight, with_mod):
     _check(r, _oracle(x, w, shift, scale, labels, 'rot', torch.float16), f'weight={with_weight} mod={with_mod}')
 
 
+@pytest.mark.parametrize('cols', [3072, 4096, 4112])
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+def test_norm_only_segments(gpu, cols, dtype):
+    # The norm-only DiT form stages the gain and the first row's shift and
+    # scale rows in each 8-row workgroup (up to 4096 columns): labels in
+    # segments that start inside workgroups (rows of one workgroup with two
+    # labels), a last workgroup of 3 rows, and 4112 columns on the unstaged path.
+    rows = 8 * 37 + 3
+    g = torch.Generator().manual_seed(cols + rows)
+    x = randn16(g, (rows, cols), 4.0, dtype)
+    w, shift, scale, _ = _tables(g, cols, rows)
+    bounds = [0, 5, 61, 62, 130, 211, 299]
+    labels = torch.zeros((rows,), dtype=torch.int32)
+    for i in range(len(bounds) - 1):
+        labels[bounds[i]:bounds[i + 1]] = (3 * i + 1) % 9
+    r = _run(x, w, shift, scale, labels, 'norm', gpu)
+    _check(r, _oracle(x, w, shift, scale, labels, 'norm', dtype), f'norm-only segments {rows}x{cols} {dtype}')
+
+
 def test_norm_labels_clamped_and_segments(gpu):
     g = torch.Generator().manual_seed(8)
     rows, cols = 10, 512
