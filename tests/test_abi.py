@@ -196,6 +196,9 @@ def test_rms_rope_argument_checks():
     _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'ldp': 4 * 128}), 'ldp')
     _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'q_out': 20482}), 'aligned')
     _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'freqs': None}), 'null')
+    # 11184816 rows x 24 heads: 6 workgroups of 64 threads per row reach 2^32 work-items
+    _expect_invalid('w8a8_rms_rope', _abi.RmsRopeArgs(**{**base, 'rows': 11184816, 'heads': 24,
+                                                        'ldp': 2 * 24 * 128}), 'too large')
     n = _abi.RmsRopeArgs(**{**base, 'rows': 0})
     assert _abi.load().w8a8_rms_rope(ctypes.byref(n)) == _abi.OK
 
