@@ -10,7 +10,7 @@
 //
 // Layout of the attention kernel: a workgroup of eight wavefronts (two per
 // SIMD) takes 256 queries of one (batch, head); a wavefront owns 32. Keys come in
-// blocks of 64 through a three-stage LDS ring (K tile 64 x 128 bytes, V^T
+// blocks of 64 through a four-stage LDS ring (K tile 64 x 128 bytes, V^T
 // tile 128 x 64 bytes). The score tile is computed transposed, S^T = K.Q^T, so a
 // lane holds one query (lane % 32) and 16 of every 32 keys: the softmax
 // statistics of a query need one exchange with the lane 32 away, and the
