@@ -52,16 +52,36 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   };
 
   if constexpr (J > 0) {
+    // Every unit's loads are issued before the first is transformed, so the
+    // row's memory latency is paid once, not once per unit (each rotation's
+    // LDS transpose orders the wave's memory accesses).
+    // Lanes past the row's last unit load that unit again (unused), so the
+    // loads are unconditional and the waits before each unit count exactly.
+    uint4 raw[J][4];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int u = min(lane + 64 * j, units - 1);
+      raw16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), raw[j]);
+    }
+    // Straight-line over all J units (a 256-column group is wholly in or
+    // out of the row, so the rotation's 16 lanes agree); units past the row
+    // are left out of the maximum and never stored.
     float v[J][16];
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const int u = lane + 64 * j;
-      if (u < units) {
-        load_unit(u, v[j]);
+      unpack16<DT>(raw[j], v[j]);
+      if constexpr (ROT != 0) {
+        convrot256_lanes<true>(v[j], buf, t);
+        if constexpr (ROT == 2) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[j][i]));
+          for (int i = 0; i < 16; ++i) v[j][i] = round_to<DT>(v[j][i]);
+        }
       }
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[j][i]));
+      amax = lane + 64 * j < units ? fmaxf(amax, m) : amax;
     }
     amax = row_max ? row_max[row] : wave_max(amax);
     if (row_max_out != nullptr && lane == 0) row_max_out[row] = amax;

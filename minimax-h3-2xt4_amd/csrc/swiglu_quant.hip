@@ -79,14 +79,37 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
   };
 
   if constexpr (P > 0) {
+    // Every pass's gate and up loads are issued before the first transform,
+    // so the row's memory latency is paid once, not once per pass. Slots
+    // past the last group load (and transform) that group again, unused:
+    // the code stays straight-line, so the waits before each pass count
+    // exactly.
+    uint4 graw[P][4], uraw[P][4];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int g = min(slot + kSlots * p, groups - 1);
+      raw16<DT>(xrow + ((int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), graw[p]);
+      raw16<DT>(xrow + (width + (int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), uraw[p]);
+    }
     float v[P][16];
     float local = 0.0f;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int g = slot + kSlots * p;
+      float gv[16], uv[16];
+      unpack16<DT>(graw[p], gv);
+      unpack16<DT>(uraw[p], uv);
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        v[p][i] = DT == kF16 ? swiglu_fp16_gate(gv[i], uv[i]) : swiglu(gv[i], uv[i]);
+      convrot256_lanes<true>(v[p], buf, t);
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[p][j]));
+      m = seg16_max(m);
       if (g < groups) {
-        transform(g, v[p]);
-        local = fmaxf(local, group_absmax(g, v[p]));
+        if (group_max && t == 0) group_max[row * groups + g] = m;
+        local = fmaxf(local, m);
       }
     }
     const float rmax = row_reduce(local);

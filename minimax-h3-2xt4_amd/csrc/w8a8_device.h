@@ -99,6 +99,40 @@ __device__ __forceinline__ void load16(const void* p, float (&v)[16]) {
   }
 }
 
+// The 16 elements of load16 in two phases: raw16 issues the loads (the
+// 32 or 64 bytes as uint4 words), unpack16 widens them, so a caller can
+// have several units' loads in flight before it uses the first.
+template <int DT>
+__device__ __forceinline__ void raw16(const void* p, uint4 (&r)[4]) {
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+  for (int i = 0; i < (DT == kF32 ? 4 : 2); ++i) r[i] = q[i];
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack16(const uint4 (&r)[4], float (&v)[16]) {
+  if constexpr (DT == kF32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[4 * i + 0] = __builtin_bit_cast(float, r[i].x);
+      v[4 * i + 1] = __builtin_bit_cast(float, r[i].y);
+      v[4 * i + 2] = __builtin_bit_cast(float, r[i].z);
+      v[4 * i + 3] = __builtin_bit_cast(float, r[i].w);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t w[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t lo = (uint16_t)(w[j] & 0xffffu), hi = (uint16_t)(w[j] >> 16);
+        v[8 * i + 2 * j + 0] = DT == kF16 ? h2f(lo) : bf2f(lo);
+        v[8 * i + 2 * j + 1] = DT == kF16 ? h2f(hi) : bf2f(hi);
+      }
+    }
+  }
+}
+
 // Round an fp32 value to the storage dtype DT and back (the rotation of a
 // 16-bit input returns a 16-bit tensor).
 template <int DT>
@@ -284,12 +318,29 @@ __device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int
 
 // The 16 int8 codes of elements 16t..16t+15 (natural order), packed for one
 // 16-byte store.
+// rne(x / s) as an fp32 integer value, without the clamp (quant1's rounding).
+__device__ __forceinline__ float quant_round(float x, float s, float rcp) {
+  const float y = x * rcp;
+  float n = rintf(y);
+  if (!(fabsf(y - n) < kTieGuard)) n = rintf(x / s);
+  return n;
+}
+
+// Sixteen quant1 codes packed little-endian. v_cvt_pk_u8_f32 converts
+// n + 128 (exact: n is an integer) with saturation to [0, 255] and packs the
+// byte, so the clamp to [-128, 127] and the packing take one instruction per
+// code and the XOR with 0x80 turns the biased bytes into two's complement.
+// NaN converts to 0 (code -128) and +-inf saturate (127 / -128), as quant1's
+// clamp gives them.
 __device__ __forceinline__ uint4 quant16(const float (&v)[16], float s, float rcp) {
   uint32_t w[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    w[i] = pack4(quant1(v[4 * i], s, rcp), quant1(v[4 * i + 1], s, rcp), quant1(v[4 * i + 2], s, rcp),
-                 quant1(v[4 * i + 3], s, rcp));
+  for (int i = 0; i < 4; ++i) {
+    uint32_t b = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) b = __builtin_amdgcn_cvt_pk_u8_f32(quant_round(v[4 * i + k], s, rcp) + 128.0f, k, b);
+    w[i] = b ^ 0x80808080u;
+  }
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
