@@ -66,23 +66,37 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     // Straight-line over all J units (a 256-column group is wholly in or
     // out of the row, so the rotation's 16 lanes agree); units past the row
     // are left out of the maximum and never stored.
-    float v[J][16];
+    // ConvRot256 rounded to fp16 (KEEP16): the rotated units are kept as
+    // packed fp16 pairs (exactly the rounded values), half the registers,
+    // and the maximum is taken on the fp32 rotation and rounded once:
+    // rounding is monotonic and odd, so that is the maximum of the rounded
+    // magnitudes (fmaxf skips NaN either way).
+    constexpr bool KEEP16 = ROT == 2 && DT == kF16;
+    float v[KEEP16 ? 1 : J][16];
+    uint32_t h16[KEEP16 ? J : 1][8];
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      unpack16<DT>(raw[j], v[j]);
+      float (&vj)[16] = v[KEEP16 ? 0 : j];
+      unpack16<DT>(raw[j], vj);
       if constexpr (ROT != 0) {
-        convrot256_lanes<true>(v[j], buf, t);
-        if constexpr (ROT == 2) {
+        convrot256_lanes<true>(vj, buf, t);
+        if constexpr (ROT == 2 && !KEEP16) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) v[j][i] = round_to<DT>(v[j][i]);
+          for (int i = 0; i < 16; ++i) vj[i] = round_to<DT>(vj[i]);
         }
       }
       float m = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[j][i]));
+      for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(vj[i]));
       amax = lane + 64 * j < units ? fmaxf(amax, m) : amax;
+      if constexpr (KEEP16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          h16[j][i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{vj[2 * i], vj[2 * i + 1]}, v2h));
+      }
     }
+    if constexpr (KEEP16) amax = round_to<DT>(amax);
     amax = row_max ? row_max[row] : wave_max(amax);
     if (row_max_out != nullptr && lane == 0) row_max_out[row] = amax;
     if (q == nullptr) return;  // maximum phase only
@@ -91,7 +105,19 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const int u = lane + 64 * j;
-      if (u < units) store_unit(u, v[j], s, rcp);
+      if (u < units) {
+        if constexpr (KEEP16) {
+          float w[16];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            w[2 * i] = h2f((uint16_t)(h16[j][i] & 0xffffu));
+            w[2 * i + 1] = h2f((uint16_t)(h16[j][i] >> 16));
+          }
+          store_unit(u, w, s, rcp);
+        } else {
+          store_unit(u, v[j], s, rcp);
+        }
+      }
     }
     if (lane == 0) scale[row] = s;
   } else {
