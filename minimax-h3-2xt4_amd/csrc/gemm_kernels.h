@@ -317,26 +317,34 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
     const uint4 (&rres)[R::ITERS] = rbuf[kResAhead ? buf_of(pass) : 0];
     // Gate values of the lane's columns for each of its rows (the row's
     // table row comes from the lane holding its label in the MFMA layout).
-    float gv[R::ITERS][R::CPL];
-    if constexpr (has_gate) {
+    // Gate values of the lane's columns for table row `label`.
+    auto load_gate = [&](int label, float (&gv)[R::CPL]) {
+      const float* gr = p.gate + (int64_t)label * p.ldg;
+      if (!in_quad) {
 #pragma unroll
-      for (int it = 0; it < R::ITERS; ++it) {
-        const int row = it * R::RPI + orow;
-        const float* gr = p.gate + (int64_t)__shfl(lbl[mb], row, 64) * p.ldg;
-        if (!in_quad) {
+        for (int j = 0; j < R::CPL; ++j) gv[j] = 0.0f;
+      } else if (p.gvec && full_cols) {
 #pragma unroll
-          for (int j = 0; j < R::CPL; ++j) gv[it][j] = 0.0f;
-        } else if (p.gvec && full_cols) {
-#pragma unroll
-          for (int q = 0; q < R::CPL / 4; ++q) {
-            const float4 g4 = *reinterpret_cast<const float4*>(gr + ncol + 4 * q);
-            gv[it][4 * q] = g4.x; gv[it][4 * q + 1] = g4.y; gv[it][4 * q + 2] = g4.z; gv[it][4 * q + 3] = g4.w;
-          }
-        } else {
-#pragma unroll
-          for (int j = 0; j < R::CPL; ++j) gv[it][j] = gr[min(ncol + j, p.n - 1)];
+        for (int q = 0; q < R::CPL / 4; ++q) {
+          const float4 g4 = *reinterpret_cast<const float4*>(gr + ncol + 4 * q);
+          gv[4 * q] = g4.x; gv[4 * q + 1] = g4.y; gv[4 * q + 2] = g4.z; gv[4 * q + 3] = g4.w;
         }
+      } else {
+#pragma unroll
+        for (int j = 0; j < R::CPL; ++j) gv[j] = gr[min(ncol + j, p.n - 1)];
       }
+    };
+    // The 32 rows of a pass almost always share one gate label (the DiT's
+    // segments are whole frames), and then one table row serves the whole
+    // pass: the lane's CPL values, loaded once. Otherwise each read-out row
+    // loads its own (the row's label comes from the lane holding it in the
+    // MFMA layout).
+    float gv[R::CPL];
+    bool gate_one = true;
+    if constexpr (has_gate) {
+      const int lab0 = __shfl(lbl[mb], 0, 64);
+      gate_one = __builtin_amdgcn_ballot_w64(lbl[mb] != lab0) == 0;
+      if (gate_one) load_gate(lab0, gv);
     }
     // acc[nb][mb] group g holds columns 32 nb + 8 g + 4 fh + [0, 4) of row fr.
 #pragma unroll
@@ -387,14 +395,17 @@ __device__ __forceinline__ void store_quadrant32_passes(const GemmParams& p, v16
         }
         f2h8_of_f32(y, words);
         if constexpr (has_res) {
+          if constexpr (has_gate) {
+            if (!gate_one) load_gate(__shfl(lbl[mb], row, 64), gv);
+          }
           const uint32_t rw[4] = {rres[it].x, rres[it].y, rres[it].z, rres[it].w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float r0 = h2f((uint16_t)(rw[i] & 0xffffu)), r1 = h2f((uint16_t)(rw[i] >> 16));
             const float b0 = h2f((uint16_t)(words[i] & 0xffffu)), b1 = h2f((uint16_t)(words[i] >> 16));
             if constexpr (has_gate) {
-              y[2 * i] = __builtin_fmaf(b0, gv[it][2 * i], r0);
-              y[2 * i + 1] = __builtin_fmaf(b1, gv[it][2 * i + 1], r1);
+              y[2 * i] = __builtin_fmaf(b0, gv[2 * i], r0);
+              y[2 * i + 1] = __builtin_fmaf(b1, gv[2 * i + 1], r1);
             } else {
               y[2 * i] = r0 + b0;
               y[2 * i + 1] = r1 + b1;

@@ -573,7 +573,8 @@ GATE_CASES = [
 
 
 @pytest.mark.parametrize('m,n,k', GATE_CASES)
-def test_gemm_gated_residual(gpu, m, n, k):
+@pytest.mark.parametrize('label_kind', ['random', 'segments'])
+def test_gemm_gated_residual(gpu, m, n, k, label_kind):
     g = torch.Generator().manual_seed(m + 3 * n + k)
     a = randi8(g, (m, k))
     b = randi8(g, (n, k))
@@ -581,7 +582,15 @@ def test_gemm_gated_residual(gpu, m, n, k):
     ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
     res = randn16(g, (m, n), 1 / 512)
     gate = torch.randn((9, n), generator=g)
-    labels = torch.randint(0, 9, (m,), generator=g, dtype=torch.int32)
+    if label_kind == 'random':
+        # Every epilogue pass mixes labels: each row reads its own table row.
+        labels = torch.randint(0, 9, (m,), generator=g, dtype=torch.int32)
+    else:
+        # DiT frames: long runs of one label, so most 32-row passes read one
+        # table row, and the boundaries (not multiples of 32) fall inside passes.
+        bounds = [0] + sorted(torch.randperm(m - 1, generator=g)[:4].add(1).tolist()) + [m]
+        labels = torch.cat([torch.full((bounds[i + 1] - bounds[i],), i % 9, dtype=torch.int32)
+                            for i in range(len(bounds) - 1)])
     got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
                        out_dtype=torch.float16, residual=res.to(gpu), gate=gate.to(gpu), gate_labels=labels.to(gpu))
     branch = o.dequantize_row(o.int_mm(np_of(a), np_of(b)), np_of(rs).reshape(-1), np_of(ws).reshape(-1), 'f16')
