@@ -995,7 +995,8 @@ def run_dit_attention(args, torch, dev):
                ms_per_step=round(ta + tp, 3),
                roofline=dict(bound='mfma', achieved=round(tops, 1), peak=PEAK_INT8_TOPS, unit='TFLOP/s',
                              frac=round(tops / PEAK_INT8_TOPS, 4), traffic=None,
-                             kernel='attention_kernel<1> (256 queries x 64-key blocks per workgroup)',
+                             kernel='attention_kernel<1> (256 queries x 128-key blocks per workgroup, one '
+                                    'online-softmax pass)',
                              algorithmic=f'{ops:.4g} int8 ops per launch (4 N^2 D H)'),
                kernels=dict(prepare_us=round(tp * 1e3, 1), attention_us=round(ta * 1e3, 1)))
     if not args.no_cpu_baseline:
@@ -1006,8 +1007,8 @@ def run_dit_attention(args, torch, dev):
         qn, kn, vn = (data[t][:, :1].float().numpy() for t in ('q', 'k', 'v'))
 
         def cpu():
-            pr = oa.prepare(qn[:, :, :rows], kn, vn)
-            return oa.attention(pr)
+            pr = oa.kitchen_prepare(qn[:, :, :rows], kn, vn, cta_k=oa.GPU_CTA_K)
+            return oa.kitchen_attention(pr)
 
         tc = _cpu_rows_timing(cpu, reps=1) * (n / rows) * h
         res['cpu_baseline'] = dict(value=round(ops / tc / 1e12, 6), unit='TOPS', cores=blas_threads(), kind='port',
@@ -1122,7 +1123,7 @@ def run_dit_attention_block(args, torch, dev):
         ka, va = (rng.standard_normal((1, 1, m, 128)).astype(np.float32) for _ in range(2))
 
         def cpu_attention():
-            return oa.attention(oa.prepare(qa, ka, va))
+            return oa.kitchen_attention(oa.kitchen_prepare(qa, ka, va, cta_k=oa.GPU_CTA_K))
 
         tc = _cpu_rows_timing(cpu_rows) * m / rows + _cpu_rows_timing(cpu_attention, reps=1) * (m / queries) * heads
         res['cpu_baseline'] = dict(value=round(ops / tc / 1e12, 6), unit='TOPS', cores=blas_threads(), kind='port',

@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 11
+#define W8A8_ABI_VERSION 12
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -236,22 +236,26 @@ int w8a8_rms_rope(const W8A8RmsRopeArgs* args);
  * prepared Kitchen route (patches/h3_operator_policy.py:173-209:
  * ck.prequantize_int8_attention, then ck.int8_attention_from_prequantized;
  * patches/kitchen_attention.py:227-238 int8_attention; the native launcher
- * patches/kitchen_attention_native/attention.cu:20-101 h3_attention, whose
- * vendored kernel is not part of the reference). The numerics are this
- * library's own SageAttention-style scheme; they match the reference's only
- * approximately:
- *   prepare: k is centred per channel (mean over the keys; softmax-invariant);
- *     q rows get per-token scales (stored multiplied by sm_scale * log2(e)),
- *     k one scale per 64-key block, v one scale per channel; INT8 codes
- *     sat(rne(x / s)) with s = max(amax * fp32(1/127), 1e-30). v is written
- *     transposed: vt8[c][64 j + 32 u + p] holds key 64 j + 32 u + 8 g + 4 h + i
- *     of channel c for p = 16 h + 4 g + i.
- *   attention: S = q8.k8 (int32); m = the query's largest logit
- *     fp32(max(S) * qs * ks[block]); probabilities
- *     P = min(255, rne(exp2(fma(S, qs * ks, log2(255) - m)))) in 0..255
- *     (hardware exp2); acc = P.v8 exact (the MFMA takes P - 128, and
- *     128 * vsum is added per channel) and sum(P) exact
- *     (nk <= 131072); output fp32(fp32(f32(acc) * vs[c]) / f32(sum P)).
+ * patches/kitchen_attention_native/attention.cu:20-66 h3_attention). The
+ * numerics are those of the reference's vendored kernel
+ * (kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh, attn_utils.cuh) for
+ * key blocks of CTA_K = 128, with the SageAttention quantizer assumed for
+ * Kitchen's absent one:
+ *   prepare: codes sat(round half away(x / s)) with s = amax / 127 + 1e-7; q rows
+ *     32 G + 8 i + j share the scale of (G, j); k is centred per channel
+ *     (its fp32 mean) and key 8 t + 2 c + e of a 128-key block shares the
+ *     scale of (block, c); v takes one scale per channel. v is written
+ *     transposed: vt8[c][128 j + 32 u + p] holds key 128 j + 32 u + 8 g + 4 h
+ *     + i of channel c for p = 16 h + 4 g + i; vsum[j][c] = 128 * the sum of
+ *     block j's v codes of channel c.
+ *   attention: one online pass over the 128-key blocks in the exp2 domain:
+ *     the block's maximum per K-scale group, tile_m = max over the groups of
+ *     fma(mt, fp32(c0 * fp32(qs * ks)), -S_U8_OFFSET) (c0 = sm_scale *
+ *     log2(e)), u8 probabilities sat(rne(exp2(fma(S, ts, -tile_m)))) relative
+ *     to the block's own maximum, FP32 rescaling of the running output and of
+ *     the four group denominators, P.V exact in int32 and added with one FMA
+ *     of the block scale; output (O * (1 / sum of denominators)) * vs[c]
+ *     (hardware exp2; nk <= 131072).
  * q, k, v: [b, h, nq|nk, d] with element strides {batch, head, token} given
  * per tensor and the d == 128 channels contiguous (e.g. the q, k and v
  * columns of a packed [tokens, 3 * h * d] QKV projection, or contiguous
@@ -269,17 +273,17 @@ typedef struct W8A8AttnPrepareArgs {
   int64_t nq;
   int64_t nk;
   int32_t d;
-  float sm_scale;          /* > 0; the reference's default is 1/sqrt(d) */
+  float sm_scale;          /* > 0 (checked; the attention call takes its own) */
   int64_t q_strides[3];    /* element strides of q's batch, head and token dims */
   int64_t k_strides[3];
   int64_t v_strides[3];
   int8_t* q8;              /* [b, h, nq, d] */
-  float* qs;               /* [b, h, nq] */
-  int8_t* k8;              /* [b, h, nkp, d], nkp = 64 * ceil(nk / 64) */
-  float* ks;               /* [b, h, nkp / 64] */
+  float* qs;               /* [b, h, nq]: each row's group scale */
+  int8_t* k8;              /* [b, h, nkp, d], nkp = 128 * ceil(nk / 128) */
+  float* ks;               /* [b, h, nkp / 128, 4]: the four group scales of each block */
   int8_t* vt8;             /* [b, h, d, nkp] */
   float* vs;               /* [b, h, d] */
-  int32_t* vsum;           /* [b, h, d]: sum over the keys of vt8, per channel */
+  int32_t* vsum;           /* [b, h, nkp / 128, d]: 128 * each block's sum of v codes */
   void* workspace;         /* w8a8_attention_workspace_size(b, h, nk) bytes */
   int64_t workspace_bytes;
   void* stream;
@@ -287,7 +291,7 @@ typedef struct W8A8AttnPrepareArgs {
 
 int w8a8_attention_prepare(const W8A8AttnPrepareArgs* args);
 
-/* Scratch bytes w8a8_attention_prepare needs (key statistics, V reciprocals). */
+/* Scratch bytes w8a8_attention_prepare needs (key statistics, V divisors). */
 int64_t w8a8_attention_workspace_size(int64_t b, int64_t h, int64_t nk);
 
 typedef struct W8A8AttentionArgs {
@@ -305,7 +309,7 @@ typedef struct W8A8AttentionArgs {
   int64_t nq;
   int64_t nk;
   int32_t d;
-  int32_t reserved;
+  float sm_scale;          /* > 0; the reference's default is 1/sqrt(d) */
   void* out;               /* [b, h, nq, d] of out_dtype, element strides out_strides */
   int64_t out_strides[3];  /* batch, head, token */
   void* stream;

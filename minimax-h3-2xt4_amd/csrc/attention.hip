@@ -1,23 +1,28 @@
-// INT8 attention for 128-wide heads: the preparation of the INT8 operands
-// (key centering, per-token Q scales, per-64-key K scales, per-channel V
-// scales, V transposed) and the attention kernel (S = Q.K^T on INT8 MFMA;
-// a first pass finds each query's largest logit, the second quantizes the
-// exp2-domain probabilities against it to integers P in 0..255 and feeds
-// P - 128 to the signed INT8 MFMA P.V product; the 128 * sum over keys of V
-// it leaves out is one per-channel integer that the preparation sums. The denominator is the sum of the same integers P, so the whole
-// accumulation is exact. The exponentials use the hardware exp2
-// (v_exp_f32).
+// INT8 attention for 128-wide heads on the reference kernel's scheme
+// (SageAttention's qk_int_sv_i8 as vendored by the reference: per-thread-group
+// Q and K scales, a one-pass online softmax in the exp2 domain, u8
+// probabilities relative to each key block's own maximum, FP32 rescaling of
+// the running output and denominators, the per-channel V scale applied at
+// the end), for key blocks of 128.
 //
-// Layout of the attention kernel: a workgroup of eight wavefronts (two per
-// SIMD) takes 256 queries of one (batch, head); a wavefront owns 32. Keys come in
-// blocks of 64 through a four-stage LDS ring (K tile 64 x 128 bytes, V^T
-// tile 128 x 64 bytes). The score tile is computed transposed, S^T = K.Q^T, so a
-// lane holds one query (lane % 32) and 16 of every 32 keys: the softmax
-// statistics of a query need one exchange with the lane 32 away, and the
-// quantized probabilities are already the B operand of O^T = V^T.P^T. Its K
-// positions follow the order in which the score layout hands out the keys,
-// so the preparation writes V^T with the same order inside each 32-key
-// group (position 16 h + 4 g + i holds key 8 g + 4 h + i).
+// Preparation: key statistics (fp32 chunk sums of K, absmax of V per
+// channel), then per 128-token block the Q codes (one scale per 32-row group
+// and row mod 8), the centred K codes (four scales per block, one per
+// (key mod 8) / 2), the V codes with the channel scales, V^T in the order the
+// score tile hands a lane its keys, and 128 times each block's sum of the V
+// codes per channel. Codes are sat(round half away(x / s)), s = amax / 127 +
+// 1e-7.
+//
+// Attention: a workgroup of eight wavefronts (two per SIMD) takes 256
+// queries of one (batch, head); a wavefront owns 32. Key blocks of 128 are
+// DMA'd global -> LDS (K 128 x 128 bytes, V^T 128 x 128 bytes, the block's
+// V sums) into a ring of four stages, three blocks ahead. Scores are computed
+// transposed, S^T = K.Q^T on v_mfma_i32_32x32x32_i8, so a lane holds one
+// query (lane % 32) and 64 of the block's keys: exactly the keys of two of
+// the four K-scale groups, whose maxima it takes alone. The u8
+// probabilities are then already the B operand of O^T = V^T.P^T; the signed
+// MFMA takes P - 128, and its accumulator starts from the block's 128 * sum
+// of V codes, so it ends with the exact P.V.
 #include "w8a8_device.h"
 #include "w8a8_host.h"
 
@@ -26,15 +31,26 @@
 
 namespace w8a8 {
 
-constexpr int kAttnD = 128;       // head dimension
-constexpr int kAttnBK = 64;       // keys per block
-constexpr int kAttnChunk = 256;   // tokens per partial of the key statistics
-constexpr int kAttnWaveQ = 32;    // queries per wavefront
-constexpr int kAttnWaves = 8;     // wavefronts per workgroup
+constexpr int kAttnD = 128;        // head dimension
+constexpr int kAttnBK = 128;       // keys per block (the reference launcher's CTA_K = 128)
+constexpr int kAttnChunk = 256;    // tokens per partial of the key statistics
+constexpr int kAttnWaveQ = 32;     // queries per wavefront
+constexpr int kAttnWaves = 8;      // wavefronts per workgroup
 constexpr int kAttnBQ = kAttnWaves * kAttnWaveQ;   // queries per workgroup
-constexpr int kAttnDma = 8 / kAttnWaves;           // 1 KB DMA instructions per wave and tile
-constexpr float kLog2e = 0x1.715476p+0f;    // fp32(log2(e))
-constexpr float kLog2_255 = 0x1.ffa37cp+2f; // fp32(log2(255))
+constexpr int kAttnTile = kAttnBK * kAttnD;        // bytes of one K or V^T tile
+constexpr int kAttnDmaTile = kAttnTile / 1024 / kAttnWaves;   // 1 KB DMA instructions per wave and tile
+constexpr int kAttnDmaBlk = 2 * kAttnDmaTile + 1;  // per wave and block: K, V^T, 64 bytes of V sums
+constexpr int kAttnMaxBlk = 1024;  // nk <= 131072
+constexpr float kLog2e = 0x1.715476p+0f;     // fp32(log2(e))
+// The reference's constants (kitchen_attention_native/vendor/attn_utils.cuh:
+// S_U8_OFFSET, :40; the running maximum's start and the out-of-bounds score
+// of its last-block path).
+constexpr float kSU8Offset = 7.9943534f;
+constexpr float kMInit = -50000.0f;
+constexpr float kMaskScore = -1e30f;
+// SageAttention's per-thread quantizers: scale = amax / 127 + 1e-7 (no scale
+// is zero, so the out-of-bounds score masks every padded key).
+constexpr float kScaleEps = 1e-7f;
 
 // Element strides of a [batch, head, token, channel] tensor whose channels
 // are contiguous; at(bh, t) is the offset of token t's row of the flat
@@ -53,18 +69,16 @@ struct AttnPrepParams {
   const void* v;
   Strides3 qst, kst, vst;
   int nq, nk, nkp, nblk, chunks;
-  float c0;   // fp32(sm_scale * log2(e))
   int8_t* q8;
   float* qs;
   int8_t* k8;
   float* ks;
   int8_t* vt8;
   float* vs;
-  int32_t* vsum;   // sum over the keys of vt8 per channel (int32 atomics)
+  int32_t* vsum;   // [bh, nblk, 128]: 128 * the block's sum of V codes per channel
   float* part_sum;
   float* part_max;
   float* kmean;
-  float* vrcp;   // 1 / vs per channel (IEEE), so tokens do not divide
 };
 
 // 8 consecutive channels of one token row (16-byte loads).
@@ -136,7 +150,8 @@ __global__ __launch_bounds__(256) void attn_stats_kernel(AttnPrepParams p) {
 }
 
 // Key mean (the partials added in chunk order, then one division by Nk) and
-// the per-channel V scale. The partials are loaded 16 chunks at a time.
+// the per-channel V scale amax / 127 + 1e-7 (IEEE division). The partials are
+// loaded 16 chunks at a time.
 __global__ __launch_bounds__(128) void attn_finalize_kernel(AttnPrepParams p) {
   const int d = threadIdx.x;
   const int64_t bh = blockIdx.x;
@@ -162,28 +177,7 @@ __global__ __launch_bounds__(128) void attn_finalize_kernel(AttnPrepParams p) {
     m = fmaxf(m, pm[(int64_t)c * kAttnD]);
   }
   p.kmean[bh * kAttnD + d] = s / (float)p.nk;
-  const float sv = row_scale_of(m);
-  p.vs[bh * kAttnD + d] = sv;
-  p.vrcp[bh * kAttnD + d] = 1.0f / sv;
-  p.vsum[bh * kAttnD + d] = 0;   // the quant kernel adds each block's codes
-}
-
-// 32 consecutive channels [32 part, 32 part + 32) of token t (16-byte loads).
-template <int DT>
-__device__ __forceinline__ void load32(const void* base, int64_t off, float (&x)[32]) {
-  float a[16], b[16];
-  if constexpr (DT == kF32) {
-    load16<kF32>(reinterpret_cast<const float*>(base) + off, a);
-    load16<kF32>(reinterpret_cast<const float*>(base) + off + 16, b);
-  } else {
-    load16<kF16>(reinterpret_cast<const uint16_t*>(base) + off, a);
-    load16<kF16>(reinterpret_cast<const uint16_t*>(base) + off + 16, b);
-  }
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    x[i] = a[i];
-    x[16 + i] = b[i];
-  }
+  p.vs[bh * kAttnD + d] = m / 127.0f + kScaleEps;
 }
 
 __device__ __forceinline__ void store32_i8(int8_t* dst, const int (&q)[32]) {
@@ -226,99 +220,99 @@ __device__ __forceinline__ void unpack32(const Raw32<DT>& r, float (&x)[32]) {
   }
 }
 
-// Block blk of 64 tokens of one (batch, head): thread (token tid / 4, part
-// tid % 4) handles 32 channels. Q rows get their own scale; K rows are
-// centred and share one scale per block; V is quantized with the channel
-// scales and written transposed (through LDS) in the permuted key order.
+// The reference quantizer's code of x / s: round half away from zero as
+// floor(q + 0.5) for q >= 0 and ceil(q - 0.5) below (each addition rounded
+// in fp32), saturated to [-128, 127].
+__device__ __forceinline__ int rha_code(float q) {
+  const float r = q >= 0.0f ? floorf(q + 0.5f) : ceilf(q - 0.5f);
+  return (int)fminf(fmaxf(r, -128.0f), 127.0f);
+}
+
+// Block blk of 128 tokens of one (batch, head): thread (token tid / 4, part
+// tid % 4) handles 32 channels. Q row 32 G + 8 i + j shares its scale with
+// the rows of the same 32-row group G and the same j; centred K key
+// 8 t + 2 c + e with the keys of the block of the same c; V takes the channel
+// scales, goes through LDS to be written transposed in the permuted key
+// order, and each channel's block sum of codes (times 128) is stored.
+// Group maxima meet in LDS (integer max of the non-negative fp32 bits).
 template <int DT>
-__global__ __launch_bounds__(256) void attn_quant_kernel(AttnPrepParams p) {
+__global__ __launch_bounds__(512) void attn_quant_kernel(AttnPrepParams p) {
   __shared__ __attribute__((aligned(16))) int8_t vtile[kAttnBK * kAttnD];
-  __shared__ float wmax[4];
+  __shared__ unsigned qmax[32], kmax[4];
   const int tid = threadIdx.x, tl = tid >> 2, part = tid & 3;
   const int blk = blockIdx.x;
   const int64_t bh = blockIdx.y;
   const int t = blk * kAttnBK + tl;
   const int c0 = 32 * part;
-  // The Q, K and V rows are loaded up front, in the order they are used
-  // (rows past the end re-read the last row and are then ignored).
+  // The Q, K and V rows are loaded up front (rows past the end re-read the
+  // last row and are then ignored).
   Raw32<DT> rq, rk, rv;
   load_raw32<DT>(p.q, p.qst.at(bh, min(t, p.nq - 1)) + c0, rq);
   load_raw32<DT>(p.k, p.kst.at(bh, min(t, p.nk - 1)) + c0, rk);
   load_raw32<DT>(p.v, p.vst.at(bh, min(t, p.nk - 1)) + c0, rv);
-  // Both phases run in every workgroup (one basic block keeps the three
-  // loads ahead); the stores are masked to the rows that exist.
+  if (tid < 32) qmax[tid] = 0u;
+  if (tid < 4) kmax[tid] = 0u;
+  __syncthreads();
   const bool q_blk = blk * kAttnBK < p.nq, k_blk = blk < p.nblk;   // workgroup-uniform
-  {
-    const bool valid = q_blk && t < p.nq;
-    float x[32];
-    unpack32<DT>(rq, x);
+  const bool qvalid = q_blk && t < p.nq, kvalid = k_blk && t < p.nk;
+  const int qg = (tl >> 5) * 8 + (tl & 7);   // row 32 G + 8 i + j of the block: group (G, j)
+  const int kg = (tl & 7) >> 1;              // key 8 t + 2 c + e of the block: group c
+  float xq[32], xk[32];
+  unpack32<DT>(rq, xq);
+  unpack32<DT>(rk, xk);
+  const float* mean = p.kmean + bh * kAttnD + c0;
+  float aq = 0.0f, ak = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) x[i] = valid ? x[i] : 0.0f;
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    const float s = row_scale_of(amax), rcp = 1.0f / s;
+  for (int i = 0; i < 32; ++i) {
+    xq[i] = qvalid ? xq[i] : 0.0f;
+    xk[i] = kvalid ? xk[i] - mean[i] : 0.0f;
+    aq = fmaxf(aq, fabsf(xq[i]));
+    ak = fmaxf(ak, fabsf(xk[i]));
+  }
+  atomicMax(&qmax[qg], __float_as_uint(aq));
+  atomicMax(&kmax[kg], __float_as_uint(ak));
+  __syncthreads();
+  if (q_blk) {
+    const float s = __uint_as_float(qmax[qg]) / 127.0f + kScaleEps;
     int q[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) q[i] = quant1(x[i], s, rcp);
-    if (valid) {
+    for (int i = 0; i < 32; ++i) q[i] = rha_code(xq[i] / s);
+    if (qvalid) {
       store32_i8(p.q8 + (bh * p.nq + t) * kAttnD + c0, q);
-      if (part == 0) p.qs[bh * p.nq + t] = s * p.c0;
+      if (part == 0) p.qs[bh * p.nq + t] = s;
     }
   }
-  {
-    const bool valid = k_blk && t < p.nk;
-    const float* mean = p.kmean + bh * kAttnD + c0;
-    float x[32];
-    unpack32<DT>(rk, x);
-#pragma unroll
-    for (int i = 0; i < 32; ++i) x[i] = valid ? x[i] - mean[i] : 0.0f;
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = wave_max(amax);
-    if ((tid & 63) == 0) wmax[tid >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const float s = row_scale_of(amax), rcp = 1.0f / s;
+  if (k_blk) {
+    const float s = __uint_as_float(kmax[kg]) / 127.0f + kScaleEps;
     int q[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) q[i] = quant1(x[i], s, rcp);
-    if (k_blk) {
-      store32_i8(p.k8 + (bh * p.nkp + t) * kAttnD + c0, q);
-      if (tid == 0) p.ks[bh * p.nblk + blk] = s;
-    }
+    for (int i = 0; i < 32; ++i) q[i] = rha_code(xk[i] / s);
+    store32_i8(p.k8 + (bh * p.nkp + t) * kAttnD + c0, q);
+    if (tl < 8 && (tl & 1) == 0 && part == 0) p.ks[(bh * p.nblk + blk) * 4 + kg] = s;
     // V: channel scales, then the tile goes through LDS to be transposed.
-    const float* vsc = p.vs + bh * kAttnD + c0;
-    const float* vrc = p.vrcp + bh * kAttnD + c0;
-    unpack32<DT>(rv, x);
+    const float* vsf = p.vs + bh * kAttnD + c0;
+    float xv[32];
+    unpack32<DT>(rv, xv);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float sv = vsc[i];
-      q[i] = valid ? quant1(x[i], sv, vrc[i]) : 0;
-    }
+    for (int i = 0; i < 32; ++i) q[i] = kvalid ? rha_code(xv[i] / vsf[i]) : 0;
     store32_i8(vtile + tl * kAttnD + c0, q);
     __syncthreads();
-    // Thread (channel ch, 32-key group gq) writes 32 bytes of V^T row ch.
-    const int ch = tid >> 1, gq = tid & 1;
+    // Thread (channel ch, 32-key slice u) writes 32 bytes of V^T row ch:
+    // position p of the slice holds key 8 ((p >> 2) & 3) + 4 (p >> 4) + (p & 3).
+    const int ch = tid >> 2, u = tid & 3;
     int vb[32];
 #pragma unroll
     for (int pos = 0; pos < 32; ++pos) {
-      const int key = 8 * ((pos >> 2) & 3) + 4 * (pos >> 4) + (pos & 3);
-      vb[pos] = vtile[(32 * gq + key) * kAttnD + ch];
+      const int key = 32 * u + 8 * ((pos >> 2) & 3) + 4 * (pos >> 4) + (pos & 3);
+      vb[pos] = vtile[key * kAttnD + ch];
     }
-    if (k_blk) {
-      store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * gq, vb);
-      // The block's codes of channel ch, added to its sum over the keys
-      // (integer atomics: exact in any order).
-      int sum = 0;
+    store32_i8(p.vt8 + (bh * kAttnD + ch) * (int64_t)p.nkp + blk * kAttnBK + 32 * u, vb);
+    int sum = 0;
 #pragma unroll
-      for (int pos = 0; pos < 32; ++pos) sum += vb[pos];
-      sum += __shfl_xor(sum, 1, 64);
-      if (gq == 0) atomicAdd(p.vsum + bh * kAttnD + ch, sum);
-    }
+    for (int pos = 0; pos < 32; ++pos) sum += vb[pos];
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (u == 0) p.vsum[(bh * p.nblk + blk) * kAttnD + ch] = 128 * sum;
   }
 }
 
@@ -349,6 +343,7 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
 }
 
+
 struct AttnParams {
   const int8_t* q8;
   const float* qs;
@@ -360,25 +355,41 @@ struct AttnParams {
   void* out;
   Strides3 ost;
   int nq, nk, nkp, nblk;
+  float c0;   // fp32(sm_scale * log2(e))
 };
 
+// One LDS stage: a block's K tile (128 keys x 128 bytes), its V^T tile (128
+// channels x 128 bytes) and its 128 * V code sums. Rows of both tiles are
+// 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7), so the
+// fragment reads (32 rows of one chunk column) are free of bank conflicts.
+struct AttnStage {
+  int8_t k[kAttnTile];
+  int8_t v[kAttnTile];
+  int32_t vsum[kAttnD];
+};
+
+// The reference's online softmax, per query row (the lane's query fr; the
+// two half-waves hold the two halves of each 32-key slice):
+//   group maxima mt_c over the block's keys of K-scale group c (the last
+//     block: keys past nk excluded and a floor of -50000);
+//   tile_m = max_c fma(mt_c, ts_c, -S_U8_OFFSET) with ts_c = fp32(c0 *
+//     fp32(qs * ks_c)); m' = max(m, tile_m); smaller = exp2(-|m - tile_m|);
+//     the state (output and the four denominators) is scaled by smaller when
+//     the tile raises the maximum, the tile's contribution otherwise;
+//   P = sat_u8(rne(exp2(fma(S, ts_c, -tile_m))));
+//   each group's denominator adds, per 16-key tile, its four P (u8 codes; the
+//     last block: the FP32 probabilities ((p0 + p1) + (p8 + p9))) times the
+//     tile scale, one FMA;
+//   O += f32(P.V) * tile scale (one FMA), P.V exact in int32;
+// finally O * (1 / ((d0 + d1) + (d2 + d3))) * vs.
+// The exponentials use the hardware exp2 (v_exp_f32).
 template <int OUT>
 __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p) {
-  // A ring of LDS stages, each [0: K tile, 64 keys x 128 bytes; 1: V^T
-  // tile, 128 channels x 64 bytes]. Two passes over the keys: the first
-  // finds each query's largest logit (K tiles only, two blocks per stage,
-  // three stages), the second quantizes the probabilities against it and
-  // accumulates P.V and sum(P) in int32 (one block per stage, four stages).
-  // In both, a step computes the next block's scores before working on the
-  // current one (the MFMAs run under the VALU work), and every DMA has two
-  // steps to land. The stages are separate arrays named by compile-time
-  // index, so the compiler sees that reads of one stage do not alias a DMA
-  // still landing in another and does not wait for that DMA before them.
-  __shared__ __attribute__((aligned(16))) int8_t stage0[2][kAttnBK * kAttnD];
-  __shared__ __attribute__((aligned(16))) int8_t stage1[2][kAttnBK * kAttnD];
-  __shared__ __attribute__((aligned(16))) int8_t stage2[2][kAttnBK * kAttnD];
-  __shared__ __attribute__((aligned(16))) int8_t stage3[2][kAttnBK * kAttnD];
-  using Stage = int8_t (*)[kAttnBK * kAttnD];
+  // Four stages, named by compile-time index so the compiler sees that reads
+  // of one stage do not alias a DMA still landing in another. Block j lives
+  // in stage j % 4; step j refills the stage of step j - 1 with block j + 3.
+  __shared__ __attribute__((aligned(16))) AttnStage st0, st1, st2, st3;
+  __shared__ float ksc[4 * kAttnMaxBlk];   // the head's K scales, four per block
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hh = lane >> 5;
   const int64_t bh = blockIdx.y;
@@ -386,6 +397,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   const int qrow = min(q0 + fr, p.nq - 1);
   const int8_t* k8 = p.k8 + bh * (int64_t)p.nkp * kAttnD;
   const int8_t* vt8 = p.vt8 + bh * (int64_t)kAttnD * p.nkp;
+  const int32_t* vsumh = p.vsum + bh * (int64_t)p.nblk * kAttnD;
   // Q fragments (B operand of S^T = K.Q^T): query fr, channels 32 ds + 16 hh + [0, 16).
   v4i qf[4];
   {
@@ -393,250 +405,195 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const v4i*>(qp + 32 * ds);
   }
-  const float qscale = p.qs[bh * p.nq + qrow];
-  // The per-block K scales of the head, staged in LDS (read before the
-  // first DMA) so the block loops issue no vector-memory loads besides the
-  // DMA and their waits can count it exactly.
-  __shared__ float ksc[2048];   // nblk <= 131072 / 64
-  for (int i = tid; i < p.nblk; i += 64 * kAttnWaves) ksc[i] = p.ks[bh * p.nblk + i];
-  // Tiles are DMA'd global -> LDS, each wave filling 2 KB of each: K rows
-  // are 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7),
-  // V^T rows 64 bytes with chunk c at c ^ ((row >> 2) & 3) (the fragment
-  // reads, 32 rows of one chunk column, are then free of bank conflicts). A
-  // DMA lane writes the next 16 bytes of its instruction's kilobyte, so it
-  // loads the chunk that lands on its physical position.
-  auto dma_tiles = [&](int j, Stage stg) {
+  const float qsr = p.qs[bh * p.nq + qrow];
+  for (int i = tid; i < 4 * p.nblk; i += 64 * kAttnWaves) ksc[i] = p.ks[bh * 4 * p.nblk + i];
+  // Block j's tiles: each wave DMAs kAttnDmaTile kilobytes of each (8 rows
+  // per instruction; a lane loads the chunk that lands on its position) and
+  // 64 bytes of the V sums (four lanes). Every block issues exactly
+  // kAttnDmaBlk instructions per wave: past the last block an in-range block
+  // is re-loaded into a stage never read, so the waits count exactly.
+  // The lanes' byte offsets within a block are loop-invariant (32-bit: a
+  // head's V^T is at most 128 x 131072 bytes); each block adds a
+  // wave-uniform base.
+  uint32_t koff[kAttnDmaTile], voff[kAttnDmaTile];
 #pragma unroll
-    for (int u = 0; u < kAttnDma; ++u) {
-      const int kb = kAttnDma * wave + u;
-      const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
-      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, stg[0] + kb * 1024);
-      const int ch = 16 * kb + (lane >> 2), vc = (lane & 3) ^ ((ch >> 2) & 3);
-      lds_dma16(vt8 + (int64_t)ch * p.nkp + kAttnBK * j + 16 * vc, stg[1] + kb * 1024);
+  for (int u = 0; u < kAttnDmaTile; ++u) {
+    const int r = 8 * (kAttnDmaTile * wave + u) + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+    koff[u] = (uint32_t)(r * kAttnD + 16 * c);
+    voff[u] = (uint32_t)(r * p.nkp + 16 * c);
+  }
+  const uint32_t soff = (uint32_t)(64 * wave + 16 * min(lane, 3));
+  // (The block's offset is added to the lane's in 32 bits, so every DMA is
+  // a scalar base plus one 32-bit lane offset.)
+  auto dma_blk = [&](int j, AttnStage& stg) {
+    j = min(j, p.nblk - 1);
+    const uint32_t jk = (uint32_t)(j * kAttnBK * kAttnD), jv = (uint32_t)(j * kAttnBK), js = (uint32_t)(j * kAttnD * 4);
+#pragma unroll
+    for (int u = 0; u < kAttnDmaTile; ++u) {
+      const int kb = kAttnDmaTile * wave + u;
+      lds_dma16(k8 + (koff[u] + jk), stg.k + kb * 1024);
+      lds_dma16(vt8 + (voff[u] + jv), stg.v + kb * 1024);
     }
+    if (lane < 4)
+      lds_dma16(reinterpret_cast<const int8_t*>(vsumh) + (soff + js), reinterpret_cast<int8_t*>(stg.vsum) + 64 * wave);
   };
-  // S^T of the K tile at kt: sacc[t][4 g + i] is the score of key
+  // S^T of the block in stg: s[t][4 g + i] is the score of key
   // 32 t + 8 g + 4 hh + i of the block for query fr.
-  auto scores_at = [&](const int8_t* kt, v16i (&sacc)[2]) {
-    sacc[0] = v16i{};
-    sacc[1] = v16i{};
+  auto scores = [&](const AttnStage& stg, v16i (&s)[4]) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 4; ++t) {
+      s[t] = v16i{};
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds) {
         const int r = 32 * t + fr, ck = 2 * ds + hh;
-        const v4i kf = *reinterpret_cast<const v4i*>(kt + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
-        sacc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], sacc[t], 0, 0, 0);
+        const v4i kf = *reinterpret_cast<const v4i*>(stg.k + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
+        s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[t], 0, 0, 0);
       }
-  };
-  // K tile of block j DMA'd to dst (the layout of dma_tiles).
-  auto dma_k = [&](int j, int8_t* dst) {
-#pragma unroll
-    for (int u = 0; u < kAttnDma; ++u) {
-      const int kb = kAttnDma * wave + u;
-      const int r = 8 * kb + (lane >> 3), kc = (lane & 7) ^ ((r >> 1) & 7);
-      lds_dma16(k8 + (int64_t)(kAttnBK * j + r) * kAttnD + 16 * kc, dst + kb * 1024);
     }
   };
-  // Keys of the last block past nk.
-  auto masked = [&](int j, int t, int x) { return kAttnBK * j + 32 * t + 8 * (x >> 2) + 4 * hh + (x & 3) >= p.nk; };
-  // Pass 1: the largest logit of the query, max over blocks of
-  // fp32(max(S) * c_j) (the lane's half of the keys, then the other half).
-  // It takes two key blocks per step (K only: block 2u in the K half of a
-  // stage, block 2u + 1 in its V half), halving the barriers.
-  float ml = -__builtin_inff();
-  {
-    // A full block (every key below nk): no masks, no checks.
-    auto block_max_full = [&](int j, const v16i (&s)[2]) {
-      int mx = INT32_MIN;
+  // O^T: o[ct][4 g + i] is channel 32 ct + 8 g + 4 hh + i of query fr.
+  float o[4][16];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+  for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-        for (int x = 0; x < 16; ++x) mx = max(mx, s[t][x]);
-      ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
-    };
-    auto block_max = [&](int j, const v16i (&s)[2]) {
-      int mx = INT32_MIN;
-      if (kAttnBK * (j + 1) > p.nk) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int x = 0; x < 16; ++x) mx = masked(j, t, x) ? mx : max(mx, s[t][x]);
-      } else {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int x = 0; x < 16; ++x) mx = max(mx, s[t][x]);
-      }
-      if (mx != INT32_MIN) ml = fmaxf(ml, (float)mx * (qscale * ksc[j]));
-    };
-    const int npairs = (p.nblk + 1) / 2;
-    // Every pair issues exactly two DMA instructions per wave, so the waits
-    // below count them exactly (the compiler's own wait placement then sees
-    // the same counts): past the last block it re-loads in-range blocks
-    // into a stage whose scores are never computed.
-    auto dma_pair = [&](int u, int8_t (*stg)[kAttnBK * kAttnD]) {
-      const int b0 = 2 * min(u, npairs - 1);
-      dma_k(b0, stg[0]);
-      dma_k(min(b0 + 1, p.nblk - 1), stg[1]);
-    };
-    auto pair_scores = [&](int u, int8_t (*stg)[kAttnBK * kAttnD], v16i (&s0)[2], v16i (&s1)[2]) {
-      scores_at(stg[0], s0);
-      if (2 * u + 1 < p.nblk) scores_at(stg[1], s1);
-    };
-    // Pair u lives in stage u % 3. Step u computes the scores of pair u + 1,
-    // refills stage u % 3 (whose scores step u - 1 computed) with pair
-    // u + 3, works on pair u, then waits for pair u + 2 only: each DMA has
-    // two steps of lead.
-    dma_pair(0, stage0);
-    dma_pair(1, stage1);
-    dma_pair(2, stage2);
-    wait_vm<2>();   // pairs 0 and 1 landed
-    __syncthreads();
-    v16i a0[2], a1[2], b0[2], b1[2];
-    pair_scores(0, stage0, a0, a1);
-    // Step u with pair u in stage s0 and pair u + 1 in stage s1.
-    auto step = [&](int u, int8_t (*s0)[kAttnBK * kAttnD], int8_t (*s1)[kAttnBK * kAttnD],
-                    const v16i (&c0)[2], const v16i (&c1)[2], v16i (&n0)[2], v16i (&n1)[2]) {
-      if (u + 1 < npairs) pair_scores(u + 1, s1, n0, n1);
-      dma_pair(u + 3, s0);
-      block_max(2 * u, c0);
-      if (2 * u + 1 < p.nblk) block_max(2 * u + 1, c1);
-      wait_vm<2>();   // pair u + 2 landed; pair u + 3 may still be in flight
-      lds_barrier();
-    };
-    // The same step for u <= npairs - 3: pairs u and u + 1 are whole and
-    // hold no key past nk (only the last block can), so nothing is checked.
-    auto step_full = [&](int u, int8_t (*s0)[kAttnBK * kAttnD], int8_t (*s1)[kAttnBK * kAttnD],
-                         const v16i (&c0)[2], const v16i (&c1)[2], v16i (&n0)[2], v16i (&n1)[2]) {
-      scores_at(s1[0], n0);
-      scores_at(s1[1], n1);
-      dma_pair(u + 3, s0);
-      block_max_full(2 * u, c0);
-      block_max_full(2 * u + 1, c1);
-      wait_vm<2>();
-      lds_barrier();
-    };
-    // Six steps return to stage 0 and to the first score buffers.
-    int u = 0;
-    for (; u + 8 <= npairs; u += 6) {
-      step_full(u, stage0, stage1, a0, a1, b0, b1);
-      step_full(u + 1, stage1, stage2, b0, b1, a0, a1);
-      step_full(u + 2, stage2, stage0, a0, a1, b0, b1);
-      step_full(u + 3, stage0, stage1, b0, b1, a0, a1);
-      step_full(u + 4, stage1, stage2, a0, a1, b0, b1);
-      step_full(u + 5, stage2, stage0, b0, b1, a0, a1);
-    }
-    // At most seven steps remain.
-    if (u < npairs) step(u, stage0, stage1, a0, a1, b0, b1);
-    if (u + 1 < npairs) step(u + 1, stage1, stage2, b0, b1, a0, a1);
-    if (u + 2 < npairs) step(u + 2, stage2, stage0, a0, a1, b0, b1);
-    if (u + 3 < npairs) step(u + 3, stage0, stage1, b0, b1, a0, a1);
-    if (u + 4 < npairs) step(u + 4, stage1, stage2, a0, a1, b0, b1);
-    if (u + 5 < npairs) step(u + 5, stage2, stage0, b0, b1, a0, a1);
-    if (u + 6 < npairs) step(u + 6, stage0, stage1, a0, a1, b0, b1);
-  }
-  const float m = fmaxf(ml, __shfl_xor(ml, 32, 64));
-  const float nm = kLog2_255 - m;
+    for (int x = 0; x < 16; ++x) o[ct][x] = 0.0f;
+  // Running maximum and the denominators of the lane's K-scale groups
+  // c = 2 hh (keys with i < 2) and c = 2 hh + 1.
+  float m = kMInit, d0 = 1.0f, d1 = 1.0f;
 
-  // Pass 2: P = min(255, rne(exp2(fma(S, c_j, nm)))) (v_cvt_pk_u8_f32
-  // rounds to nearest even and saturates), O^T += V^T.(P - 128)^T and
-  // sum(P - 128), exact in int32.
-  v16i oi[4];
+  auto work = [&](int j, const AttnStage& stg, const v16i (&s)[4], auto last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int kl = p.nk - kAttnBK * j;   // keys of the block below nk (LAST)
+    auto masked = [&](int t, int g, int i) { return LAST && 32 * t + 8 * g + 4 * hh + i >= kl; };
+    int mx0 = INT32_MIN, mx1 = INT32_MIN;
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) oi[ct] = v16i{};
-  int li = 0;
-  auto work = [&](int j, Stage stg, const v16i (&s)[2]) {
-    const float c = qscale * ksc[j];
-    uint32_t pw[2][4];
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = masked(t, g, i) ? INT32_MIN : s[t][4 * g + i];
+          if (i < 2) mx0 = max(mx0, v);
+          else mx1 = max(mx1, v);
+        }
+    float mt0 = (float)mx0, mt1 = (float)mx1;
+    if constexpr (LAST) {
+      mt0 = fmaxf(kMInit, mt0);
+      mt1 = fmaxf(kMInit, mt1);
+    }
+    const float ts0 = p.c0 * (qsr * ksc[4 * j + 2 * hh]);
+    const float ts1 = p.c0 * (qsr * ksc[4 * j + 2 * hh + 1]);
+    float tm = fmaxf(__builtin_fmaf(mt0, ts0, -kSU8Offset), __builtin_fmaf(mt1, ts1, -kSU8Offset));
+    tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+    const float mprev = m;
+    m = fmaxf(mprev, tm);
+    const float smaller = __builtin_amdgcn_exp2f(-fabsf(mprev - tm));
+    const float osc = mprev < tm ? smaller : 1.0f;
+    const float tsc = tm < mprev ? smaller : 1.0f;
+    if (__builtin_amdgcn_ballot_w64(osc != 1.0f) != 0) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) o[ct][x] = o[ct][x] * osc;
+      d0 = d0 * osc;
+      d1 = d1 * osc;
+    }
+    // Probabilities as u8 words (w[t][g] byte i: key 32 t + 8 g + 4 hh + i)
+    // and the denominators, 16-key tile tt = 2 t + (g >> 1) at a time.
+    uint32_t w[4][4];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+      const int t = tt >> 1, ga = 2 * (tt & 1);
+      float pf[2][4];
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const int g = ga + gg;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float sf = masked(t, g, i) ? kMaskScore : (float)s[t][4 * g + i];
+          pf[gg][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf, i < 2 ? ts0 : ts1, -tm));
+        }
+        uint32_t u = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][0], 0, 0u);
+        u = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][1], 1, u);
+        u = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][2], 2, u);
+        w[t][g] = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][3], 3, u);
+      }
+      float part0, part1;
+      if constexpr (LAST) {
+        part0 = (pf[0][0] + pf[0][1]) + (pf[1][0] + pf[1][1]);
+        part1 = (pf[0][2] + pf[0][3]) + (pf[1][2] + pf[1][3]);
+      } else {
+        part0 = (float)__builtin_amdgcn_udot4(w[t][ga], 0x00000101u,
+                                              __builtin_amdgcn_udot4(w[t][ga + 1], 0x00000101u, 0u, false), false);
+        part1 = (float)__builtin_amdgcn_udot4(w[t][ga], 0x01010000u,
+                                              __builtin_amdgcn_udot4(w[t][ga + 1], 0x01010000u, 0u, false), false);
+      }
+      d0 = __builtin_fmaf(part0, tsc, d0);
+      d1 = __builtin_fmaf(part1, tsc, d1);
+    }
+    // O^T += V^T.P^T per 32-channel tile: the signed MFMA takes P - 128 and
+    // starts from 128 * the block's code sums, so acc is P.V exactly.
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      v16i acc;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        float qv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qv[i] = __builtin_amdgcn_exp2f(__builtin_fmaf((float)s[t][4 * g + i], c, nm));
-        uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(qv[0], 0, 0u);
-        w = __builtin_amdgcn_cvt_pk_u8_f32(qv[1], 1, w);
-        w = __builtin_amdgcn_cvt_pk_u8_f32(qv[2], 2, w);
-        w = __builtin_amdgcn_cvt_pk_u8_f32(qv[3], 3, w);
-        pw[t][g] = w ^ 0x80808080u;   // P - 128 as signed bytes
-        li = __builtin_amdgcn_sdot4((int)pw[t][g], 0x01010101, li, false);
+        const int4 c4 = *reinterpret_cast<const int4*>(stg.vsum + 32 * ct + 8 * g + 4 * hh);
+        acc[4 * g] = c4.x; acc[4 * g + 1] = c4.y; acc[4 * g + 2] = c4.z; acc[4 * g + 3] = c4.w;
       }
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const v4i pf = {(int)pw[t][0], (int)pw[t][1], (int)pw[t][2], (int)pw[t][3]};
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
+      for (int t = 0; t < 4; ++t) {
         const int r = 32 * ct + fr, ck = 2 * t + hh;
-        const v4i vf = *reinterpret_cast<const v4i*>(stg[1] + r * kAttnBK + ((ck ^ ((r >> 2) & 3)) << 4));
-        oi[ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pf, oi[ct], 0, 0, 0);
+        const v4i vf = *reinterpret_cast<const v4i*>(stg.v + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
+        const v4i pfr = {(int)(w[t][0] ^ 0x80808080u), (int)(w[t][1] ^ 0x80808080u), (int)(w[t][2] ^ 0x80808080u),
+                         (int)(w[t][3] ^ 0x80808080u)};
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pfr, acc, 0, 0, 0);
       }
+#pragma unroll
+      for (int x = 0; x < 16; ++x) o[ct][x] = __builtin_fmaf((float)acc[x], tsc, o[ct][x]);
     }
   };
-  {
-    // Block j lives in stage j % 4. Step j computes the scores of block
-    // j + 1, refills stage (j + 3) % 4 (read by steps j - 2 and j - 1) with
-    // block j + 3, works on block j, then waits for block j + 2 only. Every
-    // block issues exactly two DMA instructions per wave (past the last
-    // block an in-range block is re-loaded into a stage never read), so the
-    // waits count exactly.
-    auto dma_blk = [&](int j, Stage stg) { dma_tiles(min(j, p.nblk - 1), stg); };
-    dma_blk(0, stage0);
-    dma_blk(1, stage1);
-    dma_blk(2, stage2);
-    wait_vm<2>();   // blocks 0 and 1 landed
-    __syncthreads();
-    v16i sa[2], sb[2];
-    scores_at(stage0[0], sa);
-    auto step = [&](int j, Stage s0, Stage s1, Stage s3, const v16i (&cur)[2], v16i (&nxt)[2]) {
-      if (j + 1 < p.nblk) scores_at(s1[0], nxt);
-      dma_blk(j + 3, s3);
-      work(j, s0, cur);
-      wait_vm<2>();   // block j + 2 landed; block j + 3 may still be in flight
-      lds_barrier();
-    };
-    // The same step when block j + 1 exists (no check).
-    auto step_full = [&](int j, Stage s0, Stage s1, Stage s3, const v16i (&cur)[2], v16i (&nxt)[2]) {
-      scores_at(s1[0], nxt);
-      dma_blk(j + 3, s3);
-      work(j, s0, cur);
-      wait_vm<2>();
-      lds_barrier();
-    };
-    int j = 0;
-    for (; j + 5 <= p.nblk; j += 4) {
-      step_full(j, stage0, stage1, stage3, sa, sb);
-      step_full(j + 1, stage1, stage2, stage0, sb, sa);
-      step_full(j + 2, stage2, stage3, stage1, sa, sb);
-      step_full(j + 3, stage3, stage0, stage2, sb, sa);
-    }
-    // At most four steps remain.
-    if (j < p.nblk) step(j, stage0, stage1, stage3, sa, sb);
-    if (j + 1 < p.nblk) step(j + 1, stage1, stage2, stage0, sb, sa);
-    if (j + 2 < p.nblk) step(j + 2, stage2, stage3, stage1, sa, sb);
-    if (j + 3 < p.nblk) step(j + 3, stage3, stage0, stage2, sb, sa);
+  using NotLast = std::false_type;
+  using Last = std::true_type;
+  // Step j: block j landed (blocks j + 1 and j + 2 may be in flight) and
+  // every wave is past step j - 1; score block j, refill step j - 1's stage
+  // with block j + 3, then the softmax update and P.V.
+  auto step = [&](int j, const AttnStage& cur, AttnStage& refill, auto last_tag) {
+    wait_vm<2 * kAttnDmaBlk>();
+    lds_barrier();
+    v16i s[4];
+    scores(cur, s);
+    dma_blk(j + 3, refill);
+    work(j, cur, s, last_tag);
+  };
+  dma_blk(0, st0);
+  dma_blk(1, st1);
+  dma_blk(2, st2);
+  __syncthreads();   // the K scales are in LDS (the DMA waits come with the steps)
+  const int nfull = p.nblk - 1;   // blocks before the last
+  int j = 0;
+  for (; j + 4 <= nfull; j += 4) {
+    step(j, st0, st3, NotLast{});
+    step(j + 1, st1, st0, NotLast{});
+    step(j + 2, st2, st1, NotLast{});
+    step(j + 3, st3, st2, NotLast{});
   }
-  // Each lane summed P - 128 over its 32 keys of every block: sum(P) puts
-  // the 128s back. Keys past nk in the last block have all-zero K and V^T
-  // codes: each scored 0, added nothing to P.V and the same P =
-  // cvt_pk_u8(exp2(fma(0, c, nm))) to this lane's sum; take them out exactly.
-  li += 128 * 32 * p.nblk;
-  {
-    const int jl = p.nblk - 1, kl = p.nk - kAttnBK * jl;
-    int npad = 0;
-#pragma unroll
-    for (int x = 0; x < 32; ++x) npad += (32 * (x >> 4) + 8 * ((x >> 2) & 3) + 4 * hh + (x & 3)) >= kl;
-    if (npad) {
-      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(0.0f, qscale * ksc[jl], nm));
-      li -= npad * (int)(__builtin_amdgcn_cvt_pk_u8_f32(e, 0, 0u) & 0xffu);
-    }
+  if (j < nfull) step(j, st0, st3, NotLast{});
+  if (j + 1 < nfull) step(j + 1, st1, st0, NotLast{});
+  if (j + 2 < nfull) step(j + 2, st2, st1, NotLast{});
+  switch (nfull - j) {
+    case 0: step(nfull, st0, st3, Last{}); break;
+    case 1: step(nfull, st1, st0, Last{}); break;
+    case 2: step(nfull, st2, st1, Last{}); break;
+    default: step(nfull, st3, st2, Last{}); break;
   }
-  const float l = (float)(li + __shfl_xor(li, 32, 64));
+  wait_vm<0>();   // no DMA may still target this workgroup's LDS at exit
+  // (d0 + d1) + (d2 + d3): each half-wave holds one pair.
+  const float dpair = d0 + d1;
+  const float rcp = 1.0f / (dpair + __shfl_xor(dpair, 32, 64));
   if (q0 + fr >= p.nq) return;
   const int64_t orow = p.ost.at(bh, q0 + fr);
   const float* vsc = p.vs + bh * kAttnD;
-  const int* vsm = p.vsum + bh * kAttnD;   // O = O' + 128 * vsum, exact in int64
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -644,11 +601,9 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       const int c0 = 32 * ct + 8 * g + 4 * hh;
       const float4 s4 = *reinterpret_cast<const float4*>(vsc + c0);
       const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-      const int4 m4 = *reinterpret_cast<const int4*>(vsm + c0);
-      const int vm[4] = {m4.x, m4.y, m4.z, m4.w};
       float y[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = ((float)((int64_t)oi[ct][4 * g + i] + 128 * (int64_t)vm[i]) * sv[i]) / l;
+      for (int i = 0; i < 4; ++i) y[i] = (o[ct][4 * g + i] * rcp) * sv[i];
       if constexpr (OUT == kF32) {
         *reinterpret_cast<float4*>(reinterpret_cast<float*>(p.out) + orow + c0) = make_float4(y[0], y[1], y[2], y[3]);
       } else {
@@ -704,8 +659,8 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   W8A8_REQUIRE(a->in_dtype == W8A8_F16 || a->in_dtype == W8A8_F32, "w8a8_attention_prepare: in_dtype not F16/F32");
   W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention_prepare: head dimension %d != 128", a->d);
   W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention_prepare: empty problem");
-  W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536,
-               "w8a8_attention_prepare: sizes out of range");
+  W8A8_REQUIRE(a->nq < (1 << 24) && a->nk <= kAttnMaxBlk * kAttnBK && a->b * a->h < 65536,
+               "w8a8_attention_prepare: sizes out of range (at most 131072 keys)");
   W8A8_REQUIRE(a->q && a->k && a->v && a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->vsum &&
                    a->workspace,
                "w8a8_attention_prepare: null buffer");
@@ -728,25 +683,23 @@ extern "C" int w8a8_attention_prepare(const W8A8AttnPrepareArgs* a) {
   p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);
   p.nkp = p.nblk * kAttnBK;
   p.chunks = (int)attn_chunks(a->nk);
-  p.c0 = a->sm_scale * kLog2e;
   p.q8 = a->q8; p.qs = a->qs; p.k8 = a->k8; p.ks = a->ks; p.vt8 = a->vt8; p.vs = a->vs; p.vsum = a->vsum;
   const int64_t bh = a->b * a->h;
   float* ws = reinterpret_cast<float*>(a->workspace);
   p.part_sum = ws;
   p.part_max = ws + bh * p.chunks * kAttnD;
   p.kmean = ws + 2 * bh * p.chunks * kAttnD;
-  p.vrcp = p.kmean + bh * kAttnD;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   const int qblocks = (p.nq + kAttnBK - 1) / kAttnBK;
   const dim3 gstat((unsigned)((p.chunks + 15) / 16), (unsigned)bh), gq((unsigned)max(qblocks, p.nblk), (unsigned)bh);
   if (a->in_dtype == W8A8_F16) {
     hipLaunchKernelGGL(attn_stats_kernel<kF16>, gstat, dim3(256), 0, s, p);
     hipLaunchKernelGGL(attn_finalize_kernel, dim3((unsigned)bh), dim3(128), 0, s, p);
-    hipLaunchKernelGGL(attn_quant_kernel<kF16>, gq, dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_quant_kernel<kF16>, gq, dim3(512), 0, s, p);
   } else {
     hipLaunchKernelGGL(attn_stats_kernel<kF32>, gstat, dim3(256), 0, s, p);
     hipLaunchKernelGGL(attn_finalize_kernel, dim3((unsigned)bh), dim3(128), 0, s, p);
-    hipLaunchKernelGGL(attn_quant_kernel<kF32>, gq, dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_quant_kernel<kF32>, gq, dim3(512), 0, s, p);
   }
   return launch_status("w8a8_attention_prepare");
 }
@@ -759,11 +712,12 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   W8A8_REQUIRE(a->out_dtype == W8A8_F16 || a->out_dtype == W8A8_F32, "w8a8_attention: out_dtype not F16/F32");
   W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention: head dimension %d != 128", a->d);
   W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention: empty problem");
-  W8A8_REQUIRE(a->nq < (1 << 24) && a->nk < (1 << 24) && a->b * a->h < 65536, "w8a8_attention: sizes out of range");
-  if (a->nk > (1 << 17)) {   // the int32 sums of (P - 128).V hold nk * 128 * 127
-    set_error("w8a8_attention: at most 131072 keys (exact int32 accumulation)");
+  W8A8_REQUIRE(a->nq < (1 << 24) && a->b * a->h < 65536, "w8a8_attention: sizes out of range");
+  if (a->nk > kAttnMaxBlk * kAttnBK) {   // the K scales of a head are staged in LDS
+    set_error("w8a8_attention: at most %d keys", kAttnMaxBlk * kAttnBK);
     return W8A8_ERR_UNSUPPORTED;
   }
+  W8A8_REQUIRE(a->sm_scale > 0.0f, "w8a8_attention: sm_scale must be positive");
   W8A8_REQUIRE(a->q8 && a->qs && a->k8 && a->ks && a->vt8 && a->vs && a->vsum && a->out,
                "w8a8_attention: null buffer");
   W8A8_REQUIRE(aligned16(a->q8) && aligned16(a->k8) && aligned16(a->vt8) && aligned16(a->vs) && aligned16(a->vsum) &&
@@ -780,6 +734,7 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   p.nq = (int)a->nq; p.nk = (int)a->nk;
   p.nblk = (int)((a->nk + kAttnBK - 1) / kAttnBK);
   p.nkp = p.nblk * kAttnBK;
+  p.c0 = a->sm_scale * kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   const dim3 grid((unsigned)((p.nq + kAttnBQ - 1) / kAttnBQ), (unsigned)(a->b * a->h));
   if (a->out_dtype == W8A8_F32) hipLaunchKernelGGL(attention_kernel<kF32>, grid, dim3(64 * kAttnWaves), 0, s, p);

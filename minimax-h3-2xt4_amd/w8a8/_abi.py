@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -83,7 +83,7 @@ class AttnPrepareArgs(ctypes.Structure):
 class AttentionArgs(ctypes.Structure):
     _fields_ = [('struct_size', _c.c_uint32), ('out_dtype', _c.c_int32), ('q8', _p), ('qs', _p), ('k8', _p),
                 ('ks', _p), ('vt8', _p), ('vs', _p), ('vsum', _p), ('b', _c.c_int64), ('h', _c.c_int64), ('nq', _c.c_int64),
-                ('nk', _c.c_int64), ('d', _c.c_int32), ('reserved', _c.c_int32), ('out', _p),
+                ('nk', _c.c_int64), ('d', _c.c_int32), ('sm_scale', _c.c_float), ('out', _p),
                 ('out_strides', _c.c_int64 * 3), ('stream', _p)]
 
 

@@ -5,14 +5,12 @@ Same names as the reference's calls into comfy-kitchen 0.2.37
 ``int8_attention_from_prequantized``; patches/kitchen_attention.py:227-238:
 ``int8_attention(q, k, v, *, scale=None, attn_mask=None)``), for 128-wide
 heads without masks. q, k, v are [batch, heads, tokens, 128] fp16 or fp32; the
-output has q's dtype. Two libw8a8 calls: the preparation (key centering,
-per-token Q and per-64-key K scales, per-channel V scales, INT8 codes, V
-transposed) and the attention kernel (INT8 MFMA for Q.K^T and P.V, two passes:
-the row maxima, then u8 probabilities relative to them with FP32 scales).
-The reference's kernel (kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh)
-is a one-pass online softmax with u8 probabilities relative to each key tile's
-maximum and per-thread Q/K scale groups; this scheme is close to it on short
-sequences and loses accuracy on long ones (the oracle records both).
+output has q's dtype. Two libw8a8 calls with the numerics of the reference's
+vendored kernel (kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh) for
+128-key blocks: the preparation (per-thread-group Q and K scales, K centred,
+per-channel V scales, INT8 codes, V transposed, per-block V code sums) and the
+attention kernel (INT8 MFMA for Q.K^T and P.V, one online-softmax pass with u8
+probabilities relative to each key block's maximum and FP32 rescaling).
 """
 from dataclasses import dataclass
 

@@ -456,7 +456,7 @@ def dequantize(acc, row_scale, col_scale, *, epilogue=EPI_ROW, out_dtype=torch.f
     return out
 
 
-ATTN_BLOCK_K = 64
+ATTN_BLOCK_K = 128
 
 
 def _row_strides(t):
@@ -472,10 +472,13 @@ def _row_strides(t):
 
 def attention_prepare(q, k, v, *, sm_scale=None):
     """INT8 operands of the attention for q [B, H, Nq, 128], k, v [B, H, Nk,
-    128] (fp16 or fp32). The inputs are read in place when their channels
-    are contiguous and their strides 16-byte multiples (e.g. transposed views
-    of a packed QKV projection), else from contiguous copies. Returns a dict
-    with q8, qs, k8, ks, vt8, vs, vsum (device tensors) and the shape."""
+    128] (fp16 or fp32), for the reference kernel's scheme with 128-key
+    blocks. The inputs are read in place when their channels are contiguous
+    and their strides 16-byte multiples (e.g. transposed views of a packed
+    QKV projection), else from contiguous copies. Returns a dict with q8, qs
+    (each row's group scale), k8, ks ([B, H, Nkp / 128, 4]: four group
+    scales per block), vt8, vs, vsum ([B, H, Nkp / 128, 128]: 128 times each
+    block's V code sums), all device tensors, the shape and sm_scale."""
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError('q, k, v must be [batch, heads, tokens, dim]')
     _device(q, k, v)
@@ -501,11 +504,11 @@ def attention_prepare(q, k, v, *, sm_scale=None):
     prep = dict(q8=torch.empty((b, h, nq, d), dtype=torch.int8, device=dev),
                 qs=torch.empty((b, h, nq), dtype=torch.float32, device=dev),
                 k8=torch.empty((b, h, nkp, d), dtype=torch.int8, device=dev),
-                ks=torch.empty((b, h, nkp // ATTN_BLOCK_K), dtype=torch.float32, device=dev),
+                ks=torch.empty((b, h, nkp // ATTN_BLOCK_K, 4), dtype=torch.float32, device=dev),
                 vt8=torch.empty((b, h, d, nkp), dtype=torch.int8, device=dev),
                 vs=torch.empty((b, h, d), dtype=torch.float32, device=dev),
-                vsum=torch.empty((b, h, d), dtype=torch.int32, device=dev),
-                shape=(b, h, nq, nk, d))
+                vsum=torch.empty((b, h, nkp // ATTN_BLOCK_K, d), dtype=torch.int32, device=dev),
+                shape=(b, h, nq, nk, d), sm_scale=scale)
     with torch.cuda.device(dev):
         nbytes = int(_abi.load().w8a8_attention_workspace_size(b, h, nk))
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -536,7 +539,7 @@ def attention(prep, *, out_dtype=torch.float16, out=None):
     args = _abi.AttentionArgs(out_dtype=_abi.DTYPE_CODE[out_dtype], q8=q8.data_ptr(), qs=prep['qs'].data_ptr(),
                               k8=prep['k8'].data_ptr(), ks=prep['ks'].data_ptr(), vt8=prep['vt8'].data_ptr(),
                               vs=prep['vs'].data_ptr(), vsum=prep['vsum'].data_ptr(), b=b, h=h, nq=nq, nk=nk, d=d,
-                              out=out.data_ptr(),
+                              sm_scale=prep['sm_scale'], out=out.data_ptr(),
                               out_strides=_row_strides(out),
                               stream=_abi.stream_of(q8))
     _abi.call('w8a8_attention', args)

@@ -3,45 +3,17 @@
 The reference routes DiT attention through comfy-kitchen 0.2.37's INT8
 attention (patches/h3_operator_policy.py:153-209: ``prequantize_int8_attention``
 then ``int8_attention_from_prequantized``; patches/kitchen_attention.py:227-238
-and the launcher patches/kitchen_attention_native/attention.cu:20-38, which
+and the launcher patches/kitchen_attention_native/attention.cu:20-66, which
 instantiates the vendored SageAttention kernel ``qk_int_sv_i8_attn_kernel`` of
-kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh and attn_utils.cuh).
-That kernel's arithmetic is restated at the end of this module
-(``kitchen_prepare`` / ``kitchen_attention``); Kitchen's quantizer is not in
-the reference (comfy-kitchen is not installed), so the restatement assumes
-the SageAttention quantizer and is **parity unpinned** for those bits and for
-CUDA's approximate exp2 / reciprocal. This build's GPU kernel implements a
-different scheme, restated first (``prepare`` / ``attention``): two passes
-instead of one online pass, u8 probabilities relative to the row's largest
-logit instead of relative to each 64-key tile's largest logit, per-token Q
-and per-64-key K scales instead of the kernel's per-thread groups. The GPU
-feeds P - 128 to its signed INT8 MFMA and adds 128 * (sum over keys of v8)
-per channel afterwards, which gives the same integer P . v8. Its error
-against exact attention grows with the key count (max-abs error over max
-|output| in tests/test_oracle.py, against the restated reference scheme):
-
-prepare (exact, checked bit for bit):
-  * K is centred per channel: mean[d] = (sum over tokens of k[t][d], fp32,
-    sequential inside 256-token chunks, then over the chunks) / Nk; kc =
-    fp32(k - mean). Centering shifts every logit of a query by the same
-    amount, so the softmax is unchanged.
-  * Q: per-token scale s = max(amax * fp32(1/127), 1e-30), q8 = sat(rne(q / s))
-    (the framework's row quantizer); the stored scale is fp32(s * c0) with
-    c0 = fp32(sm_scale * log2(e)), so logits come out in the exp2 domain.
-  * K: one scale per 64-key block (amax over the block's 64 x 128 centred
-    values), k8 = sat(rne(kc / s)); keys past Nk are zero.
-  * V: one scale per channel (amax over all tokens), v8 = sat(rne(v / s)),
-    and vsum = sum over the keys of v8 per channel (the GPU's P - 128
-    correction).
-
-attention (checked within a tolerance: the GPU's exp2 is the hardware
-approximation), per query:
-    S = q8 . k8 (int32, exact) and c_j = fp32(qs * ks[j]) for key block j;
-    m = max over blocks of fp32(max(S_j) * c_j), the largest logit;
-    nm = fp32(log2(255) - m);
-    P = min(255, rne(exp2(fma(S, c_j, nm)))), integers 0..255, 0 past Nk;
-    acc = P . v8 and l = sum(P), exact integers;
-    out = fp32(fp32(f32(acc) * vs) / f32(l)).
+kitchen_attention_native/vendor/qk_int_sv_i8_cuda.cuh and attn_utils.cuh for
+key blocks of CTA_K = 64 or 128, as Kitchen's packer chooses). That kernel's
+arithmetic is restated here (``kitchen_prepare`` / ``kitchen_attention``),
+and the GPU kernel implements it for CTA_K = 128. Kitchen's quantizer is not
+in the reference (comfy-kitchen is not installed), so the restatement assumes
+the SageAttention quantizer, with the key mean in a fixed fp32 order
+(``key_mean``), and is **parity unpinned** for those bits and for CUDA's
+approximate exp2 / reciprocal. ``reference_attention`` is exact softmax
+attention in float64, the unquantized target both are measured against.
 """
 import numpy as np
 
@@ -49,8 +21,6 @@ from .w8a8_oracle import R127, SCALE_FLOOR, quantize_rows
 
 F32 = np.float32
 LOG2E = F32(1.4426950408889634)
-L255 = F32(np.log2(255.0))
-BLOCK_K = 64
 CHUNK = 256
 
 
@@ -84,71 +54,6 @@ def key_mean(k):
             part = part + k[..., t, :]
         total = total + part
     return (total / F32(n)).astype(F32)
-
-
-def prepare(q, k, v, sm_scale=None):
-    """INT8 operands of the attention: dict of q8, qs, k8, ks, vt8, vs, vsum
-    (and kmean), for q [B, H, Nq, D], k, v [B, H, Nk, D] (any float dtype)."""
-    q, k, v = _f32(q), _f32(k), _f32(v)
-    b, h, nq, d = q.shape
-    nk = k.shape[2]
-    nkp = -(-nk // BLOCK_K) * BLOCK_K
-    scale = default_scale(d) if sm_scale is None else F32(sm_scale)
-    c0 = F32(scale * LOG2E)
-    q8, qsc = quantize_rows(q.reshape(-1, d))
-    qs = (qsc * c0).astype(F32).reshape(b, h, nq)
-    q8 = q8.reshape(b, h, nq, d)
-    mean = key_mean(k)
-    kc = np.zeros((b, h, nkp, d), F32)
-    kc[:, :, :nk] = (k - mean[:, :, None, :]).astype(F32)
-    blocks = kc.reshape(b, h, nkp // BLOCK_K, BLOCK_K * d)
-    amax = np.abs(blocks).max(-1)
-    ks = np.maximum(amax * R127, SCALE_FLOOR).astype(F32)
-    with np.errstate(over='ignore', invalid='ignore', divide='ignore'):
-        k8 = np.clip(np.rint(blocks / ks[..., None]), -128, 127).astype(np.int8).reshape(b, h, nkp, d)
-    vmax = np.abs(v).max(2)
-    vs = np.maximum(vmax * R127, SCALE_FLOOR).astype(F32)
-    v8 = np.zeros((b, h, nkp, d), np.int8)
-    with np.errstate(over='ignore', invalid='ignore', divide='ignore'):
-        v8[:, :, :nk] = np.clip(np.rint(v / vs[:, :, None, :]), -128, 127).astype(np.int8)
-    perm = perm32()
-    vt8 = v8.reshape(b, h, nkp // 32, 32, d)[:, :, :, perm, :].reshape(b, h, nkp, d).transpose(0, 1, 3, 2).copy()
-    vsum = v8.astype(np.int64).sum(2).astype(np.int32)     # per channel, exact (|sum| < 2^31)
-    return dict(q8=q8, qs=qs, k8=k8, ks=ks, vt8=vt8, vs=vs, vsum=vsum, kmean=mean, v8=v8, nk=nk)
-
-
-def attention(prep, out_dtype='f32'):
-    """INT8 attention from prepared operands (module docstring).
-    Returns [B, H, Nq, D] in out_dtype ('f32' or 'f16')."""
-    q8 = prep['q8'].astype(np.int64)
-    k8 = prep['k8'].astype(np.int64)
-    v8 = prep['v8'].astype(np.int64)
-    qs, ks, vs, nk = prep['qs'], prep['ks'], prep['vs'], prep['nk']
-    b, h, nq, d = q8.shape
-    nkp = k8.shape[2]
-    nblk = nkp // BLOCK_K
-    valid = np.arange(nkp) < nk
-    out = np.zeros((b, h, nq, d), F32)
-    for bi in range(b):
-        for hi in range(h):
-            s = q8[bi, hi] @ k8[bi, hi].T                                  # [nq, nkp] exact
-            c = (qs[bi, hi][:, None] * ks[bi, hi][None, :]).astype(F32)   # [nq, nblk]
-            cfull = np.repeat(c, BLOCK_K, axis=1)
-            smask = np.where(valid[None, :], s, np.iinfo(np.int64).min)
-            mblk = smask.reshape(nq, nblk, BLOCK_K).max(-1)
-            with np.errstate(over='ignore', invalid='ignore'):
-                mj = np.where(mblk > np.iinfo(np.int64).min, (mblk.astype(F32) * c).astype(F32), -np.inf)
-                m = mj.max(1).astype(F32)
-                nm = (L255 - m).astype(F32)
-                e = (s.astype(np.float64) * cfull.astype(np.float64) + nm[:, None]).astype(F32)
-                p = np.exp2(e).astype(F32)
-            pi = np.where(valid[None, :], np.minimum(np.rint(p), 255), 0).astype(np.int64)
-            acc = pi @ v8[bi, hi]
-            l = pi.sum(1).astype(F32)
-            out[bi, hi] = ((acc.astype(F32) * vs[bi, hi][None, :]).astype(F32) / l[:, None]).astype(F32)
-    if out_dtype == 'f16':
-        return out.astype(np.float16)
-    return out
 
 
 def reference_attention(q, k, v, sm_scale=None):
@@ -201,22 +106,31 @@ def reference_attention(q, k, v, sm_scale=None):
 # Parity unpinned: (1) Kitchen's quantizer (prequantize_int8_attention) is
 # absent from the reference; kitchen_prepare assumes the SageAttention
 # per-thread quantizer (amax / 127 per group, round half away from zero, K
-# centred by its per-channel mean, V per channel). (2) ex2.approx.ftz and
+# centred by its per-channel mean, V per channel; scale = amax / 127 + 1e-7). (2) ex2.approx.ftz and
 # rcp.approx are CUDA hardware approximations; exact exp2 and 1/d stand in.
 # (3) The fp32 updates d += den * ts and O *= o_scale are taken as nvcc
 # emits them by default (d += den * ts contracted to one fma).
 # --------------------------------------------------------------------------
 S_U8_OFFSET = F32(7.9943534)
+# SageAttention's per-thread quantizers take scale = amax / 127 + 1e-7, so no
+# scale is zero (an all-padding K group of the last block would otherwise
+# zero the score scale that masks its keys).
+SCALE_EPS = F32(1e-7)
 
 
 def _round_half_away(x):
     return np.where(x >= 0, np.floor(x + 0.5), np.ceil(x - 0.5))
 
 
-def kitchen_prepare(q, k, v, cta_k=64):
+def kitchen_prepare(q, k, v, cta_k=64, sm_scale=None):
     """INT8 operands in the layout qk_int_sv_i8_attn_kernel reads, with one
     effective scale per query row (qs) and per key (ks); see the section
-    comment for what is assumed of Kitchen's quantizer."""
+    comment for what is assumed of Kitchen's quantizer. Also the layouts the
+    GPU kernel reads: ksg [B, H, Nkp / CTA_K, 4] (the four K scales of each
+    block, group c = (key mod 8) // 2), vt8 [B, H, D, Nkp] (V^T with key
+    perm32()[p] of each 32-key group at position p) and vsum128
+    [B, H, Nkp / CTA_K, D] (128 times each block's sum of V codes per
+    channel: the GPU's signed MFMA takes P - 128)."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     b, h, nq, d = q.shape
     nk = k.shape[2]
@@ -224,27 +138,41 @@ def kitchen_prepare(q, k, v, cta_k=64):
     qp = np.zeros((b, h, nq32, d), F32)
     qp[:, :, :nq] = q
     g = qp.reshape(b, h, nq32 // 32, 4, 8, d)                  # row = 32 G + 8 i + j
-    qgs = (np.abs(g).max(axis=(3, 5)) / F32(127)).astype(F32)  # [b, h, G, 8]
-    safe = np.where(qgs > 0, qgs, F32(1))
-    q8 = np.clip(_round_half_away(g / safe[:, :, :, None, :, None]), -128, 127).astype(np.int8)
+    qgs = (np.abs(g).max(axis=(3, 5)) / F32(127) + SCALE_EPS).astype(F32)  # [b, h, G, 8]
+    q8 = np.clip(_round_half_away(g / qgs[:, :, :, None, :, None]), -128, 127).astype(np.int8)
     q8 = q8.reshape(b, h, nq32, d)[:, :, :nq]
     qs = np.broadcast_to(qgs[:, :, :, None, :], (b, h, nq32 // 32, 4, 8)).reshape(b, h, nq32)[:, :, :nq]
-    mean = (k.astype(np.float64).sum(2) / nk).astype(F32)
+    mean = key_mean(k)
     nkp = -(-nk // cta_k) * cta_k
     kc = np.zeros((b, h, nkp, d), F32)
     kc[:, :, :nk] = (k - mean[:, :, None, :]).astype(F32)
     kb = kc.reshape(b, h, nkp // cta_k, cta_k // 8, 4, 2, d)    # key = cta_k B + 8 t + 2 c + e
-    kgs = (np.abs(kb).max(axis=(3, 5, 6)) / F32(127)).astype(F32)   # [b, h, B, 4]
-    safe = np.where(kgs > 0, kgs, F32(1))
-    k8 = np.clip(_round_half_away(kb / safe[:, :, :, None, :, None, None]), -128, 127).astype(np.int8)
+    kgs = (np.abs(kb).max(axis=(3, 5, 6)) / F32(127) + SCALE_EPS).astype(F32)   # [b, h, B, 4]
+    k8 = np.clip(_round_half_away(kb / kgs[:, :, :, None, :, None, None]), -128, 127).astype(np.int8)
     k8 = k8.reshape(b, h, nkp, d)
     ks = np.broadcast_to(kgs[:, :, :, None, :, None], kb.shape[:-1]).reshape(b, h, nkp)
-    vs = (np.abs(v).max(2) / F32(127)).astype(F32)
-    safe = np.where(vs > 0, vs, F32(1))
+    vs = (np.abs(v).max(2) / F32(127) + SCALE_EPS).astype(F32)
     v8 = np.zeros((b, h, nkp, d), np.int8)
-    v8[:, :, :nk] = np.clip(_round_half_away(v / safe[:, :, None, :]), -128, 127).astype(np.int8)
+    v8[:, :, :nk] = np.clip(_round_half_away(v / vs[:, :, None, :]), -128, 127).astype(np.int8)
+    perm = perm32()
+    vt8 = v8.reshape(b, h, nkp // 32, 32, d)[:, :, :, perm, :].reshape(b, h, nkp, d).transpose(0, 1, 3, 2).copy()
+    vsum128 = (v8.astype(np.int32).reshape(b, h, nkp // cta_k, cta_k, d).sum(3) * 128).astype(np.int32)
+    scale = default_scale(d) if sm_scale is None else F32(sm_scale)
     return dict(q8=q8, qs=np.ascontiguousarray(qs), k8=k8, ks=np.ascontiguousarray(ks), v8=v8, vs=vs, nk=nk,
-                cta_k=cta_k)
+                cta_k=cta_k, ksg=np.ascontiguousarray(kgs), vt8=vt8, vsum128=vsum128, kmean=mean,
+                sm_scale=scale)
+
+
+# The key block of the GPU kernel (the reference launcher's CTA_K = 128) and
+# the prepared tensors it reads.
+GPU_CTA_K = 128
+GPU_OPERANDS = ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum')
+
+
+def gpu_operands(prep):
+    """kitchen_prepare's tensors under the GPU preparation's names and layouts."""
+    return dict(q8=prep['q8'], qs=prep['qs'], k8=prep['k8'], ks=prep['ksg'], vt8=prep['vt8'], vs=prep['vs'],
+                vsum=prep['vsum128'])
 
 
 def _exp2(x):
@@ -254,7 +182,8 @@ def _exp2(x):
 
 def kitchen_attention(prep, sm_scale=None):
     """qk_int_sv_i8_attn_kernel's arithmetic (section comment) on
-    kitchen_prepare's operands: [B, H, Nq, D] fp32."""
+    kitchen_prepare's operands: [B, H, Nq, D] fp32 (sm_scale defaults to the
+    one kitchen_prepare recorded)."""
     from .w8a8_oracle import fma_f32
     q8 = prep['q8'].astype(np.int64)
     k8 = prep['k8'].astype(np.int64)
@@ -263,7 +192,7 @@ def kitchen_attention(prep, sm_scale=None):
     b, h, nq, d = q8.shape
     nkp = k8.shape[2]
     nblk = nkp // ck
-    c0 = F32(F32(default_scale(d) if sm_scale is None else sm_scale) * LOG2E)
+    c0 = F32(F32(prep.get('sm_scale', default_scale(d)) if sm_scale is None else sm_scale) * LOG2E)
     key = np.arange(ck)
     thread = (key % 8) // 2                      # the quad thread holding each key of a block
     tile = key // 16

@@ -90,14 +90,15 @@ def fixtures():
     gk = (rng.random(128) + 0.5).astype(np.float32)
     rq, rk = o.rms_rope(packed, freqs, gq, gk, 2, 96, eps=1e-6)
     out['rms_rope'] = dict(packed=packed, freqs=freqs, q_gain=gq, k_gain=gk, q=rq, k=rk)
-    # 9. INT8 attention: prepared operands (exact) and the oracle output
+    # 9. INT8 attention (the reference kernel's scheme, 128-key blocks):
+    # prepared operands (exact) and the oracle output
     from oracle import int8_attention as oa
     qa = rng.standard_normal((1, 2, 37, 128)).astype(np.float16)
     ka = (rng.standard_normal((1, 2, 70, 128)) + 0.5).astype(np.float16)
     va = rng.standard_normal((1, 2, 70, 128)).astype(np.float16)
-    prep = oa.prepare(qa.astype(np.float32), ka.astype(np.float32), va.astype(np.float32))
-    out['attention'] = dict(q=qa, k=ka, v=va, **{n: prep[n] for n in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum')},
-                            out=oa.attention(prep, out_dtype='f32'))
+    prep = oa.kitchen_prepare(qa.astype(np.float32), ka.astype(np.float32), va.astype(np.float32),
+                              cta_k=oa.GPU_CTA_K)
+    out['attention'] = dict(q=qa, k=ka, v=va, **oa.gpu_operands(prep), out=oa.kitchen_attention(prep))
     return out
 
 

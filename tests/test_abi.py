@@ -134,10 +134,11 @@ def test_attention_argument_checks():
     _expect_invalid('w8a8_attention_prepare', _abi.AttnPrepareArgs(**{**base, 'q_strides': (0, -128, 128)}),
                     'multiples of 16 bytes')
     att = dict(struct_size=ctypes.sizeof(_abi.AttentionArgs), out_dtype=_abi.F16, q8=4096, qs=8192, k8=12288,
-               ks=16384, vt8=20480, vs=24576, vsum=26624, b=1, h=2, nq=100, nk=300, d=128, out=28672,
-               out_strides=(0, 128, 256))
+               ks=16384, vt8=20480, vs=24576, vsum=26624, b=1, h=2, nq=100, nk=300, d=128, sm_scale=0.088,
+               out=28672, out_strides=(0, 128, 256))
     _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out_dtype': _abi.I32}), 'out_dtype')
     _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out': None}), 'null')
+    _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'sm_scale': 0.0}), 'sm_scale')
     _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out_strides': (0, 128, 260)}), '16 bytes')
     # Rows overlap: the heads interleave with a token stride of one row.
     _expect_invalid('w8a8_attention', _abi.AttentionArgs(**{**att, 'out_strides': (0, 128, 128)}), 'overlap')

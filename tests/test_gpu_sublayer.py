@@ -66,16 +66,17 @@ def test_dit_attention_sublayer(gpu, rows, hidden, heads, rot):
     # stage 3: the attention operands from the packed rows, bit for bit; the
     # output within the hardware exp2 tolerance of the oracle
     heads_first = [np.ascontiguousarray(t.astype(np.float32).transpose(1, 0, 2))[None] for t in (qo, ko, vo)]
-    oprep = oa.prepare(*heads_first)
+    oprep = oa.kitchen_prepare(*heads_first, cta_k=oa.GPU_CTA_K)
+    ops = oa.gpu_operands(oprep)
     prep = kernels.attention_prepare(q.transpose(0, 1)[None], k.transpose(0, 1)[None], v.transpose(0, 1)[None])
-    for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum'):
+    for name in oa.GPU_OPERANDS:
         got = np_of(prep[name])
         if got.dtype == np.float32:
-            assert np.array_equal(got.view(np.uint32), oprep[name].view(np.uint32)), name
+            assert np.array_equal(got.view(np.uint32), ops[name].view(np.uint32)), name
         else:
-            assert np.array_equal(got, oprep[name]), name
+            assert np.array_equal(got, ops[name]), name
     attn = block.attention(q, k, v)
-    want_attn = oa.attention(oprep, out_dtype='f32')[0].transpose(1, 0, 2).reshape(rows, inner)
+    want_attn = oa.kitchen_attention(oprep)[0].transpose(1, 0, 2).reshape(rows, inner)
     err = np.abs(np_of(attn).astype(np.float64) - want_attn).max()
     assert err <= 2e-3 * np.abs(want_attn).max(), err
     # stage 4: the gated O projection of the GPU's attention rows, bit for bit,
