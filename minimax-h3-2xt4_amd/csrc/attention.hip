@@ -39,7 +39,7 @@ constexpr int kAttnWaves = 8;      // wavefronts per workgroup
 constexpr int kAttnBQ = kAttnWaves * kAttnWaveQ;   // queries per workgroup
 constexpr int kAttnTile = kAttnBK * kAttnD;        // bytes of one K or V^T tile
 constexpr int kAttnDmaTile = kAttnTile / 1024 / kAttnWaves;   // 1 KB DMA instructions per wave and tile
-constexpr int kAttnDmaBlk = 2 * kAttnDmaTile + 1;  // per wave and block: K, V^T, 64 bytes of V sums
+constexpr int kAttnDmaBlk = 2 * kAttnDmaTile + 2;  // per wave and block: K, V^T, the wave's copy of the V sums
 constexpr int kAttnMaxBlk = 1024;  // nk <= 131072
 constexpr float kLog2e = 0x1.715476p+0f;     // fp32(log2(e))
 // The reference's constants (kitchen_attention_native/vendor/attn_utils.cuh:
@@ -323,6 +323,13 @@ __device__ __forceinline__ void lds_dma16(const int8_t* g, int8_t* l) {
                                    (__attribute__((address_space(3))) void*)l, 16, 0, 0);
 }
 
+// Direct global -> LDS load (global_load_lds_dword): lane i's 4 bytes land
+// at l + 4 i.
+__device__ __forceinline__ void lds_dma4(const int8_t* g, int8_t* l) {
+  __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                   (__attribute__((address_space(3))) void*)l, 4, 0, 0);
+}
+
 // s_waitcnt vmcnt(0) (loads, including the LDS DMA, have landed).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -359,13 +366,16 @@ struct AttnParams {
 };
 
 // One LDS stage: a block's K tile (128 keys x 128 bytes), its V^T tile (128
-// channels x 128 bytes) and its 128 * V code sums. Rows of both tiles are
+// channels x 128 bytes) and each wave's copy of its 128 * V code sums (every
+// lane of every wave takes part in every DMA, so no DMA sits behind a
+// branch and each wave's count of outstanding DMAs is the same on every
+// path; the waits then need not fall back to waiting for all). Rows of both tiles are
 // 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7), so the
 // fragment reads (32 rows of one chunk column) are free of bank conflicts.
 struct AttnStage {
   int8_t k[kAttnTile];
   int8_t v[kAttnTile];
-  int32_t vsum[kAttnD];
+  int32_t vsum[kAttnWaves][kAttnD];
 };
 
 // The reference's online softmax, per query row (the lane's query fr; the
@@ -374,20 +384,29 @@ struct AttnStage {
 //     block: keys past nk excluded and a floor of -50000);
 //   tile_m = max_c fma(mt_c, ts_c, -S_U8_OFFSET) with ts_c = fp32(c0 *
 //     fp32(qs * ks_c)); m' = max(m, tile_m); smaller = exp2(-|m - tile_m|);
-//     the state (output and the four denominators) is scaled by smaller when
-//     the tile raises the maximum, the tile's contribution otherwise;
+//     the state (output and denominators) is scaled by smaller when the tile
+//     raises the maximum, the tile's contribution otherwise;
 //   P = sat_u8(rne(exp2(fma(S, ts_c, -tile_m))));
-//   each group's denominator adds, per 16-key tile, its four P (u8 codes; the
-//     last block: the FP32 probabilities ((p0 + p1) + (p8 + p9))) times the
-//     tile scale, one FMA;
+//   the denominators add the block's P (u8 codes; the last block: the FP32
+//     probabilities) times the tile scale;
 //   O += f32(P.V) * tile scale (one FMA), P.V exact in int32;
-// finally O * (1 / ((d0 + d1) + (d2 + d3))) * vs.
-// The exponentials use the hardware exp2 (v_exp_f32).
+// finally O * (1 / denominator) * vs. The reference keeps four denominators
+// (one per K-scale group, each starting at 1) and adds a group's codes per
+// 16-key tile; here a lane keeps one for its two groups, starting at 2, and
+// adds the block's code sum (exact in int32) with one FMA, which changes
+// only the FP32 rounding of the sum. The exponentials use the hardware
+// exp2 (v_exp_f32).
+//
+// Step j is software-pipelined: the VALU turns block j's scores into
+// probabilities 32 keys at a time while the MFMAs score the same 32 keys of
+// block j + 1 into the registers just freed, then O^T += V^T.P^T runs one
+// 32-channel tile at a time, each tile's accumulation overlapping the next
+// tile's MFMAs.
 template <int OUT>
 __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p) {
   // Four stages, named by compile-time index so the compiler sees that reads
   // of one stage do not alias a DMA still landing in another. Block j lives
-  // in stage j % 4; step j refills the stage of step j - 1 with block j + 3.
+  // in stage j % 4; step j refills the stage of block j - 1 with block j + 3.
   __shared__ __attribute__((aligned(16))) AttnStage st0, st1, st2, st3;
   __shared__ float ksc[4 * kAttnMaxBlk];   // the head's K scales, four per block
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -409,7 +428,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   for (int i = tid; i < 4 * p.nblk; i += 64 * kAttnWaves) ksc[i] = p.ks[bh * 4 * p.nblk + i];
   // Block j's tiles: each wave DMAs kAttnDmaTile kilobytes of each (8 rows
   // per instruction; a lane loads the chunk that lands on its position) and
-  // 64 bytes of the V sums (four lanes). Every block issues exactly
+  // its own copy of the 512 bytes of V sums (two 4-byte DMAs). Every block issues exactly
   // kAttnDmaBlk instructions per wave: past the last block an in-range block
   // is re-loaded into a stage never read, so the waits count exactly.
   // The lanes' byte offsets within a block are loop-invariant (32-bit: a
@@ -422,7 +441,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     koff[u] = (uint32_t)(r * kAttnD + 16 * c);
     voff[u] = (uint32_t)(r * p.nkp + 16 * c);
   }
-  const uint32_t soff = (uint32_t)(64 * wave + 16 * min(lane, 3));
+  const uint32_t soff = (uint32_t)(4 * lane);
   // (The block's offset is added to the lane's in 32 bits, so every DMA is
   // a scalar base plus one 32-bit lane offset.)
   auto dma_blk = [&](int j, AttnStage& stg) {
@@ -434,22 +453,27 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       lds_dma16(k8 + (koff[u] + jk), stg.k + kb * 1024);
       lds_dma16(vt8 + (voff[u] + jv), stg.v + kb * 1024);
     }
-    if (lane < 4)
-      lds_dma16(reinterpret_cast<const int8_t*>(vsumh) + (soff + js), reinterpret_cast<int8_t*>(stg.vsum) + 64 * wave);
+    const int8_t* vs8 = reinterpret_cast<const int8_t*>(vsumh);
+    lds_dma4(vs8 + (soff + js), reinterpret_cast<int8_t*>(stg.vsum[wave]));
+    lds_dma4(vs8 + (soff + js + 256), reinterpret_cast<int8_t*>(stg.vsum[wave]) + 256);
   };
-  // S^T of the block in stg: s[t][4 g + i] is the score of key
-  // 32 t + 8 g + 4 hh + i of the block for query fr.
-  auto scores = [&](const AttnStage& stg, v16i (&s)[4]) {
+  // Rows of 128 bytes, 16-byte chunk ck of row r at chunk ck ^ ((r >> 1) & 7).
+  auto frag = [&](const int8_t* tile, int r, int ck) {
+    return *reinterpret_cast<const v4i*>(tile + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
+  };
+  // Scores of the block's 32-key slice t: s[4 g + i] is the score of key
+  // 32 t + 8 g + 4 hh + i for query fr.
+  auto score_slice = [&](const AttnStage& stg, int t) {
+    v16i acc = v16i{};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      s[t] = v16i{};
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const int r = 32 * t + fr, ck = 2 * ds + hh;
-        const v4i kf = *reinterpret_cast<const v4i*>(stg.k + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
-        s[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[ds], s[t], 0, 0, 0);
-      }
-    }
+    for (int ds = 0; ds < 4; ++ds)
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(stg.k, 32 * t + fr, 2 * ds + hh), qf[ds], acc, 0, 0, 0);
+    return acc;
+  };
+  // Each lane's value combined with the other half-wave's (lane ^ 32).
+  auto halves = [](float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return std::make_pair(__uint_as_float(r[0]), __uint_as_float(r[1]));
   };
   // O^T: o[ct][4 g + i] is channel 32 ct + 8 g + 4 hh + i of query fr.
   float o[4][16];
@@ -457,14 +481,16 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
     for (int x = 0; x < 16; ++x) o[ct][x] = 0.0f;
-  // Running maximum and the denominators of the lane's K-scale groups
-  // c = 2 hh (keys with i < 2) and c = 2 hh + 1.
-  float m = kMInit, d0 = 1.0f, d1 = 1.0f;
+  float m = kMInit, den = 2.0f;
+  v16i s[4];   // the current block's scores
 
-  auto work = [&](int j, const AttnStage& stg, const v16i (&s)[4], auto last_tag) {
+  // Step j: s holds block j's scores. LAST: j is the last block (keys past
+  // nk masked). Otherwise block j + 1 is scored into s on the way.
+  auto step = [&](int j, const AttnStage& cur, const AttnStage& nxt, AttnStage& refill, auto last_tag) {
     constexpr bool LAST = decltype(last_tag)::value;
     const int kl = p.nk - kAttnBK * j;   // keys of the block below nk (LAST)
     auto masked = [&](int t, int g, int i) { return LAST && 32 * t + 8 * g + 4 * hh + i >= kl; };
+    // Group maxima, the tile maximum and the scales.
     int mx0 = INT32_MIN, mx1 = INT32_MIN;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -484,7 +510,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     const float ts0 = p.c0 * (qsr * ksc[4 * j + 2 * hh]);
     const float ts1 = p.c0 * (qsr * ksc[4 * j + 2 * hh + 1]);
     float tm = fmaxf(__builtin_fmaf(mt0, ts0, -kSU8Offset), __builtin_fmaf(mt1, ts1, -kSU8Offset));
-    tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+    {
+      const auto hv = halves(tm);
+      tm = fmaxf(hv.first, hv.second);
+    }
     const float mprev = m;
     m = fmaxf(mprev, tm);
     const float smaller = __builtin_amdgcn_exp2f(-fabsf(mprev - tm));
@@ -495,102 +524,95 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
         for (int x = 0; x < 16; ++x) o[ct][x] = o[ct][x] * osc;
-      d0 = d0 * osc;
-      d1 = d1 * osc;
+      den = den * osc;
     }
-    // Probabilities as u8 words (w[t][g] byte i: key 32 t + 8 g + 4 hh + i)
-    // and the denominators, 16-key tile tt = 2 t + (g >> 1) at a time.
+    // Block j + 1 landed and every wave is past step j - 1: refill that
+    // step's stage with block j + 3.
+    if constexpr (!LAST) {
+      wait_vm<kAttnDmaBlk>();
+      lds_barrier();
+      dma_blk(j + 3, refill);
+    }
+    // Probabilities as u8 words (w[t][g] byte i: key 32 t + 8 g + 4 hh + i),
+    // slice by slice, each slice's registers then taking block j + 1's.
     uint32_t w[4][4];
+    uint32_t csum = 0;
+    float plast = 0.0f;
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const int t = tt >> 1, ga = 2 * (tt & 1);
-      float pf[2][4];
+    for (int t = 0; t < 4; ++t) {
 #pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const int g = ga + gg;
+      for (int g = 0; g < 4; ++g) {
+        float pf[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float sf = masked(t, g, i) ? kMaskScore : (float)s[t][4 * g + i];
-          pf[gg][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf, i < 2 ? ts0 : ts1, -tm));
+          pf[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sf, i < 2 ? ts0 : ts1, -tm));
         }
-        uint32_t u = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][0], 0, 0u);
-        u = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][1], 1, u);
-        u = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][2], 2, u);
-        w[t][g] = __builtin_amdgcn_cvt_pk_u8_f32(pf[gg][3], 3, u);
+        uint32_t u = __builtin_amdgcn_cvt_pk_u8_f32(pf[0], 0, 0u);
+        u = __builtin_amdgcn_cvt_pk_u8_f32(pf[1], 1, u);
+        u = __builtin_amdgcn_cvt_pk_u8_f32(pf[2], 2, u);
+        w[t][g] = __builtin_amdgcn_cvt_pk_u8_f32(pf[3], 3, u);
+        if constexpr (LAST) {
+          plast += (pf[0] + pf[1]) + (pf[2] + pf[3]);
+        } else {
+          csum = __builtin_amdgcn_udot4(w[t][g], 0x01010101u, csum, false);
+        }
       }
-      float part0, part1;
-      if constexpr (LAST) {
-        part0 = (pf[0][0] + pf[0][1]) + (pf[1][0] + pf[1][1]);
-        part1 = (pf[0][2] + pf[0][3]) + (pf[1][2] + pf[1][3]);
-      } else {
-        part0 = (float)__builtin_amdgcn_udot4(w[t][ga], 0x00000101u,
-                                              __builtin_amdgcn_udot4(w[t][ga + 1], 0x00000101u, 0u, false), false);
-        part1 = (float)__builtin_amdgcn_udot4(w[t][ga], 0x01010000u,
-                                              __builtin_amdgcn_udot4(w[t][ga + 1], 0x01010000u, 0u, false), false);
-      }
-      d0 = __builtin_fmaf(part0, tsc, d0);
-      d1 = __builtin_fmaf(part1, tsc, d1);
+      if constexpr (!LAST) s[t] = score_slice(nxt, t);
     }
+    den = __builtin_fmaf(LAST ? plast : (float)csum, tsc, den);
     // O^T += V^T.P^T per 32-channel tile: the signed MFMA takes P - 128 and
     // starts from 128 * the block's code sums, so acc is P.V exactly.
+    v4i pfr[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      pfr[t] = v4i{(int)(w[t][0] ^ 0x80808080u), (int)(w[t][1] ^ 0x80808080u), (int)(w[t][2] ^ 0x80808080u),
+                   (int)(w[t][3] ^ 0x80808080u)};
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       v16i acc;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int4 c4 = *reinterpret_cast<const int4*>(stg.vsum + 32 * ct + 8 * g + 4 * hh);
+        const int4 c4 = *reinterpret_cast<const int4*>(cur.vsum[wave] + 32 * ct + 8 * g + 4 * hh);
         acc[4 * g] = c4.x; acc[4 * g + 1] = c4.y; acc[4 * g + 2] = c4.z; acc[4 * g + 3] = c4.w;
       }
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int r = 32 * ct + fr, ck = 2 * t + hh;
-        const v4i vf = *reinterpret_cast<const v4i*>(stg.v + r * kAttnD + ((ck ^ ((r >> 1) & 7)) << 4));
-        const v4i pfr = {(int)(w[t][0] ^ 0x80808080u), (int)(w[t][1] ^ 0x80808080u), (int)(w[t][2] ^ 0x80808080u),
-                         (int)(w[t][3] ^ 0x80808080u)};
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(vf, pfr, acc, 0, 0, 0);
-      }
+      for (int t = 0; t < 4; ++t)
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(cur.v, 32 * ct + fr, 2 * t + hh), pfr[t], acc, 0, 0, 0);
 #pragma unroll
       for (int x = 0; x < 16; ++x) o[ct][x] = __builtin_fmaf((float)acc[x], tsc, o[ct][x]);
     }
   };
   using NotLast = std::false_type;
   using Last = std::true_type;
-  // Step j: block j landed (blocks j + 1 and j + 2 may be in flight) and
-  // every wave is past step j - 1; score block j, refill step j - 1's stage
-  // with block j + 3, then the softmax update and P.V.
-  auto step = [&](int j, const AttnStage& cur, AttnStage& refill, auto last_tag) {
-    wait_vm<2 * kAttnDmaBlk>();
-    lds_barrier();
-    v16i s[4];
-    scores(cur, s);
-    dma_blk(j + 3, refill);
-    work(j, cur, s, last_tag);
-  };
   dma_blk(0, st0);
   dma_blk(1, st1);
   dma_blk(2, st2);
-  __syncthreads();   // the K scales are in LDS (the DMA waits come with the steps)
+  wait_vm<2 * kAttnDmaBlk>();
+  __syncthreads();   // block 0 and the K scales are in LDS
+#pragma unroll
+  for (int t = 0; t < 4; ++t) s[t] = score_slice(st0, t);
   const int nfull = p.nblk - 1;   // blocks before the last
   int j = 0;
   for (; j + 4 <= nfull; j += 4) {
-    step(j, st0, st3, NotLast{});
-    step(j + 1, st1, st0, NotLast{});
-    step(j + 2, st2, st1, NotLast{});
-    step(j + 3, st3, st2, NotLast{});
+    step(j, st0, st1, st3, NotLast{});
+    step(j + 1, st1, st2, st0, NotLast{});
+    step(j + 2, st2, st3, st1, NotLast{});
+    step(j + 3, st3, st0, st2, NotLast{});
   }
-  if (j < nfull) step(j, st0, st3, NotLast{});
-  if (j + 1 < nfull) step(j + 1, st1, st0, NotLast{});
-  if (j + 2 < nfull) step(j + 2, st2, st1, NotLast{});
+  if (j < nfull) step(j, st0, st1, st3, NotLast{});
+  if (j + 1 < nfull) step(j + 1, st1, st2, st0, NotLast{});
+  if (j + 2 < nfull) step(j + 2, st2, st3, st1, NotLast{});
   switch (nfull - j) {
-    case 0: step(nfull, st0, st3, Last{}); break;
-    case 1: step(nfull, st1, st0, Last{}); break;
-    case 2: step(nfull, st2, st1, Last{}); break;
-    default: step(nfull, st3, st2, Last{}); break;
+    case 0: step(nfull, st0, st1, st3, Last{}); break;
+    case 1: step(nfull, st1, st2, st0, Last{}); break;
+    case 2: step(nfull, st2, st3, st1, Last{}); break;
+    default: step(nfull, st3, st0, st2, Last{}); break;
   }
   wait_vm<0>();   // no DMA may still target this workgroup's LDS at exit
-  // (d0 + d1) + (d2 + d3): each half-wave holds one pair.
-  const float dpair = d0 + d1;
-  const float rcp = 1.0f / (dpair + __shfl_xor(dpair, 32, 64));
+  // The two half-waves' denominators (first: lane & 31's, second: lane | 32's).
+  const auto dh = halves(den);
+  const float rcp = 1.0f / (dh.first + dh.second);
   if (q0 + fr >= p.nq) return;
   const int64_t orow = p.ost.at(bh, q0 + fr);
   const float* vsc = p.vs + bh * kAttnD;
