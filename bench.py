@@ -995,8 +995,8 @@ def run_dit_attention(args, torch, dev):
                ms_per_step=round(ta + tp, 3),
                roofline=dict(bound='mfma', achieved=round(tops, 1), peak=PEAK_INT8_TOPS, unit='TFLOP/s',
                              frac=round(tops / PEAK_INT8_TOPS, 4), traffic=None,
-                             kernel='attention_kernel<1> (256 queries x 128-key blocks per workgroup, one '
-                                    'online-softmax pass)',
+                             kernel='attention_kernel<1> (128 queries x 128-key blocks per workgroup, two '
+                                    'workgroups per CU, one online-softmax pass)',
                              algorithmic=f'{ops:.4g} int8 ops per launch (4 N^2 D H)'),
                kernels=dict(prepare_us=round(tp * 1e3, 1), attention_us=round(ta * 1e3, 1)))
     if not args.no_cpu_baseline:

@@ -35,12 +35,11 @@ constexpr int kAttnD = 128;        // head dimension
 constexpr int kAttnBK = 128;       // keys per block (the reference launcher's CTA_K = 128)
 constexpr int kAttnChunk = 256;    // tokens per partial of the key statistics
 constexpr int kAttnWaveQ = 32;     // queries per wavefront
-constexpr int kAttnWaves = 8;      // wavefronts per workgroup
+constexpr int kAttnWaves = 4;      // wavefronts per workgroup (one per SIMD; two workgroups per CU)
 constexpr int kAttnBQ = kAttnWaves * kAttnWaveQ;   // queries per workgroup
 constexpr int kAttnTile = kAttnBK * kAttnD;        // bytes of one K or V^T tile
 constexpr int kAttnDmaTile = kAttnTile / 1024 / kAttnWaves;   // 1 KB DMA instructions per wave and tile
-constexpr int kAttnDmaBlk = 2 * kAttnDmaTile + 2;  // per wave and block: K, V^T, the wave's copy of the V sums
-constexpr int kAttnMaxBlk = 1024;  // nk <= 131072
+constexpr int kAttnMaxBlk = 1024;  // nk <= 131072 (32-bit DMA offsets within a head)
 constexpr float kLog2e = 0x1.715476p+0f;     // fp32(log2(e))
 // The reference's constants (kitchen_attention_native/vendor/attn_utils.cuh:
 // S_U8_OFFSET, :40; the running maximum's start and the out-of-bounds score
@@ -346,8 +345,8 @@ __device__ __forceinline__ void lds_barrier() {
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 16, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4) | (0xF << 8));
+  static_assert(N >= 0 && N < 64, "vmcnt range");   // six bits: [3:0] and [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
 
@@ -365,15 +364,16 @@ struct AttnParams {
   float c0;   // fp32(sm_scale * log2(e))
 };
 
-// One LDS stage: a block's K tile (128 keys x 128 bytes), its V^T tile (128
-// channels x 128 bytes) and each wave's copy of its 128 * V code sums (every
-// lane of every wave takes part in every DMA, so no DMA sits behind a
-// branch and each wave's count of outstanding DMAs is the same on every
-// path; the waits then need not fall back to waiting for all). Rows of both tiles are
-// 128 bytes with 16-byte chunk c stored at chunk c ^ ((r >> 1) & 7), so the
-// fragment reads (32 rows of one chunk column) are free of bank conflicts.
-struct AttnStage {
+// LDS tiles: a block's K (128 keys x 128 bytes), or its V^T (128 channels x
+// 128 bytes) with each wave's copy of the block's 128 * V code sums (every
+// lane of every wave takes part in every DMA, so no DMA sits behind a lane
+// branch). Rows of both tiles are 128 bytes with 16-byte chunk c stored at
+// chunk c ^ ((r >> 1) & 7), so the fragment reads (32 rows of one chunk
+// column) are free of bank conflicts.
+struct AttnKTile {
   int8_t k[kAttnTile];
+};
+struct AttnVTile {
   int8_t v[kAttnTile];
   int32_t vsum[kAttnWaves][kAttnD];
 };
@@ -397,18 +397,23 @@ struct AttnStage {
 // only the FP32 rounding of the sum. The exponentials use the hardware
 // exp2 (v_exp_f32).
 //
-// Step j is software-pipelined: the VALU turns block j's scores into
-// probabilities 32 keys at a time while the MFMAs score the same 32 keys of
-// block j + 1 into the registers just freed, then O^T += V^T.P^T runs one
-// 32-channel tile at a time, each tile's accumulation overlapping the next
-// tile's MFMAs.
+// A workgroup is four wavefronts, one per SIMD, and two workgroups share a
+// CU (the LDS holds two of everything below), so the two wavefronts on a
+// SIMD belong to different workgroups, wait at different barriers and drift
+// out of phase: one forms probabilities on the VALU while the other's MFMAs
+// run. Step j is software-pipelined: the VALU turns block j's scores into
+// probabilities while the MFMAs score block j + 1 into the registers just
+// freed, then O^T += V^T.P^T runs while block j + 1's statistics are taken.
+// Step j reads K of block j + 1 and V of block j; after its barrier it DMAs
+// K of block j + 2 and V of block j + 1 into the tiles that steps j - 1
+// read, so two K tiles and two V tiles suffice.
 template <int OUT>
-__global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p) {
-  // Four stages, named by compile-time index so the compiler sees that reads
-  // of one stage do not alias a DMA still landing in another. Block j lives
-  // in stage j % 4; step j refills the stage of block j - 1 with block j + 3.
-  __shared__ __attribute__((aligned(16))) AttnStage st0, st1, st2, st3;
-  __shared__ float ksc[4 * kAttnMaxBlk];   // the head's K scales, four per block
+__global__ __launch_bounds__(64 * kAttnWaves, 2) void attention_kernel(AttnParams p) {
+  // Named by compile-time index so the compiler sees that reads of one tile
+  // do not alias a DMA still landing in another.
+  __shared__ __attribute__((aligned(16))) AttnKTile ka, kb;
+  __shared__ __attribute__((aligned(16))) AttnVTile va, vb;
+  extern __shared__ __attribute__((aligned(16))) float ksc[];   // the head's K scales, four per block (16 nblk bytes)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 31, hh = lane >> 5;
   const int64_t bh = blockIdx.y;
@@ -426,14 +431,12 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   }
   const float qsr = p.qs[bh * p.nq + qrow];
   for (int i = tid; i < 4 * p.nblk; i += 64 * kAttnWaves) ksc[i] = p.ks[bh * 4 * p.nblk + i];
-  // Block j's tiles: each wave DMAs kAttnDmaTile kilobytes of each (8 rows
-  // per instruction; a lane loads the chunk that lands on its position) and
-  // its own copy of the 512 bytes of V sums (two 4-byte DMAs). Every block issues exactly
-  // kAttnDmaBlk instructions per wave: past the last block an in-range block
-  // is re-loaded into a stage never read, so the waits count exactly.
-  // The lanes' byte offsets within a block are loop-invariant (32-bit: a
-  // head's V^T is at most 128 x 131072 bytes); each block adds a
-  // wave-uniform base.
+  // Each wave DMAs kAttnDmaTile kilobytes of a tile (8 rows per
+  // instruction; a lane loads the chunk that lands on its position) and its
+  // own copy of the 512 bytes of V sums (two 4-byte DMAs). Blocks past the
+  // last are not loaded. The lanes' byte offsets within a block are
+  // loop-invariant (32-bit: a head's V^T is at most 128 x 131072 bytes);
+  // each block adds a wave-uniform base.
   uint32_t koff[kAttnDmaTile], voff[kAttnDmaTile];
 #pragma unroll
   for (int u = 0; u < kAttnDmaTile; ++u) {
@@ -442,20 +445,20 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
     voff[u] = (uint32_t)(r * p.nkp + 16 * c);
   }
   const uint32_t soff = (uint32_t)(4 * lane);
-  // (The block's offset is added to the lane's in 32 bits, so every DMA is
-  // a scalar base plus one 32-bit lane offset.)
-  auto dma_blk = [&](int j, AttnStage& stg) {
-    j = min(j, p.nblk - 1);
-    const uint32_t jk = (uint32_t)(j * kAttnBK * kAttnD), jv = (uint32_t)(j * kAttnBK), js = (uint32_t)(j * kAttnD * 4);
+  auto dma_k = [&](int j, AttnKTile& t) {
+    if (j >= p.nblk) return;
+    const uint32_t jk = (uint32_t)(j * kAttnBK * kAttnD);
 #pragma unroll
-    for (int u = 0; u < kAttnDmaTile; ++u) {
-      const int kb = kAttnDmaTile * wave + u;
-      lds_dma16(k8 + (koff[u] + jk), stg.k + kb * 1024);
-      lds_dma16(vt8 + (voff[u] + jv), stg.v + kb * 1024);
-    }
+    for (int u = 0; u < kAttnDmaTile; ++u) lds_dma16(k8 + (koff[u] + jk), t.k + (kAttnDmaTile * wave + u) * 1024);
+  };
+  auto dma_v = [&](int j, AttnVTile& t) {
+    if (j >= p.nblk) return;
+    const uint32_t jv = (uint32_t)(j * kAttnBK), js = (uint32_t)(j * kAttnD * 4);
+#pragma unroll
+    for (int u = 0; u < kAttnDmaTile; ++u) lds_dma16(vt8 + (voff[u] + jv), t.v + (kAttnDmaTile * wave + u) * 1024);
     const int8_t* vs8 = reinterpret_cast<const int8_t*>(vsumh);
-    lds_dma4(vs8 + (soff + js), reinterpret_cast<int8_t*>(stg.vsum[wave]));
-    lds_dma4(vs8 + (soff + js + 256), reinterpret_cast<int8_t*>(stg.vsum[wave]) + 256);
+    lds_dma4(vs8 + (soff + js), reinterpret_cast<int8_t*>(t.vsum[wave]));
+    lds_dma4(vs8 + (soff + js + 256), reinterpret_cast<int8_t*>(t.vsum[wave]) + 256);
   };
   // Rows of 128 bytes, 16-byte chunk ck of row r at chunk ck ^ ((r >> 1) & 7).
   auto frag = [&](const int8_t* tile, int r, int ck) {
@@ -463,14 +466,15 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
   };
   // Scores of the block's 32-key slice t: s[4 g + i] is the score of key
   // 32 t + 8 g + 4 hh + i for query fr.
-  auto score_slice = [&](const AttnStage& stg, int t) {
+  auto score_slice = [&](const AttnKTile& kt, int t) {
     v16i acc = v16i{};
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds)
-      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(stg.k, 32 * t + fr, 2 * ds + hh), qf[ds], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(kt.k, 32 * t + fr, 2 * ds + hh), qf[ds], acc, 0, 0, 0);
     return acc;
   };
-  // Each lane's value combined with the other half-wave's (lane ^ 32).
+  // Each lane's value and the other half-wave's (first: lane & 31's,
+  // second: lane | 32's).
   auto halves = [](float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return std::make_pair(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -482,15 +486,15 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
 #pragma unroll
     for (int x = 0; x < 16; ++x) o[ct][x] = 0.0f;
   float m = kMInit, den = 2.0f;
-  v16i s[4];   // the current block's scores
+  v16i s[4];                  // the current block's scores
+  float tm, ts0, ts1, tsc;    // its tile maximum, the lane's two scales and its tile scale
 
-  // Step j: s holds block j's scores. LAST: j is the last block (keys past
-  // nk masked). Otherwise block j + 1 is scored into s on the way.
-  auto step = [&](int j, const AttnStage& cur, const AttnStage& nxt, AttnStage& refill, auto last_tag) {
+  // Block j's statistics from s (LAST: keys past nk masked): the group
+  // maxima, the tile maximum, the running maximum and the scales. Returns
+  // the factor the running state is to be scaled by.
+  auto stats = [&](int j, auto last_tag) {
     constexpr bool LAST = decltype(last_tag)::value;
-    const int kl = p.nk - kAttnBK * j;   // keys of the block below nk (LAST)
-    auto masked = [&](int t, int g, int i) { return LAST && 32 * t + 8 * g + 4 * hh + i >= kl; };
-    // Group maxima, the tile maximum and the scales.
+    const int kl = p.nk - kAttnBK * j;
     int mx0 = INT32_MIN, mx1 = INT32_MIN;
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -498,7 +502,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       for (int g = 0; g < 4; ++g)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int v = masked(t, g, i) ? INT32_MIN : s[t][4 * g + i];
+          const int v = (LAST && 32 * t + 8 * g + 4 * hh + i >= kl) ? INT32_MIN : s[t][4 * g + i];
           if (i < 2) mx0 = max(mx0, v);
           else mx1 = max(mx1, v);
         }
@@ -507,18 +511,18 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       mt0 = fmaxf(kMInit, mt0);
       mt1 = fmaxf(kMInit, mt1);
     }
-    const float ts0 = p.c0 * (qsr * ksc[4 * j + 2 * hh]);
-    const float ts1 = p.c0 * (qsr * ksc[4 * j + 2 * hh + 1]);
-    float tm = fmaxf(__builtin_fmaf(mt0, ts0, -kSU8Offset), __builtin_fmaf(mt1, ts1, -kSU8Offset));
-    {
-      const auto hv = halves(tm);
-      tm = fmaxf(hv.first, hv.second);
-    }
+    ts0 = p.c0 * (qsr * ksc[4 * j + 2 * hh]);
+    ts1 = p.c0 * (qsr * ksc[4 * j + 2 * hh + 1]);
+    tm = fmaxf(__builtin_fmaf(mt0, ts0, -kSU8Offset), __builtin_fmaf(mt1, ts1, -kSU8Offset));
+    const auto hv = halves(tm);
+    tm = fmaxf(hv.first, hv.second);
     const float mprev = m;
     m = fmaxf(mprev, tm);
     const float smaller = __builtin_amdgcn_exp2f(-fabsf(mprev - tm));
-    const float osc = mprev < tm ? smaller : 1.0f;
-    const float tsc = tm < mprev ? smaller : 1.0f;
+    tsc = tm < mprev ? smaller : 1.0f;
+    return mprev < tm ? smaller : 1.0f;
+  };
+  auto rescale = [&](float osc) {
     if (__builtin_amdgcn_ballot_w64(osc != 1.0f) != 0) {
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
@@ -526,12 +530,26 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
         for (int x = 0; x < 16; ++x) o[ct][x] = o[ct][x] * osc;
       den = den * osc;
     }
-    // Block j + 1 landed and every wave is past step j - 1: refill that
-    // step's stage with block j + 3.
+  };
+
+  // Step j: s holds block j's scores, (tm, ts0, ts1, tsc) its statistics and
+  // the running state is already scaled for it. kn holds K of block j + 1,
+  // vc V of block j; kr and vr take K of block j + 2 and V of block j + 1.
+  // LAST: j is the last block; otherwise block j + 1 (the last when
+  // NEXT_LAST) is scored into s on the way and its statistics are taken
+  // while block j's P.V runs.
+  auto step = [&](int j, const AttnKTile& kn, AttnKTile& kr, const AttnVTile& vc, AttnVTile& vr, auto last_tag,
+                  auto next_last_tag) {
+    constexpr bool LAST = decltype(last_tag)::value;
+    const int kl = p.nk - kAttnBK * j;   // keys of the block below nk (LAST)
+    auto masked = [&](int t, int g, int i) { return LAST && 32 * t + 8 * g + 4 * hh + i >= kl; };
+    // Every DMA of step j - 1 (K of block j + 1, V of block j) landed and
+    // every wave is past step j - 1: refill the tiles it read.
+    wait_vm<0>();
+    lds_barrier();
     if constexpr (!LAST) {
-      wait_vm<kAttnDmaBlk>();
-      lds_barrier();
-      dma_blk(j + 3, refill);
+      dma_k(j + 2, kr);
+      dma_v(j + 1, vr);
     }
     // Probabilities as u8 words (w[t][g] byte i: key 32 t + 8 g + 4 hh + i),
     // slice by slice, each slice's registers then taking block j + 1's.
@@ -558,9 +576,12 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
           csum = __builtin_amdgcn_udot4(w[t][g], 0x01010101u, csum, false);
         }
       }
-      if constexpr (!LAST) s[t] = score_slice(nxt, t);
+      if constexpr (!LAST) s[t] = score_slice(kn, t);
     }
-    den = __builtin_fmaf(LAST ? plast : (float)csum, tsc, den);
+    const float tsj = tsc;
+    den = __builtin_fmaf(LAST ? plast : (float)csum, tsj, den);
+    float osc = 1.0f;
+    if constexpr (!LAST) osc = stats(j + 1, next_last_tag);
     // O^T += V^T.P^T per 32-channel tile: the signed MFMA takes P - 128 and
     // starts from 128 * the block's code sums, so acc is P.V exactly.
     v4i pfr[4];
@@ -573,44 +594,44 @@ __global__ __launch_bounds__(64 * kAttnWaves) void attention_kernel(AttnParams p
       v16i acc;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int4 c4 = *reinterpret_cast<const int4*>(cur.vsum[wave] + 32 * ct + 8 * g + 4 * hh);
+        const int4 c4 = *reinterpret_cast<const int4*>(vc.vsum[wave] + 32 * ct + 8 * g + 4 * hh);
         acc[4 * g] = c4.x; acc[4 * g + 1] = c4.y; acc[4 * g + 2] = c4.z; acc[4 * g + 3] = c4.w;
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(cur.v, 32 * ct + fr, 2 * t + hh), pfr[t], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(frag(vc.v, 32 * ct + fr, 2 * t + hh), pfr[t], acc, 0, 0, 0);
 #pragma unroll
-      for (int x = 0; x < 16; ++x) o[ct][x] = __builtin_fmaf((float)acc[x], tsc, o[ct][x]);
+      for (int x = 0; x < 16; ++x) o[ct][x] = __builtin_fmaf((float)acc[x], tsj, o[ct][x]);
     }
+    if constexpr (!LAST) rescale(osc);
   };
   using NotLast = std::false_type;
   using Last = std::true_type;
-  dma_blk(0, st0);
-  dma_blk(1, st1);
-  dma_blk(2, st2);
-  wait_vm<2 * kAttnDmaBlk>();
-  __syncthreads();   // block 0 and the K scales are in LDS
+  dma_k(0, ka);
+  dma_k(1, kb);
+  dma_v(0, va);
+  wait_vm<0>();
+  __syncthreads();   // the K scales, K of blocks 0 and 1 and V of block 0 are in LDS
 #pragma unroll
-  for (int t = 0; t < 4; ++t) s[t] = score_slice(st0, t);
-  const int nfull = p.nblk - 1;   // blocks before the last
+  for (int t = 0; t < 4; ++t) s[t] = score_slice(ka, t);
+  const int nb = p.nblk;
+  rescale(nb == 1 ? stats(0, Last{}) : stats(0, NotLast{}));
+  // Step j reads K tile (j + 1) % 2 and V tile j % 2. Steps 0 .. nb - 3
+  // (neither the block nor the next the last) two at a time; then nb - 2
+  // (the next the last) and nb - 1.
   int j = 0;
-  for (; j + 4 <= nfull; j += 4) {
-    step(j, st0, st1, st3, NotLast{});
-    step(j + 1, st1, st2, st0, NotLast{});
-    step(j + 2, st2, st3, st1, NotLast{});
-    step(j + 3, st3, st0, st2, NotLast{});
+  for (; j + 2 <= nb - 2; j += 2) {
+    step(j, kb, ka, va, vb, NotLast{}, NotLast{});
+    step(j + 1, ka, kb, vb, va, NotLast{}, NotLast{});
   }
-  if (j < nfull) step(j, st0, st1, st3, NotLast{});
-  if (j + 1 < nfull) step(j + 1, st1, st2, st0, NotLast{});
-  if (j + 2 < nfull) step(j + 2, st2, st3, st1, NotLast{});
-  switch (nfull - j) {
-    case 0: step(nfull, st0, st1, st3, Last{}); break;
-    case 1: step(nfull, st1, st2, st0, Last{}); break;
-    case 2: step(nfull, st2, st3, st1, Last{}); break;
-    default: step(nfull, st3, st0, st2, Last{}); break;
+  if (j < nb - 2) step(j, kb, ka, va, vb, NotLast{}, NotLast{});
+  if (nb >= 2) {
+    if ((nb - 2) & 1) step(nb - 2, ka, kb, vb, va, NotLast{}, Last{});
+    else step(nb - 2, kb, ka, va, vb, NotLast{}, Last{});
   }
-  wait_vm<0>();   // no DMA may still target this workgroup's LDS at exit
-  // The two half-waves' denominators (first: lane & 31's, second: lane | 32's).
+  if ((nb - 1) & 1) step(nb - 1, ka, kb, vb, va, Last{}, Last{});
+  else step(nb - 1, kb, ka, va, vb, Last{}, Last{});
+  // (The last step issued no DMA: nothing targets this workgroup's LDS.)
   const auto dh = halves(den);
   const float rcp = 1.0f / (dh.first + dh.second);
   if (q0 + fr >= p.nq) return;
@@ -735,7 +756,7 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   W8A8_REQUIRE(a->d == kAttnD, "w8a8_attention: head dimension %d != 128", a->d);
   W8A8_REQUIRE(a->b > 0 && a->h > 0 && a->nq > 0 && a->nk > 0, "w8a8_attention: empty problem");
   W8A8_REQUIRE(a->nq < (1 << 24) && a->b * a->h < 65536, "w8a8_attention: sizes out of range");
-  if (a->nk > kAttnMaxBlk * kAttnBK) {   // the K scales of a head are staged in LDS
+  if (a->nk > kAttnMaxBlk * kAttnBK) {   // the limit w8a8_attention_prepare enforces
     set_error("w8a8_attention: at most %d keys", kAttnMaxBlk * kAttnBK);
     return W8A8_ERR_UNSUPPORTED;
   }
@@ -759,7 +780,8 @@ extern "C" int w8a8_attention(const W8A8AttentionArgs* a) {
   p.c0 = a->sm_scale * kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(a->stream);
   const dim3 grid((unsigned)((p.nq + kAttnBQ - 1) / kAttnBQ), (unsigned)(a->b * a->h));
-  if (a->out_dtype == W8A8_F32) hipLaunchKernelGGL(attention_kernel<kF32>, grid, dim3(64 * kAttnWaves), 0, s, p);
-  else hipLaunchKernelGGL(attention_kernel<kF16>, grid, dim3(64 * kAttnWaves), 0, s, p);
+  const size_t ksc_bytes = (size_t)16 * p.nblk;   // two workgroups per CU up to 53504 keys or so, one beyond
+  if (a->out_dtype == W8A8_F32) hipLaunchKernelGGL(attention_kernel<kF32>, grid, dim3(64 * kAttnWaves), ksc_bytes, s, p);
+  else hipLaunchKernelGGL(attention_kernel<kF16>, grid, dim3(64 * kAttnWaves), ksc_bytes, s, p);
   return launch_status("w8a8_attention");
 }
