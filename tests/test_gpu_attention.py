@@ -87,6 +87,24 @@ def test_attention_matches_oracle(gpu, b, h, nq, nk, dtype):
     assert torch.equal(out16, out.half())
 
 
+@pytest.mark.parametrize('nk', [1024, 4096, 16384, 53504])
+def test_error_vs_exact_no_worse_than_restatement(gpu, nk):
+    # Long rows up to the DiT sequence (53504 keys), a short query set: the
+    # kernel's error against exact float64 attention stays within 2% of the
+    # restatement's (whose exp2 is exact), at every length.
+    g = torch.Generator().manual_seed(nk)
+    q, k, v = _qkv(g, 1, 1, 32, nk, torch.float16)
+    prep = kernels.attention_prepare(q.to(gpu), k.to(gpu), v.to(gpu))
+    out = np_of(kernels.attention(prep, out_dtype=torch.float32)).astype(np.float64)
+    want = oa.kitchen_attention(oa.kitchen_prepare(_np(q), _np(k), _np(v), cta_k=oa.GPU_CTA_K)).astype(np.float64)
+    exact = oa.reference_attention(_np(q), _np(k), _np(v))
+    scale = np.abs(exact).max()
+    err_gpu = np.abs(out - exact).max() / scale
+    err_oracle = np.abs(want - exact).max() / scale
+    print(f'nk={nk}: max error / max |exact|: kernel {err_gpu:.4e}, restatement {err_oracle:.4e}')
+    assert err_gpu <= 1.02 * err_oracle + 1e-5, (err_gpu, err_oracle)
+
+
 def test_large_logits_and_uniform_keys(gpu):
     g = torch.Generator().manual_seed(5)
     q, k, v = _qkv(g, 1, 1, 96, 200, torch.float32, qmul=40.0)     # sharp softmax, large running maxima
