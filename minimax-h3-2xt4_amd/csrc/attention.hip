@@ -13,13 +13,14 @@
 // codes per channel. Codes are sat(round half away(x / s)), s = amax / 127 +
 // 1e-7.
 //
-// Attention: a workgroup of eight wavefronts (two per SIMD) takes 256
-// queries of one (batch, head); a wavefront owns 32. Key blocks of 128 are
-// DMA'd global -> LDS (K 128 x 128 bytes, V^T 128 x 128 bytes, the block's
-// V sums) into a ring of four stages, three blocks ahead. Scores are computed
-// transposed, S^T = K.Q^T on v_mfma_i32_32x32x32_i8, so a lane holds one
-// query (lane % 32) and 64 of the block's keys: exactly the keys of two of
-// the four K-scale groups, whose maxima it takes alone. The u8
+// Attention: a workgroup of four wavefronts (one per SIMD, two workgroups
+// per CU) takes 128 queries of one (batch, head); a wavefront owns 32. Key
+// blocks of 128 are DMA'd global -> LDS into two K tiles and two V^T tiles
+// (with each wave's copy of the block's V sums): step j reads K of block
+// j + 1 and V of block j, then refills the tiles step j - 1 read. Scores are
+// computed transposed, S^T = K.Q^T on v_mfma_i32_32x32x32_i8, so a lane
+// holds one query (lane % 32) and 64 of the block's keys: exactly the keys of
+// two of the four K-scale groups, whose maxima it takes alone. The u8
 // probabilities are then already the B operand of O^T = V^T.P^T; the signed
 // MFMA takes P - 128, and its accumulator starts from the block's 128 * sum
 // of V codes, so it ends with the exact P.V.

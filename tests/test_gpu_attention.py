@@ -20,11 +20,11 @@ SHAPES = [
     (2, 3, 200, 64, torch.float32),
     (1, 1, 128, 300, torch.float16),
     (1, 2, 257, 1000, torch.float16),
-    # the step loop's four-stage unroll and every tail length (blocks - 1 =
-    # 12, 13, 14, 15 after the loop: 0, 1, 2, 3 non-last steps before the
-    # last), key counts that are and are not multiples of 128, and long
-    # sequences (queries are independent, so a short query set exercises the
-    # whole key loop)
+    # the step loop's two-step unroll and every tail (13, 14 and 15 blocks:
+    # after the loop one or no further step, then the step whose next block
+    # is the last, alternating tiles), key counts that are and are not
+    # multiples of 128, and long sequences (queries are independent, so a
+    # short query set exercises the whole key loop)
     (1, 1, 64, 1600, torch.float16),
     (1, 1, 33, 1664, torch.float16),
     (1, 1, 40, 1792, torch.float16),
