@@ -215,15 +215,8 @@ extern "C" int w8a8_gemm_noalloc(const W8A8GemmArgs* a) {
   int dev = 0;
   int rc = scratch_of_current_device(&ws, &dev);
   if (rc != W8A8_OK) return rc;
-  if (a->m > 0 && a->n > 0 && a->k > 0 && a->rope == nullptr && a->m < (1LL << 31) && a->n < (1LL << 31) &&
-      a->k < (1LL << 31)) {
-    int64_t need = 0;
-    gemm_ksplit(a->m, a->n, a->k, dev, &need);
-    W8A8_REQUIRE(need <= kScratchBytes,
-                 "w8a8_gemm_noalloc: %lld x %lld x %lld splits K and needs %lld scratch bytes, above the "
-                 "%lld-byte static scratch",
-                 (long long)a->m, (long long)a->n, (long long)a->k, (long long)need, (long long)kScratchBytes);
-  }
+  // A split whose partials outgrow the scratch runs unsplit (launch_gemm
+  // re-plans when the workspace is too small), with the same result.
   return gemm_entry(a, ws, kScratchBytes);
 }
 

@@ -365,9 +365,13 @@ def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
     a = randi8(g, (m, k))
     b = randi8(g, (n, k))
     acc = o.int_mm(np_of(a), np_of(b))
+    need = kernels.gemm_workspace_bytes(m, n, k, gpu)
     if epi == 'int32':
         got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32)
         assert_bits_equal(np_of(got), acc, 'split-K int32')
+        two_kernel = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32,
+                                  workspace=torch.empty(need - 8, dtype=torch.uint8, device=gpu))
+        assert_bits_equal(np_of(two_kernel), acc, 'split-K int32 finished by the second kernel')
         return
     rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
     ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
@@ -378,6 +382,11 @@ def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
               bias=None if bias is None else bias.to(gpu), residual=None if res is None else res.to(gpu))
     got = kernels.gemm(a.to(gpu), b.to(gpu), **kw)
     unsplit = kernels.gemm(a.to(gpu), b.to(gpu), workspace=torch.empty(0, dtype=torch.uint8, device=gpu), **kw)
+    # A workspace one word short of the tiles' arrival words still holds the
+    # partials: the split then finishes in a second kernel.
+    two_kernel = kernels.gemm(a.to(gpu), b.to(gpu), workspace=torch.empty(need - 8, dtype=torch.uint8, device=gpu),
+                              **kw)
+    assert_bits_equal(np_of(two_kernel), np_of(got), 'split-K finished by the second kernel')
     fn = o.dequantize_row if epi == 'row' else o.dequantize_column
     want = fn(acc, np_of(rs).reshape(-1), np_of(ws).reshape(-1), tname(out_dtype),
               None if bias is None else np_of(bias))
@@ -385,6 +394,30 @@ def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
         want = o.residual_add(np_of(res), want)
     assert_bits_equal(np_of(got), want, f'split-K {epi} {out_dtype}')
     assert_bits_equal(np_of(unsplit), np_of(got), 'split-K equals the unsplit GEMM')
+
+
+def test_gemm_split_k_gated_residual_and_reused_workspace(gpu):
+    # The DiT gate in the split-K finish; the same workspace serves three
+    # calls in a row (its arrival words hold the previous call's state, its
+    # first call's were never written).
+    m, n, k = 300, 520, 2048
+    assert kernels.gemm_workspace_bytes(m, n, k, gpu) > 0
+    g = torch.Generator().manual_seed(19)
+    ws_buf = torch.full((kernels.gemm_workspace_bytes(m, n, k, gpu),), 0xA5, dtype=torch.uint8, device=gpu)
+    for call in range(3):
+        a = randi8(g, (m, k))
+        b = randi8(g, (n, k))
+        rs = torch.rand((m, 1), generator=g) * 0.01 + 1e-4
+        ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
+        res = randn16(g, (m, n), 1 / 512)
+        gate = torch.randn((9, n), generator=g)
+        labels = torch.randint(0, 9, (m,), generator=g, dtype=torch.int32)
+        got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu),
+                           col_scale=ws.to(gpu), out_dtype=torch.float16, residual=res.to(gpu), gate=gate.to(gpu),
+                           gate_labels=labels.to(gpu), workspace=ws_buf)
+        branch = o.dequantize_row(o.int_mm(np_of(a), np_of(b)), np_of(rs).reshape(-1), np_of(ws).reshape(-1), 'f16')
+        want = o.gated_residual_add(np_of(res), branch, np_of(gate), np_of(labels))
+        assert_bits_equal(np_of(got), want, f'split-K gated residual, call {call}')
 
 
 def test_gemm_unaligned_output_rows(gpu):

@@ -154,6 +154,32 @@ def test_eps_fold_is_exact_on_the_scaled_stream(gpu):
     assert_bits_equal(np_of(scaled), want, 'folded eps norm')
 
 
+def _ordered(t):
+    """16-bit floats as integers in value order (sign-magnitude to two's complement)."""
+    bits = t.view(torch.int16).to(torch.int32)
+    return torch.where(bits < 0, -(bits & 0x7FFF), bits)
+
+
+@pytest.mark.parametrize('dtype', [torch.float16, torch.bfloat16])
+def test_stable_norm_agrees_with_torch_rms_norm(gpu, dtype):
+    """StableNorm's kernel (fixed-order fp32 sum, IEEE sqrt and division)
+    against the reference's own expression, F.rms_norm(x.float(), ..., eps)
+    cast back (patches/h3_tensor_flow.py:48-69), on the same device: at most
+    one unit in the last place apart, and nearly all outputs bit-identical."""
+    g = torch.Generator().manual_seed(53)
+    norm = torch.nn.RMSNorm(3072, eps=1e-6, device=gpu)
+    norm.weight.data.copy_(torch.rand(3072, generator=g) + 0.5)
+    sn = StableNorm(norm, divisor=512.0)
+    x = ((torch.randn((4096, 3072), generator=g) * torch.rand((4096, 1), generator=g) * 4) / 512).to(dtype).to(gpu)
+    got = sn(x)
+    want = torch.nn.functional.rms_norm(x.float(), (3072,), norm.weight.detach().float(), sn.eps).to(dtype)
+    d = (_ordered(got) - _ordered(want)).abs()
+    same = (d == 0).float().mean().item()
+    print(f'{dtype}: max {d.max().item()} ulp apart, {same:.5f} bit-identical')
+    assert d.max().item() <= 1
+    assert same >= 0.99
+
+
 def test_dit_block_runs_its_sublayers(gpu):
     from w8a8.tp_dit import TPDiTBlockINT8
     g = torch.Generator().manual_seed(52)

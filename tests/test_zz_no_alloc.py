@@ -1,10 +1,13 @@
 """The no-allocation GEMM entry point (w8a8_gemm_noalloc) through the C ABI.
 
-Its split-K partials live in the library's file-scope device scratch array
-instead of a caller workspace. Two calls in a row (the second smaller, so
-stale partials of the first remain in the array) must equal w8a8_gemm with a
-torch-allocated workspace bit for bit, and the oracle; shapes that would
-need more scratch than the array holds, and a caller workspace, are refused.
+Its split-K partials and tile arrival words live in the library's file-scope
+device scratch array instead of a caller workspace. Two calls in a row (the
+second smaller, so stale partials and arrival words of the first remain in
+the array) must equal w8a8_gemm with a torch-allocated workspace bit for
+bit, and the oracle. A shape whose split would need more scratch than the
+array holds runs unsplit, with the same result; a caller workspace is
+refused. A split call captured in a HIP graph replays bit-identically, with
+other calls reusing the scratch between the replays.
 """
 import ctypes
 
@@ -63,19 +66,61 @@ def test_noalloc_gemm_equals_gemm_on_two_calls(gpu, call):
         assert torch.equal(got16.view(torch.int16), ref16.view(torch.int16))
 
 
-def test_noalloc_gemm_refuses_what_it_cannot_hold(gpu):
+def test_noalloc_gemm_runs_unsplit_what_it_cannot_hold(gpu):
     m, n, k = 768, 12288, 65536      # 256 x 192 tiles, K split four ways: 144 MB of partials
     need = kernels.gemm_workspace_bytes(m, n, k, gpu)
     assert need > _abi.GEMM_SCRATCH_BYTES
-    q = torch.zeros((m, k), dtype=torch.int8, device=gpu)
-    w = torch.zeros((n, k), dtype=torch.int8, device=gpu)
+    gg = torch.Generator(device=gpu).manual_seed(9)
+    q = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=gpu, generator=gg)
+    w = torch.randint(-128, 128, (n, k), dtype=torch.int8, device=gpu, generator=gg)
+    ref = kernels.gemm(q, w)                               # split K in a torch workspace
     out = torch.full((m, n), 5, dtype=torch.int32, device=gpu)
     rc, msg = _noalloc(_args(q, w, out, _abi.EPI_INT32))
-    assert rc == _abi.ERR_INVALID and 'static scratch' in msg
+    assert rc == _abi.OK, msg
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
     ws = torch.empty(1024, dtype=torch.uint8, device=gpu)
-    small = torch.zeros((200, 1000), dtype=torch.int32, device=gpu)
+    small = torch.full((200, 1000), 5, dtype=torch.int32, device=gpu)
     rc, msg = _noalloc(_args(q[:200, :4096], w[:1000, :4096], small, _abi.EPI_INT32, workspace=ws.data_ptr(),
                              workspace_bytes=1024))
     assert rc == _abi.ERR_INVALID and 'replaces the workspace' in msg
     torch.cuda.synchronize()
-    assert bool((out == 5).all())                          # nothing was launched
+    assert bool((small == 5).all())                        # nothing was launched
+
+
+def test_noalloc_split_gemm_replays_in_a_graph(gpu):
+    m, n, k = 512, 4096, 14336       # 128 x 256 tiles, K split four ways, finished in the kernel
+    assert 0 < kernels.gemm_workspace_bytes(m, n, k, gpu) <= _abi.GEMM_SCRATCH_BYTES
+    g = torch.Generator().manual_seed(10)
+    q = randi8(g, (m, k)).to(gpu)
+    w = randi8(g, (n, k)).to(gpu)
+    a = (torch.rand((m, 1), generator=g) * 1e-2).to(gpu)
+    s = (torch.rand((n, 1), generator=g) * 1e-3).to(gpu)
+    ref = kernels.gemm(q, w, epilogue=kernels.EPI_ROW, row_scale=a, col_scale=s, out_dtype=torch.float16)
+    q2 = randi8(g, (200, 4096)).to(gpu)                    # another split shape sharing the scratch
+    w2 = randi8(g, (1000, 4096)).to(gpu)
+    ref2 = kernels.gemm(q2, w2)
+    out = torch.zeros((m, n), dtype=torch.float16, device=gpu)
+    out2 = torch.zeros((200, 1000), dtype=torch.int32, device=gpu)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        rc, msg = _noalloc(_args(q, w, out, _abi.EPI_ROW, a.reshape(-1), s.reshape(-1)))   # eager, on the stream
+        assert rc == _abi.OK, msg
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=stream):
+            rc, msg = _noalloc(_args(q, w, out, _abi.EPI_ROW, a.reshape(-1), s.reshape(-1)))
+        assert rc == _abi.OK, msg
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.fill_(float('nan'))
+        out2.fill_(-1)
+        rc, msg = _noalloc(_args(q2, w2, out2, _abi.EPI_INT32))   # overwrites the scratch between replays
+        assert rc == _abi.OK, msg
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref2), rep
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), rep
