@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 12
+#define W8A8_ABI_VERSION 13
 
 typedef enum w8a8_status {
   W8A8_OK = 0,
@@ -79,6 +79,12 @@ typedef enum w8a8_epilogue {
  *   to the MAX exchange (patches/tilelang_row_quant.py:49-62 maximum_kernel,
  *   :136-146). Requires row_max == NULL. With q == scale == NULL only the
  *   maximum is computed (the maximum phase).
+ * convrot_signs: optional [cols] sign words for a seeded ConvRot (with
+ *   convrot, 16-byte aligned): 0 keeps column j, 0x80000000 negates it
+ *   before the rotation, which becomes diag(s) then H (s = +-1; weights
+ *   rotated the same way keep the GEMM unchanged). NULL: s = +1, the
+ *   reference's ConvRot. No counterpart in the reference (an option of the
+ *   configuration it is benchmarked on).
  * Requirements: cols % 16 == 0 (cols % 256 == 0 with convrot), x, q 16-byte
  *   aligned, ldx * elem and ldq multiples of 16 bytes.
  */
@@ -97,6 +103,7 @@ typedef struct W8A8QuantArgs {
   float* scale;
   void* stream;
   float* row_max_out;
+  const uint32_t* convrot_signs;
 } W8A8QuantArgs;
 
 int w8a8_quantize_rows(const W8A8QuantArgs* args);
@@ -116,6 +123,8 @@ int w8a8_quantize_rows(const W8A8QuantArgs* args);
  * group_max: optional [rows, width/256] output of per-group absmax.
  * q: [rows, width] int8 (row stride ldq) or NULL (maximum phase only).
  * scale: [rows] fp32 (required when q is non-NULL).
+ * convrot_signs: optional [width] sign words applied to the SwiGLU output
+ *   before its rotation, as in w8a8_quantize_rows.
  */
 typedef struct W8A8SwigluArgs {
   uint32_t struct_size;
@@ -131,6 +140,7 @@ typedef struct W8A8SwigluArgs {
   int64_t ldq;
   float* scale;
   void* stream;
+  const uint32_t* convrot_signs;
 } W8A8SwigluArgs;
 
 int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
@@ -155,8 +165,9 @@ int w8a8_swiglu_quantize(const W8A8SwigluArgs* args);
  *   inv  = 1 / sqrt(ss * fp32(1/cols) + eps)      (IEEE sqrt and division)
  *   y    = x_dtype(((((x * inv) * w) * (1 + mod_scale[l])) + mod_shift[l]))
  * y: optional [rows, cols] x_dtype output of the normalized rows (ldy).
- * convrot, round_rotated, q, ldq, q_scale: as w8a8_quantize_rows applied to
- *   y. q NULL runs the norm alone (y required).
+ * convrot, round_rotated, q, ldq, q_scale, convrot_signs: as
+ *   w8a8_quantize_rows applied to y. q NULL runs the norm alone (y
+ *   required).
  * Requirements: cols % 16 == 0 (cols % 256 == 0 with convrot and q), x, y,
  *   q and every table 16-byte aligned with 16-byte row strides.
  */
@@ -182,6 +193,7 @@ typedef struct W8A8NormArgs {
   int64_t ldq;
   float* q_scale;
   void* stream;
+  const uint32_t* convrot_signs;
 } W8A8NormArgs;
 
 int w8a8_norm_quantize(const W8A8NormArgs* args);

@@ -17,12 +17,12 @@ void set_error(const char* fmt, ...) {
 
 }  // namespace w8a8
 
-static_assert(sizeof(W8A8QuantArgs) == 96, "W8A8QuantArgs layout");
-static_assert(sizeof(W8A8SwigluArgs) == 96, "W8A8SwigluArgs layout");
+static_assert(sizeof(W8A8QuantArgs) == 104, "W8A8QuantArgs layout");
+static_assert(sizeof(W8A8SwigluArgs) == 104, "W8A8SwigluArgs layout");
 static_assert(sizeof(W8A8GemmArgs) == 192, "W8A8GemmArgs layout");
 static_assert(sizeof(W8A8RopeEpilogue) == 48, "W8A8RopeEpilogue layout");
 static_assert(sizeof(W8A8DequantArgs) == 144, "W8A8DequantArgs layout");
-static_assert(sizeof(W8A8NormArgs) == 144, "W8A8NormArgs layout");
+static_assert(sizeof(W8A8NormArgs) == 152, "W8A8NormArgs layout");
 static_assert(sizeof(W8A8RmsRopeArgs) == 104, "W8A8RmsRopeArgs layout");
 static_assert(sizeof(W8A8AttnPrepareArgs) == 224, "W8A8AttnPrepareArgs layout");
 static_assert(sizeof(W8A8AttentionArgs) == 144, "W8A8AttentionArgs layout");

@@ -31,6 +31,7 @@ struct NormParams {
   int8_t* q;
   int64_t ldq;
   float* qscale;
+  const uint32_t* signs;   // ConvRot sign words (0 or 0x80000000 per column), or null
 };
 
 // MODE: 0 norm only, 1 quantize, 2 ConvRot256 (fp32) + quantize,
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(64 * W) void norm_quant_kernel(NormParams p) {
       dst[1] = make_uint4(bits[4], bits[5], bits[6], bits[7]);
     }
     if constexpr (ROT != 0) {
-      convrot256_lanes<true>(v, buf, t);
+      convrot256_lanes<true>(v, buf, t, p.signs ? p.signs + 256 * (u >> 4) : nullptr);
       if constexpr (ROT == 2) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = round_to<DT>(v[i]);
@@ -354,6 +355,9 @@ extern "C" int w8a8_norm_quantize(const W8A8NormArgs* a) {
   p.q = a->q;
   p.ldq = a->ldq;
   p.qscale = a->q_scale;
+  W8A8_REQUIRE(a->convrot_signs == nullptr || (a->q && a->convrot && aligned16(a->convrot_signs)),
+               "w8a8_norm_quantize: convrot_signs needs q, convrot and a 16-byte aligned array");
+  p.signs = a->convrot_signs;
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
   const int mode = a->q == nullptr ? 0 : a->convrot == 0 ? 1 : a->round_rotated ? 3 : 2;
   if (a->x_dtype == W8A8_F16) {

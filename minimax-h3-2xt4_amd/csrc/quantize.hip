@@ -26,7 +26,7 @@ template <int DT, int ROT, int J>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t cols,
     const float* __restrict__ row_max, int8_t* __restrict__ q, int64_t ldq,
-    float* __restrict__ scale, float* __restrict__ row_max_out) {
+    float* __restrict__ scale, float* __restrict__ row_max_out, const uint32_t* __restrict__ signs) {
   __shared__ float lds[ROT ? kQuantWaves * kRotWave : 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + wave;
@@ -37,10 +37,12 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
   float* buf = ROT ? rot_slot(lds, wave, lane) : nullptr;
   const int t = lane & 15;
 
+  // The sign words of unit u's 256-column group (ConvRot with signs).
+  auto smask = [&](int u) { return signs ? signs + 256 * (u >> 4) : nullptr; };
   auto load_unit = [&](int u, float (&v)[16]) {
     load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v);
     if constexpr (ROT != 0) {
-      convrot256_lanes<true>(v, buf, t);
+      convrot256_lanes<true>(v, buf, t, smask(u));
       if constexpr (ROT == 2) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = round_to<DT>(v[i]);
@@ -80,7 +82,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
       float (&vj)[16] = v[KEEP16 ? 0 : j];
       unpack16<DT>(raw[j], vj);
       if constexpr (ROT != 0) {
-        convrot256_lanes<true>(vj, buf, t);
+        convrot256_lanes<true>(vj, buf, t, smask(min(lane + 64 * j, units - 1)));
         if constexpr (ROT == 2 && !KEEP16) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) vj[i] = round_to<DT>(vj[i]);
@@ -162,7 +164,8 @@ constexpr int row_wg_lds_bytes() { return ((ROT ? W * kRotWave : 0) + W) * 4; }
 template <int DT, int ROT, int J, int W>
 __global__ __launch_bounds__(64 * W) void quantize_row_wg_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t cols, const float* __restrict__ row_max,
-    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, float* __restrict__ row_max_out) {
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, float* __restrict__ row_max_out,
+    const uint32_t* __restrict__ signs) {
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* const lds = smem;
   float* const wmax = smem + (ROT ? W * kRotWave : 0);
@@ -180,7 +183,7 @@ __global__ __launch_bounds__(64 * W) void quantize_row_wg_kernel(
     if (u < units) {
       load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v[j]);
       if constexpr (ROT != 0) {
-        convrot256_lanes<true>(v[j], buf, t);
+        convrot256_lanes<true>(v[j], buf, t, signs ? signs + 256 * (u >> 4) : nullptr);
         if constexpr (ROT == 2) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) v[j][i] = round_to<DT>(v[j][i]);
@@ -243,7 +246,7 @@ static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
         enabled.fetch_or(bit, std::memory_order_acq_rel);
       }
       hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, 1, 16>), g, dim3(1024), kLds, stream, a->x, a->ldx,
-                         a->cols, a->row_max, a->q, a->ldq, a->scale, a->row_max_out);
+                         a->cols, a->row_max, a->q, a->ldq, a->scale, a->row_max_out, a->convrot_signs);
       return launch_status("w8a8_quantize_rows");
     }
     const int jw = (int)((a->cols / 16 + 255) / 256);
@@ -251,7 +254,7 @@ static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
     constexpr int kLds4 = row_wg_lds_bytes<ROT, 4>();
 #define W8A8_WLAUNCH(JJ)                                                                                    \
   hipLaunchKernelGGL((quantize_row_wg_kernel<DT, ROT, JJ, 4>), g, b, kLds4, stream, a->x, a->ldx, a->cols, \
-                     a->row_max, a->q, a->ldq, a->scale, a->row_max_out)
+                     a->row_max, a->q, a->ldq, a->scale, a->row_max_out, a->convrot_signs)
     switch (jw) {
       case 1: W8A8_WLAUNCH(1); break;
       case 2: W8A8_WLAUNCH(2); break;
@@ -267,7 +270,7 @@ static int launch_quantize(const W8A8QuantArgs* a, hipStream_t stream) {
   const dim3 block(64 * kQuantWaves);
 #define W8A8_QLAUNCH(JJ)                                                                      \
   hipLaunchKernelGGL((quantize_rows_kernel<DT, ROT, JJ>), grid, block, 0, stream, a->x, a->ldx, \
-                     a->rows, a->cols, a->row_max, a->q, a->ldq, a->scale, a->row_max_out)
+                     a->rows, a->cols, a->row_max, a->q, a->ldq, a->scale, a->row_max_out, a->convrot_signs)
   switch (jneed) {
     case 1: W8A8_QLAUNCH(1); break;
     case 2: W8A8_QLAUNCH(2); break;
@@ -310,6 +313,8 @@ extern "C" int w8a8_quantize_rows(const W8A8QuantArgs* a) {
   W8A8_REQUIRE(aligned16(a->x) && (a->ldx * es) % 16 == 0 &&
                (a->q == nullptr || (aligned16(a->q) && a->ldq % 16 == 0)),
                "w8a8_quantize_rows: x/q must be 16-byte aligned with 16-byte row strides");
+  W8A8_REQUIRE(a->convrot_signs == nullptr || (a->convrot && aligned16(a->convrot_signs)),
+               "w8a8_quantize_rows: convrot_signs needs convrot and a 16-byte aligned array");
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
   W8A8_REQUIRE(a->round_rotated == 0 || a->round_rotated == 1, "w8a8_quantize_rows: round_rotated must be 0 or 1");
   const int mode = a->convrot == 0 ? 0 : (a->round_rotated && a->x_dtype != W8A8_F32) ? 2 : 1;

@@ -35,7 +35,7 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t width,
     const float* __restrict__ row_max_in, float* __restrict__ row_max_out,
     float* __restrict__ group_max, int8_t* __restrict__ q, int64_t ldq,
-    float* __restrict__ scale) {
+    float* __restrict__ scale, const uint32_t* __restrict__ signs) {
   constexpr int kWaves = W, kSlots = 4 * kWaves;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* const lds = smem;
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
     load16<DT>(xrow + (width + (int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), uv);
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = DT == kF16 ? swiglu_fp16_gate(gv[i], uv[i]) : swiglu(gv[i], uv[i]);
-    convrot256_lanes<true>(v, buf, t);
+    convrot256_lanes<true>(v, buf, t, signs ? signs + 256 * g : nullptr);
   };
   auto group_absmax = [&](int g, const float (&v)[16]) {
     float m = 0.0f;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         v[p][i] = DT == kF16 ? swiglu_fp16_gate(gv[i], uv[i]) : swiglu(gv[i], uv[i]);
-      convrot256_lanes<true>(v[p], buf, t);
+      convrot256_lanes<true>(v[p], buf, t, signs ? signs + 256 * min(g, groups - 1) : nullptr);
       float m = 0.0f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[p][j]));
@@ -157,7 +157,7 @@ static void launch_swiglu_w(const W8A8SwigluArgs* a, hipStream_t stream) {
 #define W8A8_SLAUNCH(PP)                                                                                 \
   hipLaunchKernelGGL((swiglu_quant_kernel<DT, PP, W>), grid, block, swiglu_lds_bytes<W>(), stream, a->x, \
                      a->ldx, a->rows, a->width, a->row_max, a->row_max_out, a->group_max, a->q, a->ldq,  \
-                     a->scale)
+                     a->scale, a->convrot_signs)
   switch (passes) {
     case 1: W8A8_SLAUNCH(1); break;
     case 2: W8A8_SLAUNCH(2); break;
@@ -235,6 +235,8 @@ extern "C" int w8a8_swiglu_quantize(const W8A8SwigluArgs* a) {
     W8A8_REQUIRE(a->ldq >= a->width && a->ldq % 16 == 0 && aligned16(a->q),
                  "w8a8_swiglu_quantize: q must be 16-byte aligned with ldq >= width, ldq %% 16 == 0");
   }
+  W8A8_REQUIRE(a->convrot_signs == nullptr || aligned16(a->convrot_signs),
+               "w8a8_swiglu_quantize: convrot_signs must be 16-byte aligned");
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
   return a->x_dtype == W8A8_F16 ? launch_swiglu<kF16>(a, stream) : launch_swiglu<kF32>(a, stream);
 }

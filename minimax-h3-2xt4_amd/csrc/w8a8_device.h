@@ -277,8 +277,23 @@ __device__ __forceinline__ float* rot_slot(float* lds, int wave, int lane) {
 // slot (rot_slot). On return, if NATURAL, v again holds elements
 // 16t..16t+15; otherwise v[j] holds element 16j + t. The 1/16 factor is
 // applied last, as in the reference butterfly.
+// smask (optional, wave-uniformly null or not): the group's 256 sign words,
+// 0 or 0x80000000 per element, XORed into the values first: the rotation
+// diag(s) then H, with s a +-1 vector (exact: only signs change).
 template <bool NATURAL>
-__device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int t) {
+__device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int t,
+                                                 const uint32_t* smask = nullptr) {
+  if (smask != nullptr) {
+    const uint4* m = reinterpret_cast<const uint4*>(smask + 16 * t);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 w = m[i];
+      v[4 * i] = __uint_as_float(__float_as_uint(v[4 * i]) ^ w.x);
+      v[4 * i + 1] = __uint_as_float(__float_as_uint(v[4 * i + 1]) ^ w.y);
+      v[4 * i + 2] = __uint_as_float(__float_as_uint(v[4 * i + 2]) ^ w.z);
+      v[4 * i + 3] = __uint_as_float(__float_as_uint(v[4 * i + 3]) ^ w.w);
+    }
+  }
   h4_low_digits(v);
   const int sw = (t >> 1) & 3;
   float4* row = reinterpret_cast<float4*>(buf + 16 * t);

@@ -15,7 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / 'libw8a8.so'
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_LAUNCH = 0, 1, 2, 3
 F16, BF16, F32, I32, I8 = 1, 2, 3, 4, 5
 EPI_INT32, EPI_ROW, EPI_COLUMN = 0, 1, 2
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _c = ctypes
 _p = ctypes.c_void_p
@@ -25,13 +25,14 @@ class QuantArgs(ctypes.Structure):
     _fields_ = [('struct_size', _c.c_uint32), ('x_dtype', _c.c_int32), ('x', _p), ('ldx', _c.c_int64),
                 ('rows', _c.c_int64), ('cols', _c.c_int64), ('convrot', _c.c_int32),
                 ('round_rotated', _c.c_int32), ('row_max', _p), ('q', _p), ('ldq', _c.c_int64),
-                ('scale', _p), ('stream', _p), ('row_max_out', _p)]
+                ('scale', _p), ('stream', _p), ('row_max_out', _p), ('convrot_signs', _p)]
 
 
 class SwigluArgs(ctypes.Structure):
     _fields_ = [('struct_size', _c.c_uint32), ('x_dtype', _c.c_int32), ('x', _p), ('ldx', _c.c_int64),
                 ('rows', _c.c_int64), ('width', _c.c_int64), ('row_max', _p), ('row_max_out', _p),
-                ('group_max', _p), ('q', _p), ('ldq', _c.c_int64), ('scale', _p), ('stream', _p)]
+                ('group_max', _p), ('q', _p), ('ldq', _c.c_int64), ('scale', _p), ('stream', _p),
+                ('convrot_signs', _p)]
 
 
 class RopeEpilogue(ctypes.Structure):
@@ -62,7 +63,8 @@ class NormArgs(ctypes.Structure):
                 ('rows', _c.c_int64), ('cols', _c.c_int64), ('weight', _p), ('mod_shift', _p),
                 ('mod_scale', _p), ('ld_mod', _c.c_int64), ('mod_rows', _c.c_int32), ('eps', _c.c_float),
                 ('labels', _p), ('y', _p), ('ldy', _c.c_int64), ('convrot', _c.c_int32),
-                ('round_rotated', _c.c_int32), ('q', _p), ('ldq', _c.c_int64), ('q_scale', _p), ('stream', _p)]
+                ('round_rotated', _c.c_int32), ('q', _p), ('ldq', _c.c_int64), ('q_scale', _p), ('stream', _p),
+                ('convrot_signs', _p)]
 
 
 class RmsRopeArgs(ctypes.Structure):

@@ -44,12 +44,13 @@ def _scale_vec(s, n, name):
     return s, (0 if s.numel() == 1 else 1)
 
 
-def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=None, scale_out=None):
+def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=None, scale_out=None, signs=None):
     """Per-row absmax INT8 quantization of x [M, K] -> (q int8 [M,K], scale fp32 [M,1]).
 
     convrot=True rotates each 256-column group first (regular-H4 ConvRot256);
     round_rotated rounds the rotated values to x's dtype before the absmax.
-    row_max [M] (or [M,1]) fp32 replaces the row's own absmax.
+    row_max [M] (or [M,1]) fp32 replaces the row's own absmax. signs: the
+    sign words of a seeded ConvRot (convrot.sign_words), with convrot.
     """
     x = _rows_2d(x)
     if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
@@ -74,17 +75,20 @@ def quantize_rows(x, *, convrot=False, round_rotated=True, row_max=None, out=Non
         row_max = row_max.to(torch.float32).reshape(-1).contiguous()
         if row_max.numel() != rows:
             raise ValueError('row_max must have one entry per row')
+    if signs is not None and not convrot:
+        raise ValueError('signs apply to the ConvRot256 rotation (convrot=True)')
+    signs = _sign_words(signs, cols, x.device)
     if rows == 0:
         return q, scale
     args = _abi.QuantArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows, cols=cols,
                           convrot=256 if convrot else 0, round_rotated=1 if round_rotated else 0,
                           row_max=_abi.ptr(row_max), q=q.data_ptr(), ldq=q.stride(0), scale=scale.data_ptr(),
-                          stream=_abi.stream_of(x))
+                          stream=_abi.stream_of(x), convrot_signs=_abi.ptr(signs))
     _abi.call('w8a8_quantize_rows', args)
     return q, scale
 
 
-def row_absmax(x, *, convrot=False, round_rotated=True):
+def row_absmax(x, *, convrot=False, round_rotated=True, signs=None):
     """Maximum phase of quantize_rows: fp32 [M, 1] row absmax of x [M, K]
     (after ConvRot256 when convrot), the value a tensor-parallel owner of a
     K slice contributes to the MAX exchange before quantizing with the
@@ -97,6 +101,9 @@ def row_absmax(x, *, convrot=False, round_rotated=True):
     if (convrot and cols % 256) or cols % 16:
         raise ValueError('input features must be a multiple of 16 (256 with ConvRot256)')
     _device(x)
+    if signs is not None and not convrot:
+        raise ValueError('signs apply to the ConvRot256 rotation (convrot=True)')
+    signs = _sign_words(signs, cols, x.device)
     res = torch.empty((rows, 1), dtype=torch.float32, device=x.device)
     if rows == 0:
         return res
@@ -105,9 +112,21 @@ def row_absmax(x, *, convrot=False, round_rotated=True):
     args = _abi.QuantArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows, cols=cols,
                           convrot=256 if convrot else 0, round_rotated=1 if round_rotated else 0,
                           row_max=None, q=None, ldq=0, scale=None, stream=_abi.stream_of(x),
-                          row_max_out=res.data_ptr())
+                          row_max_out=res.data_ptr(), convrot_signs=_abi.ptr(signs))
     _abi.call('w8a8_quantize_rows', args)
     return res
+
+
+def _sign_words(signs, cols, device):
+    """Check a ConvRot sign-word tensor (convrot.sign_words): int32 [cols],
+    contiguous and 16-byte aligned on device; None stays None."""
+    if signs is None:
+        return None
+    if signs.dtype != torch.int32 or signs.numel() != cols or not signs.is_contiguous() or signs.data_ptr() % 16:
+        raise ValueError(f'signs must be the int32 sign words of convrot.sign_words ({cols} entries, contiguous)')
+    if signs.device != device:
+        raise ValueError('all tensors must be on the same device')
+    return signs
 
 
 def _table(t, name, cols):
@@ -119,7 +138,7 @@ def _table(t, name, cols):
 
 
 def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, *, eps, quantize=True, convrot=True,
-                  round_rotated=True, want_normalized=False):
+                  round_rotated=True, want_normalized=False, signs=None):
     """Modulated RMSNorm of x [M, K] (F16/BF16), optionally fused with
     ConvRot256 and per-row INT8 quantization.
 
@@ -128,7 +147,9 @@ def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, *, eps, q
     no gain); shift/scale fp32 [R, K] AdaLN tables with labels int32 [M]
     (each row's table row), or None for a plain RMSNorm.
     Returns a dict with 'q' [M,K] int8 and 'scale' [M,1] fp32 when quantize,
-    and 'y' [M,K] (x's dtype) when want_normalized or not quantize.
+    and 'y' [M,K] (x's dtype) when want_normalized or not quantize. signs:
+    the sign words of a seeded ConvRot (convrot.sign_words), with quantize
+    and convrot.
     """
     x = _rows_2d(x)
     _device(x, weight, shift, scale, labels)
@@ -159,6 +180,9 @@ def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, *, eps, q
         if labels is None or labels.dtype != torch.int32 or labels.numel() != rows:
             raise ValueError('modulation tables need int32 labels, one per row')
         labels = labels.reshape(-1).contiguous()
+    if signs is not None and not (quantize and convrot):
+        raise ValueError('signs apply to the ConvRot256 rotation of the quantized output')
+    signs = _sign_words(signs, cols, x.device)
     out = {}
     want_y = want_normalized or not quantize
     y = torch.empty((rows, cols), dtype=x.dtype, device=x.device) if want_y else None
@@ -177,7 +201,7 @@ def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, *, eps, q
                          labels=_abi.ptr(labels), y=_abi.ptr(y), ldy=cols if y is not None else 0,
                          convrot=256 if convrot else 0, round_rotated=1 if round_rotated else 0,
                          q=_abi.ptr(q), ldq=cols if q is not None else 0, q_scale=_abi.ptr(qs),
-                         stream=_abi.stream_of(x))
+                         stream=_abi.stream_of(x), convrot_signs=_abi.ptr(signs))
     _abi.call('w8a8_norm_quantize', args)
     return out
 
@@ -225,12 +249,13 @@ def rms_rope(packed, freqs, q_gain, k_gain, *, heads, rot_dim, eps, dim=128, out
     return q, k
 
 
-def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_group_max=False):
+def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_group_max=False, signs=None):
     """Fused FP32 SwiGLU -> ConvRot256 -> row absmax -> INT8 of x [M, 2W].
 
     Returns a dict with 'q' [M,W] int8 and 'scale' [M,1] fp32 (when
     quantize), 'row_max' [M,1] and 'group_max' [M,W/256] when requested.
-    row_max (input) is an external absmax for the quantization.
+    row_max (input) is an external absmax for the quantization. signs: the
+    sign words of a seeded ConvRot (convrot.sign_words) of width W.
     """
     x = _rows_2d(x)
     _device(x, row_max)
@@ -255,12 +280,14 @@ def swiglu_quantize(x, *, row_max=None, quantize=True, want_row_max=False, want_
         row_max = row_max.to(torch.float32).reshape(-1).contiguous()
         if row_max.numel() != rows:
             raise ValueError('row_max must have one entry per row')
+    signs = _sign_words(signs, width, dev)
     if rows == 0:
         return res
     args = _abi.SwigluArgs(x_dtype=_abi.DTYPE_CODE[x.dtype], x=x.data_ptr(), ldx=x.stride(0), rows=rows,
                            width=width, row_max=_abi.ptr(row_max), row_max_out=_abi.ptr(res.get('row_max')),
                            group_max=_abi.ptr(res.get('group_max')), q=_abi.ptr(res.get('q')),
-                           ldq=width, scale=_abi.ptr(res.get('scale')), stream=_abi.stream_of(x))
+                           ldq=width, scale=_abi.ptr(res.get('scale')), stream=_abi.stream_of(x),
+                           convrot_signs=_abi.ptr(signs))
     _abi.call('w8a8_swiglu_quantize', args)
     return res
 

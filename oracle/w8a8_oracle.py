@@ -111,17 +111,26 @@ def hadamard256():
     return np.where(count % 2 == 0, 1.0, -1.0) / 16.0
 
 
-def convrot256(x):
+def convrot256(x, signs=None):
     """Regular-H4 ConvRot256 butterfly in fp32 over each 256-column group.
 
     Follows patches/tilelang_swiglu_quant.py:26-36 and :46: four stages with
     strides 1, 4, 16, 64; at output digit d the input at position 3-d is
     negated and the four inputs are summed as ((p + q) + r) + s in input
     order; after the last stage the values are multiplied by fp32(1/16).
+    signs (optional, one +-1 per column; no counterpart in the reference,
+    whose rotation has fixed signs): column j is negated first where
+    signs[j] < 0, so the rotation is diag(signs) then H (a sign change is
+    exact).
     """
     x = _f32(x)
     if x.shape[-1] % GROUP:
         raise ValueError('whole 256-column groups required')
+    if signs is not None:
+        s = np.asarray(signs).reshape(-1)
+        if s.size != x.shape[-1]:
+            raise ValueError('one sign per column required')
+        x = np.where(s < 0, -x, x).astype(np.float32)
     shape = x.shape
     a = x.reshape(-1, GROUP).copy()
     for stage in range(4):
@@ -179,7 +188,7 @@ def swiglu_f32(gate, up):
         return (act * u).astype(np.float32)
 
 
-def prepare_activation(x, convrot=True, x_dtype='f16'):
+def prepare_activation(x, convrot=True, x_dtype='f16', signs=None):
     """Column-path activation preparation: optional ConvRot256, then quantize.
 
     Follows patches/dit_column_linear.py:13-21: the rotation runs in x's
@@ -193,7 +202,7 @@ def prepare_activation(x, convrot=True, x_dtype='f16'):
     """
     xf = _to_f32(x, x_dtype)
     if convrot:
-        r = convrot256(xf)
+        r = convrot256(xf, signs)
         if x_dtype == 'f16':
             with np.errstate(over='ignore'):
                 r = r.astype(np.float16).astype(np.float32)
@@ -203,7 +212,7 @@ def prepare_activation(x, convrot=True, x_dtype='f16'):
     return quantize_rows(xf.reshape(-1, xf.shape[-1]))
 
 
-def fc2_prologue(x, width=None, row_max=None, x_dtype='f16', return_rotated=False):
+def fc2_prologue(x, width=None, row_max=None, x_dtype='f16', return_rotated=False, signs=None):
     """Fused FC2 prologue: FP32 SwiGLU -> ConvRot256 -> row absmax -> quantize.
 
     Follows patches/tilelang_swiglu_quant.py:38-51 (stored phase: SwiGLU,
@@ -220,7 +229,7 @@ def fc2_prologue(x, width=None, row_max=None, x_dtype='f16', return_rotated=Fals
     if w % GROUP or xf.shape[1] != 2 * w:
         raise ValueError('[M, 2W] input with W % 256 == 0 required')
     act = swiglu_f32(xf[:, :w], xf[:, w:])
-    rot = convrot256(act)
+    rot = convrot256(act, signs)
     gmax = np.abs(rot).reshape(rot.shape[0], w // GROUP, GROUP).max(-1)
     rmax = gmax.max(-1) if row_max is None else _f32(row_max).reshape(-1)
     q, scale = quantize_rows(rot, rmax)
@@ -405,7 +414,7 @@ def modulated_rms_norm(x, weight=None, shift=None, scale=None, labels=None, eps=
 
 
 def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, eps=1e-6, x_dtype='f16', convrot=True,
-                  round_rotated=True):
+                  round_rotated=True, signs=None):
     """Modulated RMSNorm followed by the column path's activation preparation.
 
     The composition of patches/tilelang_dit_fusion.py:10-36 (normalized rows
@@ -415,9 +424,9 @@ def norm_quantize(x, weight=None, shift=None, scale=None, labels=None, eps=1e-6,
     """
     y = modulated_rms_norm(x, weight, shift, scale, labels, eps, x_dtype)
     if convrot and not round_rotated:
-        q, s = quantize_rows(convrot256(_to_f32(y, x_dtype)))
+        q, s = quantize_rows(convrot256(_to_f32(y, x_dtype), signs))
     else:
-        q, s = prepare_activation(y, convrot, x_dtype)
+        q, s = prepare_activation(y, convrot, x_dtype, signs)
     return q, s, y
 
 

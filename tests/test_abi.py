@@ -35,7 +35,7 @@ def test_version_and_struct_sizes():
         assert lib.w8a8_struct_size(i) == ctypes.sizeof(st)
     assert lib.w8a8_struct_size(99) == -1
     # header field order: sizes computed from the C declaration
-    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [96, 96, 192, 144, 144, 104, 224, 144]
+    assert [ctypes.sizeof(s) for s in _abi.STRUCTS] == [104, 104, 192, 144, 152, 104, 224, 144]
     assert ctypes.sizeof(_abi.RopeEpilogue) == 48   # static_assert'ed in the library too
 
 
@@ -65,6 +65,10 @@ def test_quantize_argument_checks():
     _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'q': None, 'scale': None}), 'no output')
     _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'row_max': 4096, 'row_max_out': 4096}),
                     'own maximum')
+    # ConvRot sign words need the rotation and a 16-byte aligned array
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'convrot_signs': 4096}), 'convrot_signs')
+    _expect_invalid('w8a8_quantize_rows', _abi.QuantArgs(**{**base, 'convrot': 256, 'convrot_signs': 4100}),
+                    'convrot_signs')
 
 
 def test_gemm_argument_checks():
@@ -155,6 +159,7 @@ def test_swiglu_argument_checks():
     _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'x_dtype': _abi.BF16}), 'x_dtype')
     _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'q': None, 'scale': None}), 'no output')
     _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'ldx': 256}), 'ldx')
+    _expect_invalid('w8a8_swiglu_quantize', _abi.SwigluArgs(**{**base, 'convrot_signs': 4100}), 'convrot_signs')
 
 
 def test_dequantize_argument_checks():
@@ -180,6 +185,8 @@ def test_norm_argument_checks():
                                                             'ld_mod': 250, 'mod_rows': 3, 'labels': 64}), 'ld_mod')
     _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'weight': 4100}), 'weight')
     _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'ldx': 200}), 'ldx')
+    _expect_invalid('w8a8_norm_quantize', _abi.NormArgs(**{**base, 'convrot': 0, 'convrot_signs': 4096}),
+                    'convrot_signs')
     # without quantization a 16-column multiple is enough
     n = _abi.NormArgs(**{**base, 'q': None, 'q_scale': None, 'y': 8192, 'ldy': 272, 'cols': 272, 'ldx': 272,
                          'rows': 0})

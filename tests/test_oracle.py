@@ -107,6 +107,47 @@ def test_butterfly_unit_vectors_and_norm():
     assert np.allclose(n0, n1, rtol=1e-6)
 
 
+def test_signed_butterfly_equals_closed_form_and_inverts():
+    # (x diag(s)) H exactly on integers (sums of 256 small integers / 16 are
+    # exact in fp32); H H = I, so rotating again and re-applying the signs
+    # gives x back, which a sign applied after the butterfly instead of
+    # before would not.
+    rng = np.random.default_rng(5)
+    x = rng.integers(-2000, 2000, (7, 768)).astype(np.float32)
+    s = rng.choice(np.array([-1, 1], np.int8), 768)
+    ref = ((x.astype(np.float64) * s).reshape(-1, 256) @ o.hadamard256()).reshape(x.shape)
+    r = o.convrot256(x, s)
+    assert np.array_equal(r.astype(np.float64), ref)
+    back = o.convrot256(r * 16) / 16
+    assert np.array_equal(back * s, x)
+    assert not np.array_equal(o.convrot256(x * s)[0], (o.convrot256(x) * s)[0])
+    # all-positive signs are the unsigned rotation; a single negated column j
+    # of the identity gives -H[j]
+    assert np.array_equal(o.convrot256(x, np.ones(768, np.int8)), o.convrot256(x))
+    eye = np.eye(256, dtype=np.float32)
+    one = np.ones(256, np.int8)
+    one[37] = -1
+    assert np.array_equal(o.convrot256(eye, one).astype(np.float64)[37], -o.hadamard256()[37])
+    assert np.array_equal(o.convrot256(eye, one)[36], o.convrot256(eye)[36])
+
+
+def test_signed_prologues_rotate_before_quantizing():
+    # The FC2 prologue and the column path with signs equal their unsigned
+    # forms on inputs whose marked columns are negated first (SwiGLU is
+    # applied before the rotation, so the signs act on its output).
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((5, 1024)) * 3).astype(np.float16)
+    s = rng.choice(np.array([-1, 1], np.int8), 512)
+    q, sc, gm = o.fc2_prologue(x, signs=s)
+    act = o.swiglu_f32(x[:, :512].astype(np.float32), x[:, 512:].astype(np.float32))
+    wq, ws = o.quantize_rows(o.convrot256(act * s))
+    assert np.array_equal(q, wq) and np.array_equal(sc, ws)
+    assert np.array_equal(gm, np.abs(o.convrot256(act * s)).reshape(5, 2, 256).max(-1))
+    xs = (x[:, :512] * s).astype(np.float16)
+    assert all(np.array_equal(a, b) for a, b in
+               zip(o.prepare_activation(x[:, :512], True, 'f16', signs=s), o.prepare_activation(xs, True, 'f16')))
+
+
 def test_butterfly_summation_order_left_to_right():
     # First quad [1e8, 1, -1e8, 1]: fp32 ((p+q)+r)+s gives -1, 2e8, 1, -2e8
     # (exact arithmetic would give 0, 2e8+2, 0, -2e8+2). The later stages only
