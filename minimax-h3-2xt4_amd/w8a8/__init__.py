@@ -5,6 +5,7 @@ Modules mirror the reference's operator API for this path:
   dit_column_linear  - column_linear / shared_column_linears
   swiglu_quant       - fused FP32 SwiGLU + ConvRot256 FC2 prologue, row_linear
   row_quant          - external-maximum quantizer
+  convrot            - seeded ConvRot sign vectors and the matching weight rotation
   column_epilogue    - column-order INT32 dequantization
   h3_operator_policy - operator selection for the row projections
   h3_tensor_flow     - residual divisor folding and residual add
@@ -15,4 +16,4 @@ Modules mirror the reference's operator API for this path:
 from . import _abi  # noqa: F401
 
 __all__ = ['kernels', 'parallel_int8', 'dit_column_linear', 'swiglu_quant', 'row_quant', 'column_epilogue',
-           'h3_operator_policy', 'h3_tensor_flow', 'tp_dit', 'workloads']
+           'h3_operator_policy', 'h3_tensor_flow', 'tp_dit', 'workloads', 'convrot']

@@ -33,9 +33,12 @@ def quantize(rotated, maximum, width=None, start=0, division='fast'):
 
 
 def maximum(x, width=None, start=0):
-    """Row absmax over the owned slice [start, start + width) -> fp32 [rows, 1]."""
+    """Row absmax over the owned slice [start, start + width) -> fp32 [rows, 1]
+    (the maximum phase of the quantize kernel: no codes are written)."""
     _check(x)
     width = x.shape[1] if width is None else width
-    if x.ndim != 2 or start < 0 or width < 1 or start + width > x.shape[1]:
+    if x.ndim != 2 or x.shape[0] < 1 or start < 0 or width < 1 or start + width > x.shape[1]:
         raise ValueError('Invalid owned slice')
-    return x[:, start:start + width].abs().amax(-1, keepdim=True)
+    if width % 16 or start % 4:
+        raise ValueError('the owned slice must start on a 16-byte boundary and span a multiple of 16 columns')
+    return kernels.row_absmax(x[:, start:start + width])

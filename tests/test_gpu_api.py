@@ -104,6 +104,8 @@ def test_row_quant_and_column_epilogue_api(gpu):
     assert_bits_equal(np_of(s).reshape(-1), rs, 'row_quant scale')
     assert_bits_equal(np_of(row_quant.maximum(rot.to(gpu), 512, 256)).reshape(-1),
                       np.abs(np_of(rot)[:, 256:768]).max(1), 'row_quant maximum')
+    with pytest.raises(ValueError):
+        row_quant.maximum(rot.to(gpu), 500, 256)      # the kernel reads 16-column units
     acc = torch.randint(-2 ** 24, 2 ** 24, (9, 64), generator=g, dtype=torch.int32)
     a = torch.rand((9, 1), generator=g)
     w = torch.rand((64,), generator=g) * 1e-3
