@@ -356,13 +356,10 @@ int w8a8_attention(const W8A8AttentionArgs* args);
  *   aligned, any contents). When w8a8_gemm_workspace_size() is non-zero for
  *   the shape and the workspace holds at least that many bytes, grids too
  *   small to fill the GPU split K across workgroups: each writes exact int32
- *   partial sums into the workspace and counts itself in its output tile's
- *   arrival word there; the last of a tile's workgroups adds the partials
- *   and runs the epilogue, in the same launch (a workspace large enough for
- *   the partials but not the arrival words finishes in a second kernel).
- *   The result is bit-identical to the unsplit GEMM. NULL / 0 never splits.
- *   Calls that share a workspace must not overlap; calls in sequence may
- *   share one, and a captured graph may replay it.
+ *   partial sums into the workspace and a second kernel adds them and runs
+ *   the epilogue (the result is bit-identical to the unsplit GEMM). NULL / 0
+ *   never splits. Calls that share a workspace must not overlap; calls in
+ *   sequence may share one, and a captured graph may replay it.
  * rope: optional RMS-RoPE epilogue (W8A8RopeEpilogue) for a packed QKV
  *   projection: the Q and K heads of the output are normalized and rotated
  *   as w8a8_rms_rope would on the stored fp16 output, in the same kernel, so
@@ -434,16 +431,15 @@ int w8a8_gemm(const W8A8GemmArgs* args);
  * w8a8_gemm that allocates nothing and takes no workspace. No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). The split-K partials and arrival words go to a file-scope
- * device array of W8A8_GEMM_SCRATCH_BYTES per GPU, which the library holds
- * until the process ends; a shape whose split needs more runs unsplit (the
- * same result, more slowly). A non-NULL args->workspace or a non-zero
- * workspace_bytes is rejected (W8A8_ERR_INVALID). Every call on one GPU
- * shares that GPU's array, so calls that overlap on one GPU (e.g. on two
- * streams) race. Nothing in the array needs clearing: every split writes its
- * whole partial tile before the finish reads it, and an arrival word left by
- * another call or shape starts a fresh count. Otherwise identical to
- * w8a8_gemm (same arguments, numerics and errors).
+ * hipMalloc). The split-K partials go to a file-scope device array of
+ * W8A8_GEMM_SCRATCH_BYTES per GPU, which the library holds until the process
+ * ends; a shape whose split needs more runs unsplit (the same result, more
+ * slowly). A non-NULL args->workspace or a non-zero workspace_bytes is
+ * rejected (W8A8_ERR_INVALID). Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU (e.g. on two streams) race.
+ * Nothing in the array needs clearing: every split writes its whole partial
+ * tile before the reduction reads it. Otherwise identical to w8a8_gemm (same
+ * arguments, numerics and errors).
  */
 #define W8A8_GEMM_SCRATCH_BYTES (64ll << 20)
 int w8a8_gemm_noalloc(const W8A8GemmArgs* args);

@@ -34,7 +34,7 @@ int gemm_ksplit(int64_t m, int64_t n, int64_t k, int dev, int64_t* workspace_byt
   if (k % kSK != 0) return 1;
   if ((m - 1) * k + k >= (1ll << 32) || (n - 1) * k + k >= (1ll << 32)) return 1;
   const GemmPlan plan = gemm_plan(m, n, k, device_cus(dev));
-  *workspace_bytes = plan_workspace_bytes(m, n, plan);
+  *workspace_bytes = split_partials_bytes(m, n, plan.ksplit);
   return plan.ksplit;
 }
 #endif

@@ -210,12 +210,7 @@ __device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xF | (
 
 // Compile-time epilogue options of the persistent kernel (each variant
 // carries only the loads it uses).
-enum EpilogueFlags { kWithBias = 1, kWithResidual = 2, kWithGate = 4, kWithRope = 8, kSplitFin = 16 };
-
-// FLAGS of the persistent kernel's split-K pass with the in-kernel finish:
-// the work items store int32 partials, and the last to arrive at a tile runs
-// the call's epilogue (final EPI in bits 5-6, final OUT in bits 7-9).
-constexpr int split_fin_flags(int epi, int out) { return kSplitFin | (epi << 5) | (out << 7); }
+enum EpilogueFlags { kWithBias = 1, kWithResidual = 2, kWithGate = 4, kWithRope = 8 };
 
 // Layout of the staged epilogue's read-out: a lane owns CPL consecutive
 // columns of a 64-column half of the quadrant (8 for 2-byte outputs, 4 for
@@ -819,7 +814,6 @@ __device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw,
 // rows x one chunk per 16-lane group) free of bank conflicts. A DMA lane
 // therefore loads the logical chunk that lands on its physical slot.
 constexpr int kSK = 128;                    // K bytes per stage
-constexpr int kMaxSplitFin = 8;             // largest K split of a plan (gemm_plan's max_split)
 constexpr int kSTile = 256 * kSK;           // one operand tile of one stage (32 KB): a ring slot
 constexpr int kSlots = 5;                   // ring of half stages
 constexpr int kPersistentLds = kSlots * kSTile;
@@ -846,80 +840,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   if constexpr (LO < HI) {
     f(std::integral_constant<int, LO>{});
     static_for<LO + 1, HI>(f);
-  }
-}
-
-// Split-K finish of one output tile, run by every work item of the tile
-// right after it stored its int32 partial (tile pid `tile`, raster position
-// tm, tn): count the arrival; the last of the ksplit items adds the partial
-// planes and runs the call's epilogue (epilogue4 with the final EPI and OUT
-// carried in FLAGS). flag is 4 bytes of this workgroup's LDS that no DMA
-// writes before the next block barrier.
-//
-// Ordering: each wave's release fence at agent scope (an L2 write-back on
-// gfx950) makes its partial stores visible before thread 0 counts the
-// arrival; the last arrival's waves take the acquire fence (an L2
-// invalidate) before reading the other items' planes. The arrival word of
-// the tile holds (tag << 8) | arrivals; an arrival that finds another tag
-// (an earlier call, or memory never written) starts the count at 1, and the
-// last arrival clears the word to 0, a tag no call uses, so a replayed HIP
-// graph (same tag) starts from a cleared word. The update is a
-// compare-and-swap loop on one lane: each failed attempt means another
-// arrival's attempt succeeded, so it ends after at most ksplit tries.
-template <int FLAGS, int BM, int BN>
-__device__ __forceinline__ void split_finish(const GemmParams& p, int tile, int tm, int tn, int ksplit,
-                                             int8_t* flag_lds) {
-  constexpr int FE = (FLAGS >> 5) & 3, FO = (FLAGS >> 7) & 7;
-  const int tid = threadIdx.x;
-  int* const flag = reinterpret_cast<int*>(flag_lds);
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  block_barrier();
-  if (tid == 0) {
-    unsigned long long* const word = p.split_cnt + tile;
-    unsigned long long old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    unsigned long long want;
-    do {
-      want = (old >> 8) == p.split_tag ? old + 1 : (p.split_tag << 8) | 1ull;
-    } while (!__hip_atomic_compare_exchange_strong(word, &old, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT));
-    const int last = (int)(want & 0xFF) == ksplit;
-    if (last) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = last;
-  }
-  wait_lgkm();
-  block_barrier();
-  const int last = __builtin_amdgcn_readfirstlane(*flag);
-  wait_lgkm();
-  block_barrier();   // every wave has read the flag before any DMA may reuse its bytes
-  if (!last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  const int r0 = tm * BM, c0 = tn * BN;
-  const int rows = min(BM, p.m - r0), cols = min(BN, p.n - c0);
-  constexpr int Q = BN / 4;   // four columns per thread and row
-  const int32_t* const ws = p.split_ws;
-  const bool vec = (p.n & 3) == 0;
-#pragma unroll 2
-  for (int idx = tid; idx < BM * Q; idx += 256) {
-    const int r = idx / Q, cq = idx - r * Q;
-    if (r >= rows || 4 * cq >= cols) continue;
-    const int m = r0 + r, n = c0 + 4 * cq;
-    const int valid = min(4, p.n - n);
-    const int32_t* src = ws + (int64_t)m * p.n + n;
-    int c[4] = {0, 0, 0, 0};
-    if (valid == 4 && vec) {
-      int4 v[kMaxSplitFin];
-#pragma unroll
-      for (int sp = 0; sp < kMaxSplitFin; ++sp)
-        v[sp] = sp < ksplit ? *reinterpret_cast<const int4*>(src + sp * p.split_stride) : make_int4(0, 0, 0, 0);
-#pragma unroll
-      for (int sp = 0; sp < kMaxSplitFin; ++sp) {
-        c[0] += v[sp].x; c[1] += v[sp].y; c[2] += v[sp].z; c[3] += v[sp].w;
-      }
-    } else {
-      for (int sp = 0; sp < ksplit; ++sp)
-        for (int v = 0; v < valid; ++v) c[v] += src[sp * p.split_stride + v];
-    }
-    epilogue4<FE, FO>(p, m, n, valid, c, FE != kEpiInt32 ? p.row_scale[m] : 0.0f);
   }
 }
 
@@ -1203,18 +1123,7 @@ void gemm_i8_persistent(GemmParams p) {
     const int64_t out_off = (item % ksplit) * p.split_stride;
     // Interior quadrants take a copy without store masks (not for the gate
     // variants, whose registers a second copy would push into spills).
-    if constexpr ((FLAGS & kSplitFin) != 0) {
-      // The item's int32 partial tile, at plane item % ksplit of split_ws.
-      GemmParams q = p;
-      q.out = p.split_ws;
-      q.ldc = p.n;
-      q.vec16 = (p.n & 3) == 0;
-      q.vec_out = q.vec16;
-      if (q.vec16 && mw + 128 <= p.m && nw + WN <= p.n)
-        store_quadrant32_passes<EPI, OUT, 0, true, NB>(q, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
-      else
-        store_quadrant32_passes<EPI, OUT, 0, false, NB>(q, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
-    } else if constexpr ((FLAGS & kWithRope) != 0) {
+    if constexpr ((FLAGS & kWithRope) != 0) {
       if (nw >= 2 * p.rope_heads * 128) {   // V columns
         if (p.vec16 && mw + 128 <= p.m && nw + 128 <= p.n)
           store_quadrant32_passes<EPI, OUT, 0, true>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w, out_off);
@@ -1238,7 +1147,6 @@ void gemm_i8_persistent(GemmParams p) {
     // stage; a wave's DMA into a slot writes the same 8 KB it used for
     // staging, so its own staging reads returning is all that unit waits for.
     wait_lgkm();
-    if constexpr ((FLAGS & kSplitFin) != 0) split_finish<FLAGS, BM, BN>(p, item / ksplit, tm, tn, ksplit, smem + stg * kSTile);
     // The next tile's first fragments (its stage 0 landed before the last
     // barrier, in the slots cur_a and the one after).
     static_for<0, NB - 1>([&](auto k) { read_group(cur_a, next_slot(cur_a), 0, decltype(k)::value, fa0, fb0); });
@@ -1679,13 +1587,6 @@ inline int current_device(int& dev) {
   return W8A8_OK;
 }
 
-// A fresh tag for a split-K launch's arrival words: 1, 2, ... below 2^56
-// (0 marks a cleared word).
-inline unsigned long long next_split_tag() {
-  static std::atomic<unsigned long long> tags{0};
-  return ((tags.fetch_add(1, std::memory_order_relaxed)) % ((1ull << 56) - 1)) + 1;
-}
-
 template <int EPI, int OUT, int FLAGS, int NB>
 int launch_persistent(const GemmParams& p, int64_t tiles, int dev, hipStream_t s) {
   // The LDS ring and staging area exceed the 64 KB default: raise the
@@ -1786,22 +1687,9 @@ int launch_gemm(const GemmParams& p, hipStream_t s) {
   // Tile width and K split (the RoPE epilogue takes neither: one head per
   // 128-column quadrant, whole K).
   GemmPlan plan = p.rope_heads ? GemmPlan{4, 1} : gemm_plan(p.m, p.n, p.k, device_cus(dev));
-  const int64_t ws_need = plan.ksplit > 1 ? split_partials_bytes(p.m, p.n, plan.ksplit) : 0;
+  const int64_t ws_need = split_partials_bytes(p.m, p.n, plan.ksplit);
   if (plan.ksplit > 1 && (p.ws == nullptr || p.ws_bytes < ws_need)) plan = gemm_plan(p.m, p.n, p.k, device_cus(dev), 1);
   const int ksplit = plan.ksplit;
-  if (ksplit > 1 && p.ws_bytes >= plan_workspace_bytes(p.m, p.n, plan)) {
-    // One launch: the last work item of each tile adds the partials and
-    // runs the epilogue (a workspace sized for the partials alone takes the
-    // separate finish below).
-    GemmParams q = p;
-    q.ksplit = ksplit;
-    q.split_stride = (int64_t)p.m * p.n;
-    q.split_ws = reinterpret_cast<int32_t*>(p.ws);
-    q.split_cnt = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(p.ws) +
-                                                        split_counters_offset(p.m, p.n, ksplit));
-    q.split_tag = next_split_tag();
-    return launch_persistent_nb<kEpiInt32, kI32, split_fin_flags(EPI, OUT)>(q, plan, dev, s);
-  }
   if (ksplit > 1) {
     GemmParams q = p;
     q.out = p.ws;

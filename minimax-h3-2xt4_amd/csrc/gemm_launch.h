@@ -47,24 +47,12 @@ struct GemmParams {
   // Caller's split-K workspace (may be null).
   void* ws;
   int64_t ws_bytes;
-  // Split K finished inside the persistent kernel (kSplitFin): the work
-  // items write their int32 partial tiles at split_ws (plane s at s *
-  // split_stride, rows of n), and the last of a tile's ksplit items to arrive
-  // adds the planes and runs the call's own epilogue. split_cnt holds one
-  // 64-bit word per output tile: (call tag << 8) | arrivals. A call's tag is
-  // fresh (below 2^56), so whatever the words hold from before - including
-  // never-initialized memory - the first arrival of each tile replaces it.
-  int32_t* split_ws;
-  unsigned long long* split_cnt;
-  unsigned long long split_tag;
 };
 
-// Workspace of a split-K GEMM finished in the kernel: the int32 partial
-// planes (ksplit x m x n), then, 256-byte aligned, one 8-byte arrival word
-// per output tile.
-inline int64_t split_partials_bytes(int64_t m, int64_t n, int ksplit) { return (int64_t)ksplit * m * n * 4; }
-inline int64_t split_counters_offset(int64_t m, int64_t n, int ksplit) {
-  return (split_partials_bytes(m, n, ksplit) + 255) & ~(int64_t)255;
+// Workspace of a split-K GEMM: the int32 partial planes (ksplit x m x n),
+// which the finishing kernel adds (0 without a split).
+inline int64_t split_partials_bytes(int64_t m, int64_t n, int ksplit) {
+  return ksplit > 1 ? (int64_t)ksplit * m * n * 4 : 0;
 }
 
 // EPI: kEpiInt32 / kEpiRow / kEpiColumn; OUT: kI32 / kF16 / kBF16 / kF32.
@@ -88,13 +76,6 @@ struct GemmPlan {
 inline int64_t plan_tiles(int64_t m, int64_t n, const GemmPlan& plan) {
   const int64_t bm = plan.nb == 2 ? 128 : 256, bn = plan.nb == 2 ? 256 : 64 * plan.nb;
   return ((m + bm - 1) / bm) * ((n + bn - 1) / bn);
-}
-
-// Workspace bytes of a persistent-kernel plan that splits K: the partial
-// planes and the tiles' arrival words (0 without a split).
-inline int64_t plan_workspace_bytes(int64_t m, int64_t n, const GemmPlan& plan) {
-  if (plan.ksplit <= 1) return 0;
-  return split_counters_offset(m, n, plan.ksplit) + 8 * plan_tiles(m, n, plan);
 }
 
 // The plan of least modelled time for an m x n x k GEMM (k a multiple of

@@ -369,9 +369,9 @@ def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
     if epi == 'int32':
         got = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32)
         assert_bits_equal(np_of(got), acc, 'split-K int32')
-        two_kernel = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32,
-                                  workspace=torch.empty(need - 8, dtype=torch.uint8, device=gpu))
-        assert_bits_equal(np_of(two_kernel), acc, 'split-K int32 finished by the second kernel')
+        short = kernels.gemm(a.to(gpu), b.to(gpu), epilogue=kernels.EPI_INT32,
+                             workspace=torch.empty(need - 16, dtype=torch.uint8, device=gpu))
+        assert_bits_equal(np_of(short), acc, 'int32 with a workspace too small to split')
         return
     rs = torch.rand((m, 1), generator=g) * 0.05 + 1e-4
     ws = torch.rand((n, 1), generator=g) * 1e-3 + 1e-6
@@ -382,11 +382,9 @@ def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
               bias=None if bias is None else bias.to(gpu), residual=None if res is None else res.to(gpu))
     got = kernels.gemm(a.to(gpu), b.to(gpu), **kw)
     unsplit = kernels.gemm(a.to(gpu), b.to(gpu), workspace=torch.empty(0, dtype=torch.uint8, device=gpu), **kw)
-    # A workspace one word short of the tiles' arrival words still holds the
-    # partials: the split then finishes in a second kernel.
-    two_kernel = kernels.gemm(a.to(gpu), b.to(gpu), workspace=torch.empty(need - 8, dtype=torch.uint8, device=gpu),
-                              **kw)
-    assert_bits_equal(np_of(two_kernel), np_of(got), 'split-K finished by the second kernel')
+    # A workspace 16 bytes short of the partials: the GEMM runs unsplit.
+    short = kernels.gemm(a.to(gpu), b.to(gpu), workspace=torch.empty(need - 16, dtype=torch.uint8, device=gpu), **kw)
+    assert_bits_equal(np_of(short), np_of(got), 'a workspace too small to split')
     fn = o.dequantize_row if epi == 'row' else o.dequantize_column
     want = fn(acc, np_of(rs).reshape(-1), np_of(ws).reshape(-1), tname(out_dtype),
               None if bias is None else np_of(bias))
@@ -398,8 +396,8 @@ def test_gemm_split_k(gpu, m, n, k, epi, out_dtype, bias_dtype, residual):
 
 def test_gemm_split_k_gated_residual_and_reused_workspace(gpu):
     # The DiT gate in the split-K finish; the same workspace serves three
-    # calls in a row (its arrival words hold the previous call's state, its
-    # first call's were never written).
+    # calls in a row (filled with 0xA5 first: the splits write every partial
+    # before the finish reads it).
     m, n, k = 300, 520, 2048
     assert kernels.gemm_workspace_bytes(m, n, k, gpu) > 0
     g = torch.Generator().manual_seed(19)

@@ -1,9 +1,8 @@
 """The no-allocation GEMM entry point (w8a8_gemm_noalloc) through the C ABI.
 
-Its split-K partials and tile arrival words live in the library's file-scope
-device scratch array instead of a caller workspace. Two calls in a row (the
-second smaller, so stale partials and arrival words of the first remain in
-the array) must equal w8a8_gemm with a torch-allocated workspace bit for
+Its split-K partials live in the library's file-scope device scratch array
+instead of a caller workspace. Two calls in a row (the second smaller, so
+stale partials of the first remain in the array) must equal w8a8_gemm with a torch-allocated workspace bit for
 bit, and the oracle. A shape whose split would need more scratch than the
 array holds runs unsplit, with the same result; a caller workspace is
 refused. A split call captured in a HIP graph replays bit-identically, with
