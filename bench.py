@@ -688,6 +688,12 @@ def run_te_skinny(args, torch, dev):
                         weight_gbs=round(n * k / (tg * 1e-3) / 1e9, 1),
                         gemm_frac=round(gemm_bytes / (tg * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
                         gemm_tops=round(2.0 * m * n * k / (tg * 1e-3) / 1e12, 1))
+            if m >= 256:
+                # The vendor library on the same operands (torch._int_mm, int32 out, no dequantization).
+                qv = qx if name == 'up' else qd
+                wv = (wu if name == 'up' else wd).t()
+                line['hipblaslt_int32_us'] = round(graph_timed(torch, lambda: torch._int_mm(qv, wv), args.steps,
+                                                               args.warmup) * 1e3, 2)
             if not args.no_cpu_baseline:
                 # The same projection in the reference's torch CPU ops.
                 torch.set_num_threads(cpu_threads())
@@ -1193,7 +1199,8 @@ def _compact(name, res):
     """The figures of one config's result worth carrying on the default line."""
     keep = {k: res[k] for k in ('metric', 'value', 'unit', 'us', 'ms', 'kernels', 'cpu_baseline') if k in res}
     if name == 'te_skinny':
-        keep['lines'] = [{k: l[k] for k in ('m', 'proj', 'gemm_us', 'gemm_frac', 'cpu_us') if k in l}
+        keep['lines'] = [{k: l[k] for k in ('m', 'proj', 'gemm_us', 'gemm_frac', 'hipblaslt_int32_us', 'cpu_us')
+                          if k in l}
                          for l in res['lines']]
     return keep
 
