@@ -35,9 +35,12 @@ struct NormParams {
 };
 
 // MODE: 0 norm only, 1 quantize, 2 ConvRot256 (fp32) + quantize,
-// 3 ConvRot256 rounded to the storage dtype + quantize.
+// 3 ConvRot256 rounded to the storage dtype + quantize; 2 or 3 | kNormSigned
+// (4): the rotation takes the sign words (diag(s) then H), a compile-time
+// choice so that the kernels without signs hold no registers for them.
+constexpr int kNormSigned = 4;
 template <int MODE>
-constexpr int rot_of() { return MODE == 2 ? 1 : MODE == 3 ? 2 : 0; }
+constexpr int rot_of() { return (MODE & 3) == 2 ? 1 : (MODE & 3) == 3 ? 2 : 0; }
 
 __device__ __forceinline__ void load16_f32(const float* p, float (&v)[16]) {
   const float4* q = reinterpret_cast<const float4*>(p);
@@ -155,7 +158,8 @@ __global__ __launch_bounds__(64 * W) void norm_quant_kernel(NormParams p) {
       dst[1] = make_uint4(bits[4], bits[5], bits[6], bits[7]);
     }
     if constexpr (ROT != 0) {
-      convrot256_lanes<true>(v, buf, t, p.signs ? p.signs + 256 * (u >> 4) : nullptr);
+      constexpr bool SG = (MODE & kNormSigned) != 0;
+      convrot256_lanes<true, SG>(v, buf, t, SG ? p.signs + 256 * (u >> 4) : nullptr);
       if constexpr (ROT == 2) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = round_to<DT>(v[i]);
@@ -359,19 +363,24 @@ extern "C" int w8a8_norm_quantize(const W8A8NormArgs* a) {
                "w8a8_norm_quantize: convrot_signs needs q, convrot and a 16-byte aligned array");
   p.signs = a->convrot_signs;
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
-  const int mode = a->q == nullptr ? 0 : a->convrot == 0 ? 1 : a->round_rotated ? 3 : 2;
+  const int mode = (a->q == nullptr ? 0 : a->convrot == 0 ? 1 : a->round_rotated ? 3 : 2) |
+                   (a->convrot_signs ? kNormSigned : 0);
   if (a->x_dtype == W8A8_F16) {
     switch (mode) {
       case 0: return launch_norm<kF16, 0>(p, stream);
       case 1: return launch_norm<kF16, 1>(p, stream);
       case 2: return launch_norm<kF16, 2>(p, stream);
-      default: return launch_norm<kF16, 3>(p, stream);
+      case 3: return launch_norm<kF16, 3>(p, stream);
+      case 6: return launch_norm<kF16, 6>(p, stream);
+      default: return launch_norm<kF16, 7>(p, stream);
     }
   }
   switch (mode) {
     case 0: return launch_norm<kBF16, 0>(p, stream);
     case 1: return launch_norm<kBF16, 1>(p, stream);
     case 2: return launch_norm<kBF16, 2>(p, stream);
-    default: return launch_norm<kBF16, 3>(p, stream);
+    case 3: return launch_norm<kBF16, 3>(p, stream);
+    case 6: return launch_norm<kBF16, 6>(p, stream);
+    default: return launch_norm<kBF16, 7>(p, stream);
   }
 }

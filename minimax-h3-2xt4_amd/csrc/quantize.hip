@@ -19,31 +19,36 @@ template <int DT>
 constexpr int dt_bytes() { return DT == kF32 ? 4 : 2; }
 
 // ROT: 0 no rotation, 1 ConvRot256 kept in FP32, 2 ConvRot256 rounded to
-// the input dtype. J > 0: the row (at most J units per lane) stays in
+// the input dtype; | kSigned (4): the rotation takes the sign words
+// (diag(s) then H). J > 0: the row (at most J units per lane) stays in
 // registers between the absmax and the quantization. J == 0: streaming, the
 // row is read twice.
+constexpr int kSigned = 4;
+
 template <int DT, int ROT, int J>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t cols,
     const float* __restrict__ row_max, int8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale, float* __restrict__ row_max_out, const uint32_t* __restrict__ signs) {
-  __shared__ float lds[ROT ? kQuantWaves * kRotWave : 1];
+  constexpr int RM = ROT & 3;
+  constexpr bool SG = (ROT & kSigned) != 0;
+  __shared__ float lds[RM ? kQuantWaves * kRotWave : 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kQuantWaves + wave;
   if (row >= rows) return;
   const int units = (int)(cols >> 4);
   const int jcount = (units + 63) >> 6;
   const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * dt_bytes<DT>();
-  float* buf = ROT ? rot_slot(lds, wave, lane) : nullptr;
+  float* buf = RM ? rot_slot(lds, wave, lane) : nullptr;
   const int t = lane & 15;
 
   // The sign words of unit u's 256-column group (ConvRot with signs).
-  auto smask = [&](int u) { return signs ? signs + 256 * (u >> 4) : nullptr; };
+  auto smask = [&](int u) { return SG ? signs + 256 * (u >> 4) : nullptr; };
   auto load_unit = [&](int u, float (&v)[16]) {
     load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v);
-    if constexpr (ROT != 0) {
-      convrot256_lanes<true>(v, buf, t, smask(u));
-      if constexpr (ROT == 2) {
+    if constexpr (RM != 0) {
+      convrot256_lanes<true, SG>(v, buf, t, smask(u));
+      if constexpr (RM == 2) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = round_to<DT>(v[i]);
       }
@@ -73,7 +78,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     // and the maximum is taken on the fp32 rotation and rounded once:
     // rounding is monotonic and odd, so that is the maximum of the rounded
     // magnitudes (fmaxf skips NaN either way).
-    constexpr bool KEEP16 = ROT == 2 && DT == kF16;
+    constexpr bool KEEP16 = RM == 2 && DT == kF16;
     float v[KEEP16 ? 1 : J][16];
     uint32_t h16[KEEP16 ? J : 1][8];
     float amax = 0.0f;
@@ -81,9 +86,9 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     for (int j = 0; j < J; ++j) {
       float (&vj)[16] = v[KEEP16 ? 0 : j];
       unpack16<DT>(raw[j], vj);
-      if constexpr (ROT != 0) {
-        convrot256_lanes<true>(vj, buf, t, smask(min(lane + 64 * j, units - 1)));
-        if constexpr (ROT == 2 && !KEEP16) {
+      if constexpr (RM != 0) {
+        convrot256_lanes<true, SG>(vj, buf, t, smask(min(lane + 64 * j, units - 1)));
+        if constexpr (RM == 2 && !KEEP16) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) vj[i] = round_to<DT>(vj[i]);
         }
@@ -159,21 +164,23 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
 // row is spread over W wavefronts instead of one: W = 16 for up to one row
 // per CU (four waves per SIMD), W = 4 beyond.
 template <int ROT, int W>
-constexpr int row_wg_lds_bytes() { return ((ROT ? W * kRotWave : 0) + W) * 4; }
+constexpr int row_wg_lds_bytes() { return (((ROT & 3) ? W * kRotWave : 0) + W) * 4; }
 
 template <int DT, int ROT, int J, int W>
 __global__ __launch_bounds__(64 * W) void quantize_row_wg_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t cols, const float* __restrict__ row_max,
     int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, float* __restrict__ row_max_out,
     const uint32_t* __restrict__ signs) {
+  constexpr int RM = ROT & 3;
+  constexpr bool SG = (ROT & kSigned) != 0;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* const lds = smem;
-  float* const wmax = smem + (ROT ? W * kRotWave : 0);
+  float* const wmax = smem + (RM ? W * kRotWave : 0);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t row = blockIdx.x;
   const int units = (int)(cols >> 4);
   const char* xrow = reinterpret_cast<const char*>(x) + row * ldx * dt_bytes<DT>();
-  float* buf = ROT ? rot_slot(lds, wave, lane) : nullptr;
+  float* buf = RM ? rot_slot(lds, wave, lane) : nullptr;
   const int t = lane & 15;
   float v[J][16];
   float amax = 0.0f;
@@ -182,9 +189,9 @@ __global__ __launch_bounds__(64 * W) void quantize_row_wg_kernel(
     const int u = tid + 64 * W * j;
     if (u < units) {
       load16<DT>(xrow + (int64_t)u * 16 * dt_bytes<DT>(), v[j]);
-      if constexpr (ROT != 0) {
-        convrot256_lanes<true>(v[j], buf, t, signs ? signs + 256 * (u >> 4) : nullptr);
-        if constexpr (ROT == 2) {
+      if constexpr (RM != 0) {
+        convrot256_lanes<true, SG>(v[j], buf, t, SG ? signs + 256 * (u >> 4) : nullptr);
+        if constexpr (RM == 2) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) v[j][i] = round_to<DT>(v[j][i]);
         }
@@ -317,15 +324,21 @@ extern "C" int w8a8_quantize_rows(const W8A8QuantArgs* a) {
                "w8a8_quantize_rows: convrot_signs needs convrot and a 16-byte aligned array");
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
   W8A8_REQUIRE(a->round_rotated == 0 || a->round_rotated == 1, "w8a8_quantize_rows: round_rotated must be 0 or 1");
-  const int mode = a->convrot == 0 ? 0 : (a->round_rotated && a->x_dtype != W8A8_F32) ? 2 : 1;
-  switch (a->x_dtype * 4 + mode) {
-    case W8A8_F16 * 4 + 0: return launch_quantize<kF16, 0>(a, stream);
-    case W8A8_F16 * 4 + 1: return launch_quantize<kF16, 1>(a, stream);
-    case W8A8_F16 * 4 + 2: return launch_quantize<kF16, 2>(a, stream);
-    case W8A8_BF16 * 4 + 0: return launch_quantize<kBF16, 0>(a, stream);
-    case W8A8_BF16 * 4 + 1: return launch_quantize<kBF16, 1>(a, stream);
-    case W8A8_BF16 * 4 + 2: return launch_quantize<kBF16, 2>(a, stream);
-    case W8A8_F32 * 4 + 0: return launch_quantize<kF32, 0>(a, stream);
+  const int mode = (a->convrot == 0 ? 0 : (a->round_rotated && a->x_dtype != W8A8_F32) ? 2 : 1) |
+                   (a->convrot_signs ? kSigned : 0);
+  switch (a->x_dtype * 8 + mode) {
+    case W8A8_F16 * 8 + 0: return launch_quantize<kF16, 0>(a, stream);
+    case W8A8_F16 * 8 + 1: return launch_quantize<kF16, 1>(a, stream);
+    case W8A8_F16 * 8 + 2: return launch_quantize<kF16, 2>(a, stream);
+    case W8A8_F16 * 8 + 5: return launch_quantize<kF16, 5>(a, stream);
+    case W8A8_F16 * 8 + 6: return launch_quantize<kF16, 6>(a, stream);
+    case W8A8_BF16 * 8 + 0: return launch_quantize<kBF16, 0>(a, stream);
+    case W8A8_BF16 * 8 + 1: return launch_quantize<kBF16, 1>(a, stream);
+    case W8A8_BF16 * 8 + 2: return launch_quantize<kBF16, 2>(a, stream);
+    case W8A8_BF16 * 8 + 5: return launch_quantize<kBF16, 5>(a, stream);
+    case W8A8_BF16 * 8 + 6: return launch_quantize<kBF16, 6>(a, stream);
+    case W8A8_F32 * 8 + 0: return launch_quantize<kF32, 0>(a, stream);
+    case W8A8_F32 * 8 + 5: return launch_quantize<kF32, 5>(a, stream);
     default: return launch_quantize<kF32, 1>(a, stream);
   }
 }

@@ -30,7 +30,7 @@ constexpr int swiglu_lds_bytes() { return (W * kRotWave + W) * 4; }
 // P > 0: the row's rotated values stay in registers (P passes of 4 W
 // groups). P == 0: streaming, the row is transformed twice (maximum, then
 // quantize).
-template <int DT, int P, int W>
+template <int DT, int P, int W, bool SG>
 __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t width,
     const float* __restrict__ row_max_in, float* __restrict__ row_max_out,
@@ -55,7 +55,7 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
     load16<DT>(xrow + (width + (int64_t)g * 256 + 16 * t) * sw_bytes<DT>(), uv);
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = DT == kF16 ? swiglu_fp16_gate(gv[i], uv[i]) : swiglu(gv[i], uv[i]);
-    convrot256_lanes<true>(v, buf, t, signs ? signs + 256 * g : nullptr);
+    convrot256_lanes<true, SG>(v, buf, t, SG ? signs + 256 * g : nullptr);
   };
   auto group_absmax = [&](int g, const float (&v)[16]) {
     float m = 0.0f;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i)
         v[p][i] = DT == kF16 ? swiglu_fp16_gate(gv[i], uv[i]) : swiglu(gv[i], uv[i]);
-      convrot256_lanes<true>(v[p], buf, t, signs ? signs + 256 * min(g, groups - 1) : nullptr);
+      convrot256_lanes<true, SG>(v[p], buf, t, SG ? signs + 256 * min(g, groups - 1) : nullptr);
       float m = 0.0f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) m = fmaxf(m, fabsf(v[p][j]));
@@ -149,13 +149,13 @@ __global__ __launch_bounds__(64 * W) void swiglu_quant_kernel(
   }
 }
 
-template <int DT, int W>
+template <int DT, int W, bool SG>
 static void launch_swiglu_w(const W8A8SwigluArgs* a, hipStream_t stream) {
   const int groups = (int)(a->width >> 8);
   const int passes = (groups + 4 * W - 1) / (4 * W);
   const dim3 grid((unsigned)a->rows), block(64 * W);
 #define W8A8_SLAUNCH(PP)                                                                                 \
-  hipLaunchKernelGGL((swiglu_quant_kernel<DT, PP, W>), grid, block, swiglu_lds_bytes<W>(), stream, a->x, \
+  hipLaunchKernelGGL((swiglu_quant_kernel<DT, PP, W, SG>), grid, block, swiglu_lds_bytes<W>(), stream, a->x, \
                      a->ldx, a->rows, a->width, a->row_max, a->row_max_out, a->group_max, a->q, a->ldq,  \
                      a->scale, a->convrot_signs)
   switch (passes) {
@@ -171,16 +171,16 @@ static void launch_swiglu_w(const W8A8SwigluArgs* a, hipStream_t stream) {
 
 // The 16-wave variants' LDS exceeds the 64 KB default: raise their limit once
 // per device.
-template <int DT>
+template <int DT, bool SG>
 static int enable_wide_swiglu(int dev) {
   static std::atomic<uint64_t> done{0};
   const uint64_t bit = 1ull << dev;
   if (done.load(std::memory_order_acquire) & bit) return W8A8_OK;
-  const void* fns[] = {reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 0, 16>),
-                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 1, 16>),
-                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 2, 16>),
-                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 3, 16>),
-                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 4, 16>)};
+  const void* fns[] = {reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 0, 16, SG>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 1, 16, SG>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 2, 16, SG>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 3, 16, SG>),
+                       reinterpret_cast<const void*>(&swiglu_quant_kernel<DT, 4, 16, SG>)};
   for (const void* f : fns) {
     const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, swiglu_lds_bytes<16>());
     if (e != hipSuccess) {
@@ -193,7 +193,7 @@ static int enable_wide_swiglu(int dev) {
   return W8A8_OK;
 }
 
-template <int DT>
+template <int DT, bool SG>
 static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
@@ -201,11 +201,11 @@ static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
     return W8A8_ERR_LAUNCH;
   }
   if (a->rows <= (int64_t)device_cus(dev)) {
-    const int rc = enable_wide_swiglu<DT>(dev);
+    const int rc = enable_wide_swiglu<DT, SG>(dev);
     if (rc != W8A8_OK) return rc;
-    launch_swiglu_w<DT, 16>(a, stream);
+    launch_swiglu_w<DT, 16, SG>(a, stream);
   } else {
-    launch_swiglu_w<DT, 4>(a, stream);
+    launch_swiglu_w<DT, 4, SG>(a, stream);
   }
   return launch_status("w8a8_swiglu_quantize");
 }
@@ -238,5 +238,9 @@ extern "C" int w8a8_swiglu_quantize(const W8A8SwigluArgs* a) {
   W8A8_REQUIRE(a->convrot_signs == nullptr || aligned16(a->convrot_signs),
                "w8a8_swiglu_quantize: convrot_signs must be 16-byte aligned");
   hipStream_t stream = reinterpret_cast<hipStream_t>(a->stream);
-  return a->x_dtype == W8A8_F16 ? launch_swiglu<kF16>(a, stream) : launch_swiglu<kF32>(a, stream);
+  // The sign words select their own kernels (compile-time), so the kernels
+  // without them hold no registers for the sign path.
+  if (a->convrot_signs)
+    return a->x_dtype == W8A8_F16 ? launch_swiglu<kF16, true>(a, stream) : launch_swiglu<kF32, true>(a, stream);
+  return a->x_dtype == W8A8_F16 ? launch_swiglu<kF16, false>(a, stream) : launch_swiglu<kF32, false>(a, stream);
 }

@@ -277,13 +277,14 @@ __device__ __forceinline__ float* rot_slot(float* lds, int wave, int lane) {
 // slot (rot_slot). On return, if NATURAL, v again holds elements
 // 16t..16t+15; otherwise v[j] holds element 16j + t. The 1/16 factor is
 // applied last, as in the reference butterfly.
-// smask (optional, wave-uniformly null or not): the group's 256 sign words,
-// 0 or 0x80000000 per element, XORed into the values first: the rotation
-// diag(s) then H, with s a +-1 vector (exact: only signs change).
-template <bool NATURAL>
+// SIGNS: smask holds the group's 256 sign words, 0 or 0x80000000 per
+// element, XORed into the values first: the rotation diag(s) then H, with s
+// a +-1 vector (exact: only signs change). A compile-time choice, so kernels
+// without signs hold no registers for them.
+template <bool NATURAL, bool SIGNS = false>
 __device__ __forceinline__ void convrot256_lanes(float (&v)[16], float* buf, int t,
                                                  const uint32_t* smask = nullptr) {
-  if (smask != nullptr) {
+  if constexpr (SIGNS) {
     const uint4* m = reinterpret_cast<const uint4*>(smask + 16 * t);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
