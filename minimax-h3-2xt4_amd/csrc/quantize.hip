@@ -18,13 +18,13 @@ constexpr int kQuantMaxJ = 8;  // units per lane kept in registers
 template <int DT>
 constexpr int dt_bytes() { return DT == kF32 ? 4 : 2; }
 
-// ROT: 0 no rotation, 1 ConvRot256 kept in FP32, 2 ConvRot256 rounded to
-// the input dtype; | kSigned (4): the rotation takes the sign words
-// (diag(s) then H). J > 0: the row (at most J units per lane) stays in
-// registers between the absmax and the quantization. J == 0: streaming, the
-// row is read twice.
+// The ROT bit of a rotation that takes the sign words (diag(s) then H).
 constexpr int kSigned = 4;
 
+// ROT: 0 no rotation, 1 ConvRot256 kept in FP32, 2 ConvRot256 rounded to
+// the input dtype, each rotation | kSigned with signs. J > 0: the row (at
+// most J units per lane) stays in registers between the absmax and the
+// quantization. J == 0: streaming, the row is read twice.
 template <int DT, int ROT, int J>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const void* __restrict__ x, int64_t ldx, int64_t rows, int64_t cols,
