@@ -1,8 +1,8 @@
 """GPU INT8 attention on the reference kernel's scheme (128-key blocks): the
 preparation bit for bit against the oracle's restatement (kitchen_prepare),
-the attention within a tolerance of kitchen_attention (the GPU uses the
-hardware exp2; the restatement exact exp2) and close to exact softmax
-attention."""
+the attention within 1e-5 of kitchen_attention (the same u8 codes; the GPU
+uses the hardware exp2 and its own FP32 summation order, measured below 1e-6
+at 130 to 53504 keys) and close to exact softmax attention."""
 import numpy as np
 import pytest
 import torch
@@ -80,8 +80,9 @@ def test_attention_matches_oracle(gpu, b, h, nq, nk, dtype):
     want = oa.kitchen_attention(oprep).astype(np.float64)
     exact = oa.reference_attention(_np(q), _np(k), _np(v))
     # Tile-relative u8 probabilities keep their accuracy on long rows; the
-    # GPU-vs-oracle bound (hardware exp2) is the same at every length.
-    rel = _check(out, want, exact, 2e-3, min_cos=0.9995)
+    # GPU-vs-oracle bound (hardware exp2, FP32 order) is the same at every
+    # length.
+    rel = _check(out, want, exact, 1e-5, min_cos=0.9995)
     print(f'b={b} h={h} nq={nq} nk={nk}: max |gpu - oracle| / max |oracle| = {rel:.2e}')
     out16 = kernels.attention(prep, out_dtype=torch.float16)
     assert torch.equal(out16, out.half())
@@ -103,6 +104,7 @@ def test_error_vs_exact_no_worse_than_restatement(gpu, nk):
     err_oracle = np.abs(want - exact).max() / scale
     print(f'nk={nk}: max error / max |exact|: kernel {err_gpu:.4e}, restatement {err_oracle:.4e}')
     assert err_gpu <= 1.02 * err_oracle + 1e-5, (err_gpu, err_oracle)
+    assert np.abs(out - want).max() <= 1e-5 * np.abs(want).max()
 
 
 def test_large_logits_and_uniform_keys(gpu):
