@@ -81,5 +81,8 @@ def test_kernels_reproduce_golden_fixtures_of_the_dit_rows(gpu):
     for name in ('q8', 'qs', 'k8', 'ks', 'vt8', 'vs', 'vsum'):
         assert_bits_equal(np_of(prep[name]), d[name], f'golden attention {name}')
     out = np_of(kernels.attention(prep, out_dtype=torch.float32)).astype(np.float64)
-    # the GPU takes the hardware exp2: within 2e-3 of the oracle's output
-    assert np.abs(out - d['out']).max() <= 2e-3 * np.abs(d['out']).max()
+    # the GPU takes the hardware exp2 and its own FP32 order: within 1e-5 of
+    # the oracle's output (the same u8 codes)
+    err = np.abs(out - d['out']).max() / np.abs(d['out']).max()
+    print(f'attention fixture: max |gpu - oracle| / max |oracle| = {err:.2e}')
+    assert err <= 1e-5

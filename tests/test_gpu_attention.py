@@ -117,7 +117,7 @@ def test_large_logits_and_uniform_keys(gpu):
     exact = oa.reference_attention(_np(q), _np(k), _np(v))
     # A near one-hot softmax magnifies the Q/K quantization error: the scheme
     # itself is looser here, the kernel still follows the oracle closely.
-    _check(out, want, exact, 2e-3, min_cos=0.95)
+    print(f'sharp softmax: max |gpu - oracle| / max |oracle| = {_check(out, want, exact, 1e-5, min_cos=0.95):.2e}')
     # identical keys (a partial last block: the floor scale keeps its padded
     # keys masked): every query averages the quantized values
     ku = torch.ones((1, 1, 250, 128)) * torch.randn((1, 1, 1, 128), generator=g)
@@ -147,7 +147,8 @@ def test_reference_api(gpu):
     scaled = int8_attention.int8_attention(q, k, v, scale=0.05)
     want = oa.kitchen_attention(oa.kitchen_prepare(_np(q.cpu()), _np(k.cpu()), _np(v.cpu()), cta_k=oa.GPU_CTA_K,
                                                    sm_scale=0.05))
-    assert np.abs(np_of(scaled).astype(np.float64) - want).max() <= 2e-3 * np.abs(want).max() + 1e-3
+    # fp16 output: within one fp16 rounding of the restatement
+    assert np.abs(np_of(scaled).astype(np.float64) - want).max() <= 2 ** -10 * np.abs(want).max()
 
 
 @pytest.mark.parametrize('b,h,n,dtype', [(1, 3, 150, torch.float16), (2, 2, 70, torch.float32)])

@@ -78,7 +78,8 @@ def test_dit_attention_sublayer(gpu, rows, hidden, heads, rot):
     attn = block.attention(q, k, v)
     want_attn = oa.kitchen_attention(oprep)[0].transpose(1, 0, 2).reshape(rows, inner)
     err = np.abs(np_of(attn).astype(np.float64) - want_attn).max()
-    assert err <= 2e-3 * np.abs(want_attn).max(), err
+    print(f'attention rows: max |gpu - oracle| / max |oracle| = {err / np.abs(want_attn).max():.2e}')
+    assert err <= 2 ** -10 * np.abs(want_attn).max(), err   # fp16 rows: one rounding of the restatement
     # stage 4: the gated O projection of the GPU's attention rows, bit for bit,
     # and the sublayer output
     want = o.row_linear(np_of(attn), wo, so, residual=np_of(x), gate=np_of(gate), labels=labels)
