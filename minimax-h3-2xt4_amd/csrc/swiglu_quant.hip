@@ -5,11 +5,12 @@
 // [16t, 16t + 16) of the group with 128-bit loads). The rotated FP32 values
 // stay in registers until the row maximum is known, so the only HBM traffic
 // is the FP16 gate|up row in and the int8 row out (plus the fp32 scale).
-// Many rows take W = 4 (timed on one box: at width 8192 two passes of 4-wave
-// workgroups run 220 us against 262 us for one pass of 8-wave workgroups);
-// up to one row per CU takes W = 16, so a lane transforms a quarter of the
-// groups with four waves per SIMD issuing (one row of width 14336: 13.0 ->
-// 8.6 us; at two rows per CU the 16-wave workgroups no longer gain).
+// Many rows take the fewest waves (1, 2, 4 or 8) that leave each wave at
+// most three passes (the launcher lists the timings behind the rule; at
+// width 8192 that is W = 4, two passes); up to one row per CU takes W = 16,
+// so a lane transforms a quarter of the groups with four waves per SIMD
+// issuing (one row of width 14336: 13.0 -> 8.6 us; at two rows per CU the
+// 16-wave workgroups no longer gain).
 #include <atomic>
 
 #include "w8a8_device.h"
@@ -17,7 +18,7 @@
 
 namespace w8a8 {
 
-constexpr int kSwigluMaxPasses = 4;  // register-resident up to width 16384 (W = 4)
+constexpr int kSwigluMaxPasses = 4;  // register-resident up to 16 W groups per row
 
 template <int DT>
 constexpr int sw_bytes() { return DT == kF32 ? 4 : 2; }
@@ -200,12 +201,25 @@ static int launch_swiglu(const W8A8SwigluArgs* a, hipStream_t stream) {
     set_error("w8a8_swiglu_quantize: hipGetDevice failed");
     return W8A8_ERR_LAUNCH;
   }
-  if (a->rows <= (int64_t)device_cus(dev)) {
+  // Waves per row: 16 while the rows fit the CUs one each; otherwise the
+  // fewest (a power of two) that leave each wave at most three passes of
+  // its 4 groups. Timed on one box at 16384 rows (W = 1 / 2 / 4 / 8):
+  // width 2048 41 / 56 / 88 / 156 us, 4096 87 / 78 / 116 / 187, 6144
+  // 248 / 141 / 159 / 227, 8192 341 / 197 / 187 / 262, 16384
+  // 664 / 631 / 402 / 391, 20480 824 / 790 / 770 / 558 (bit-identical).
+  const int64_t groups = a->width >> 8;
+  if (a->rows <= (int64_t)device_cus(dev) || groups > 4 * 8 * 3) {
     const int rc = enable_wide_swiglu<DT, SG>(dev);
     if (rc != W8A8_OK) return rc;
     launch_swiglu_w<DT, 16, SG>(a, stream);
-  } else {
+  } else if (groups <= 4 * 1 * 3) {
+    launch_swiglu_w<DT, 1, SG>(a, stream);
+  } else if (groups <= 4 * 2 * 3) {
+    launch_swiglu_w<DT, 2, SG>(a, stream);
+  } else if (groups <= 4 * 4 * 3) {
     launch_swiglu_w<DT, 4, SG>(a, stream);
+  } else {
+    launch_swiglu_w<DT, 8, SG>(a, stream);
   }
   return launch_status("w8a8_swiglu_quantize");
 }

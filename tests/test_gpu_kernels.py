@@ -529,7 +529,11 @@ def test_quantize_ties_and_strided_rows(gpu):
 
 
 # ------------------------------------------------------------------ FC2 prologue
-SWIGLU_CASES = [(1, 256), (3, 512), (64, 3072), (5, 8192), (2, 12800), (2, 20480), (130, 4096)]
+SWIGLU_CASES = [(1, 256), (3, 512), (64, 3072), (5, 8192), (2, 12800), (2, 20480), (130, 4096),
+                # more rows than CUs: 1 wave per row (2048, 3072), 2 (4096, 6144), 4 (8192),
+                # 8 (12800, 20480) and, past 96 groups, 16 (24832)
+                (300, 2048), (270, 3072), (300, 4096), (300, 6144), (280, 8192), (300, 12800), (260, 20480),
+                (260, 24832)]
 
 
 @pytest.mark.parametrize('rows,width', SWIGLU_CASES)
