@@ -799,14 +799,21 @@ __device__ __forceinline__ void load_readout_scales(const GemmParams& p, int nw,
 // accumulators through the B slot of its last stage, whose next unit is
 // issued only during the next stage.
 //
+// 128 x 256 tiles (a 48 KB stage, whose A tile would fill half a slot) take
+// a ring of three whole stages instead: stage g computes from slot g mod 3
+// while stage g + 1 lands and stage g + 2 streams into the slot stage g - 1
+// released, so two stages are in flight.
+//
 // The waits count outstanding loads instead of draining them: before each
 // stage barrier vmcnt(NA) lgkmcnt(0) (the next stage landed; only the A unit
 // issued after it may still be in flight; this wave's fragment reads of the
 // stage returned), and before the epilogue vmcnt(NA + JB / 2) (the tile's
 // scale and bias loads, issued before its K loop, have landed; only the
-// next stage's A unit and half its B unit are younger): 8 / 12 for 256 x 256,
-// 8 / 11 for 256 x 192 and 4 / 8 for 128 x 256 tiles. Loads return in order,
-// so a count is exact whenever at least that many younger loads exist.
+// next stage's A unit and half its B unit are younger): 8 / 12 for 256 x 256
+// and 8 / 11 for 256 x 192 tiles. The three-stage ring waits vmcnt(NA +
+// 3 JB / 4) = 10 at the barrier (stage g + 2's instructions issued so far
+// are younger) and vmcnt(NA + JB) = 12 before the epilogue. Loads return in
+// order, so a count is exact whenever at least that many younger loads exist.
 //
 // LDS rows are 128 bytes: 16-byte chunk c of row r sits at physical chunk
 // c ^ ((r >> 1) & 7), which keeps both the DMA writes (lane i writes bytes
@@ -922,11 +929,11 @@ void gemm_i8_persistent(GemmParams p) {
     }
   };
   // DMA instruction J (0..NA - 1 of A, 0..JB - 1 of B) of this wave's part
-  // of the cursor stage's A or B tile into slot.
-  auto dma_one = [&](auto b_tag, auto j_tag, int slot) {
+  // of the cursor stage's A or B tile into the ring tile at byte offset base.
+  auto dma_one = [&](auto b_tag, auto j_tag, int base) {
     constexpr bool B = decltype(b_tag)::value;
     constexpr int J = decltype(j_tag)::value;
-    int8_t* st = smem + slot * kSTile + wave * (B ? JB : NA) * 1024 + J * 1024;
+    int8_t* st = smem + base + wave * (B ? JB : NA) * 1024 + J * 1024;
     const uint32_t kof = (uint32_t)(dma_ks * kSK);
     if constexpr (B) dma16(p.b + (off_b[J] + kof), st);
     else dma16(p.a + (off_a[J] + kof), st);
@@ -934,16 +941,16 @@ void gemm_i8_persistent(GemmParams p) {
   };
   // Part R (of NB, one per MFMA row) of half H of a unit: instructions
   // [C H + R C / NB, C H + (R + 1) C / NB) with C the half's length.
-  auto dma_part = [&](auto b_tag, auto h_tag, auto r_tag, int slot) {
+  auto dma_part = [&](auto b_tag, auto h_tag, auto r_tag, int base) {
     constexpr bool B = decltype(b_tag)::value;
     constexpr int H = decltype(h_tag)::value, R = decltype(r_tag)::value;
     constexpr int C = B ? JB / 2 : NA / 2;
-    static_for<C * H + R * C / NB, C * H + (R + 1) * C / NB>([&](auto j) { dma_one(b_tag, j, slot); });
+    static_for<C * H + R * C / NB, C * H + (R + 1) * C / NB>([&](auto j) { dma_one(b_tag, j, base); });
   };
-  auto issue_half = [&](auto b_tag, auto h_tag, int slot) {
+  auto issue_half = [&](auto b_tag, auto h_tag, int base) {
     constexpr bool B = decltype(b_tag)::value;
     constexpr int H = decltype(h_tag)::value, C = B ? JB / 2 : NA / 2;
-    static_for<C * H, C * H + C>([&](auto j) { dma_one(b_tag, j, slot); });
+    static_for<C * H, C * H + C>([&](auto j) { dma_one(b_tag, j, base); });
   };
   using A_ = std::false_type;
   using B_ = std::true_type;
@@ -957,9 +964,9 @@ void gemm_i8_persistent(GemmParams p) {
   const int wm = NB == 2 ? 0 : wave >> 1, wn = NB == 2 ? wave : wave & 1;
   const int fr = lane & 31, fh = lane >> 5;
   const int a_row = wm * 128 * kSK + fr * kSK, b_row = wn * WN * kSK + fr * kSK;
-  auto read_frags = [&](int slot_a, int slot_b, int u, v4i (&fa)[NB], v4i (&fb)[4]) {
-    const int8_t* sa = smem + slot_a * kSTile;
-    const int8_t* sb = smem + slot_b * kSTile;
+  auto read_frags = [&](int base_a, int base_b, int u, v4i (&fa)[NB], v4i (&fb)[4]) {
+    const int8_t* sa = smem + base_a;
+    const int8_t* sb = smem + base_b;
     const int off = lds_chunk(fr, 2 * u + fh) << 4;   // rows 32 i + fr share (row >> 1) & 7
 #pragma unroll
     for (int i = 0; i < NB; ++i) fa[i] = *reinterpret_cast<const v4i*>(sb + b_row + i * 32 * kSK + off);
@@ -972,10 +979,10 @@ void gemm_i8_persistent(GemmParams p) {
   // fb[3], fa[0..1], k = 2 fa[2..3]; NB = 3: k = 0 fb[0..3], k = 1
   // fa[0..2]; NB = 2: k = 0 all six. The last MFMA row of a sub-step issues
   // no reads, so the reads have landed when the next sub-step starts.
-  auto read_group = [&](int slot_a, int slot_b, int u, int k, v4i (&fa)[NB], v4i (&fb)[4]) {
+  auto read_group = [&](int base_a, int base_b, int u, int k, v4i (&fa)[NB], v4i (&fb)[4]) {
     const int off = lds_chunk(fr, 2 * u + fh) << 4;
-    const int8_t* sa = smem + slot_a * kSTile + a_row + off;
-    const int8_t* sb = smem + slot_b * kSTile + b_row + off;
+    const int8_t* sa = smem + base_a + a_row + off;
+    const int8_t* sb = smem + base_b + b_row + off;
     auto rd = [](const int8_t* base, int i) { return *reinterpret_cast<const v4i*>(base + i * 32 * kSK); };
     if constexpr (NB == 4) {
       if (k == 0) {
@@ -1008,19 +1015,45 @@ void gemm_i8_persistent(GemmParams p) {
   // c = 2g mod 5). During it the second half of unit 2g + 3 and unit 2g + 4
   // are issued (slots c + 3, c + 4, freed by stage g - 1); its end releases
   // slots c, c + 1, and the first half of unit 2g + 5 goes to slot c.
-  issue_half(A_{}, H0{}, 0);
-  issue_half(A_{}, H1{}, 0);
-  issue_half(B_{}, H0{}, 1);
-  issue_half(B_{}, H1{}, 1);
-  issue_half(A_{}, H0{}, 2);
-  issue_half(A_{}, H1{}, 2);
-  issue_half(B_{}, H0{}, 3);
-  wait_vmcnt<NA + JB / 2>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
+  //
+  // 128 x 256 tiles (NB = 2) take a ring of three whole stages instead
+  // (STAGE_RING): stage slot s holds the A tile (16 KB) at 48 KB s and the
+  // B tile (32 KB) after it. Stage g computes from slot g mod 3 while stage
+  // g + 1 (issued during stage g - 1) lands and stage g + 2 is issued into
+  // the slot stage g - 1 released: two stages (96 KB) in flight, where the
+  // five half-stage slots keep about one (their A slots half empty).
+  constexpr bool STAGE_RING = NB == 2;
+  constexpr int kStage2 = (BM + BN) * kSK, kA2 = BM * kSK;
+  static_assert(!STAGE_RING || 3 * kStage2 <= kPersistentLds, "three stages fit the LDS");
+  auto next_slot = [](int slot) { return slot == (STAGE_RING ? 2 : kSlots - 1) ? 0 : slot + 1; };
+  // Byte offsets of the A and B tiles of the stage in slot s (STAGE_RING),
+  // or whose A tile is in slot s (its B tile in the next slot).
+  auto a_of = [&](int s) { return STAGE_RING ? s * kStage2 : s * kSTile; };
+  auto b_of = [&](int s) { return STAGE_RING ? s * kStage2 + kA2 : next_slot(s) * kSTile; };
+  if constexpr (STAGE_RING) {
+    issue_half(A_{}, H0{}, a_of(0));
+    issue_half(A_{}, H1{}, a_of(0));
+    issue_half(B_{}, H0{}, b_of(0));
+    issue_half(B_{}, H1{}, b_of(0));
+    issue_half(A_{}, H0{}, a_of(1));
+    issue_half(A_{}, H1{}, a_of(1));
+    issue_half(B_{}, H0{}, b_of(1));
+    issue_half(B_{}, H1{}, b_of(1));
+    wait_vmcnt<NA + JB>();  // stage 0 landed (stage 1 in flight)
+  } else {
+    issue_half(A_{}, H0{}, 0);
+    issue_half(A_{}, H1{}, 0);
+    issue_half(B_{}, H0{}, kSTile);
+    issue_half(B_{}, H1{}, kSTile);
+    issue_half(A_{}, H0{}, 2 * kSTile);
+    issue_half(A_{}, H1{}, 2 * kSTile);
+    issue_half(B_{}, H0{}, 3 * kSTile);
+    wait_vmcnt<NA + JB / 2>();  // stage 0 landed (unit 2 and half of unit 3 in flight)
+  }
   block_barrier();
   v4i fa0[NB], fb0[4], fa1[NB], fb1[4];
-  read_frags(0, 1, 0, fa0, fb0);
-  auto next_slot = [](int slot) { return slot == kSlots - 1 ? 0 : slot + 1; };
-  int cur_a = 0;   // slot of the current stage's A tile; its B tile is the next slot
+  read_frags(a_of(0), b_of(0), 0, fa0, fb0);
+  int cur_a = 0;   // slot of the current stage (STAGE_RING) or of its A tile
   for (int i = 0; i < ntiles; ++i) {
     const int item = item_of(i);
     int tm, tn;
@@ -1054,14 +1087,14 @@ void gemm_i8_persistent(GemmParams p) {
     const int nks = ks_end(item) - ks_begin(item);   // >= 1
     // One stage: 16 NB MFMAs, 4 (NB + 4) fragment reads and NA + JB DMA
     // instructions.
-    int stg = 0;   // the last stage's B slot: the epilogue's staging area
+    int stg = 0;   // byte offset of the last stage's B tile: the epilogue's staging area
     int ks = 0;
     // A sub-step in fixed order: each MFMA row of the current fragments but
     // the last is followed by one group of the next sub-step's fragment
     // reads, and every row by its part of the half-unit of DMA
     // (sched_barrier keeps the compiler from regrouping them).
     auto substep = [&](const v4i (&ca)[NB], const v4i (&cb)[4], int ra, int rb, int u, v4i (&na)[NB],
-                       v4i (&nb)[4], auto b_tag, auto h_tag, int dslot) {
+                       v4i (&nb)[4], auto b_tag, auto h_tag, int dbase) {
       static_for<0, NB>([&](auto r_tag) {
         constexpr int R = decltype(r_tag)::value;
         mfma_row(R, ca, cb);
@@ -1070,7 +1103,7 @@ void gemm_i8_persistent(GemmParams p) {
           __builtin_amdgcn_sched_barrier(0);
           read_group(ra, rb, u, R, na, nb);
         }
-        dma_part(b_tag, h_tag, r_tag, dslot);
+        dma_part(b_tag, h_tag, r_tag, dbase);
         __builtin_amdgcn_sched_barrier(0);
       });
     };
@@ -1078,39 +1111,68 @@ void gemm_i8_persistent(GemmParams p) {
       // At a tile's last stage the next tile's first fragments are read
       // after the epilogue, so they do not hold registers through it.
       const bool last = ks + 1 == nks;
-      const int cur_b = next_slot(cur_a);
-      const int nxt_a = next_slot(cur_b), nxt_b = next_slot(nxt_a), fill = next_slot(nxt_b);
-      substep(fa0, fb0, cur_a, cur_b, 1, fa1, fb1, B_{}, H1{}, nxt_b);
-      substep(fa1, fb1, cur_a, cur_b, 2, fa0, fb0, A_{}, H0{}, fill);
-      substep(fa0, fb0, cur_a, cur_b, 3, fa1, fb1, A_{}, H1{}, fill);
-      // The first MFMA row of the last sub-step consumes its fragments, so
-      // past it this wave is done reading the stage's slots.
-      mfma_row(0, fa1, fb1);
-      __builtin_amdgcn_sched_barrier(0);
-      // The next stage (units 2g + 2, 2g + 3) landed - only unit 2g + 4,
-      // issued after them, may still be in flight - and this wave's reads of
-      // this stage returned;
-      wait_vm_lgkm<NA>();
-      block_barrier();   // ... for every wave: both slots are released.
-      static_for<0, NB>([&](auto r_tag) {
-        constexpr int R = decltype(r_tag)::value;
-        if constexpr (R > 0) {
-          mfma_row(R, fa1, fb1);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (R + 1 < NB) {
-          if (!last) read_group(nxt_a, nxt_b, 0, R, fa0, fb0);
-        }
-        dma_part(B_{}, H0{}, r_tag, cur_a);
+      if constexpr (STAGE_RING) {
+        // Stage g + 2 goes to the slot stage g - 1 released: its A tile
+        // during sub-steps 0 and 1, its B tile during 2 and 3.
+        using R0 = std::integral_constant<int, 0>;
+        using R1 = std::integral_constant<int, 1>;
+        const int nxt = next_slot(cur_a), fill = next_slot(nxt);
+        const int ca = a_of(cur_a), cb = b_of(cur_a);
+        substep(fa0, fb0, ca, cb, 1, fa1, fb1, A_{}, H0{}, a_of(fill));
+        substep(fa1, fb1, ca, cb, 2, fa0, fb0, A_{}, H1{}, a_of(fill));
+        substep(fa0, fb0, ca, cb, 3, fa1, fb1, B_{}, H0{}, b_of(fill));
+        mfma_row(0, fa1, fb1);
         __builtin_amdgcn_sched_barrier(0);
-      });
-      stg = cur_b;
-      cur_a = nxt_a;
+        dma_part(B_{}, H1{}, R0{}, b_of(fill));
+        __builtin_amdgcn_sched_barrier(0);
+        // Stage g + 1 landed - only the NA + 3 JB / 4 instructions of stage
+        // g + 2 issued so far are younger - and this wave's reads of stage g
+        // returned; the barrier releases slot g mod 3 for stage g + 3.
+        wait_vm_lgkm<NA + 3 * JB / 4>();
+        block_barrier();
+        if (!last) read_group(a_of(nxt), b_of(nxt), 0, 0, fa0, fb0);
+        dma_part(B_{}, H1{}, R1{}, b_of(fill));
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_row(1, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        stg = cb;
+        cur_a = nxt;
+      } else {
+        const int cur_b = next_slot(cur_a);
+        const int nxt_a = next_slot(cur_b), nxt_b = next_slot(nxt_a), fill = next_slot(nxt_b);
+        substep(fa0, fb0, a_of(cur_a), a_of(cur_b), 1, fa1, fb1, B_{}, H1{}, a_of(nxt_b));
+        substep(fa1, fb1, a_of(cur_a), a_of(cur_b), 2, fa0, fb0, A_{}, H0{}, a_of(fill));
+        substep(fa0, fb0, a_of(cur_a), a_of(cur_b), 3, fa1, fb1, A_{}, H1{}, a_of(fill));
+        // The first MFMA row of the last sub-step consumes its fragments, so
+        // past it this wave is done reading the stage's slots.
+        mfma_row(0, fa1, fb1);
+        __builtin_amdgcn_sched_barrier(0);
+        // The next stage (units 2g + 2, 2g + 3) landed - only unit 2g + 4,
+        // issued after them, may still be in flight - and this wave's reads of
+        // this stage returned;
+        wait_vm_lgkm<NA>();
+        block_barrier();   // ... for every wave: both slots are released.
+        static_for<0, NB>([&](auto r_tag) {
+          constexpr int R = decltype(r_tag)::value;
+          if constexpr (R > 0) {
+            mfma_row(R, fa1, fb1);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          if constexpr (R + 1 < NB) {
+            if (!last) read_group(a_of(nxt_a), a_of(nxt_b), 0, R, fa0, fb0);
+          }
+          dma_part(B_{}, H0{}, r_tag, a_of(cur_a));
+          __builtin_amdgcn_sched_barrier(0);
+        });
+        stg = a_of(cur_b);
+        cur_a = nxt_a;
+      }
     } while (++ks < nks);
-    // The tile's scale and bias loads have landed: at most unit 2g + 4 and
-    // the first half of unit 2g + 5 are younger and in flight. (The
-    // epilogue's residual loads queue behind those NA + JB / 2 instructions.)
-    wait_vmcnt<NA + JB / 2>();
+    // The tile's scale and bias loads have landed: they are older than the
+    // DMA still in flight (half-stage slots: at most unit 2g + 4 and the
+    // first half of unit 2g + 5; STAGE_RING: stage g + 2). (The epilogue's
+    // residual loads queue behind those instructions.)
+    wait_vmcnt<STAGE_RING ? NA + JB : NA + JB / 2>();
     float bsc[2][8];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -1119,7 +1181,7 @@ void gemm_i8_persistent(GemmParams p) {
         bsc[h][j] = (FLAGS & kWithBias) == 0       ? 0.0f
                     : p.bias_dtype == kF16 ? h2f((uint16_t)braw[h][j])
                                            : __builtin_bit_cast(float, braw[h][j]);
-    int8_t* const stage_w = smem + stg * kSTile + wave * 8192;
+    int8_t* const stage_w = smem + stg + wave * 8192;
     const int64_t out_off = (item % ksplit) * p.split_stride;
     // Interior quadrants take a copy without store masks (not for the gate
     // variants, whose registers a second copy would push into spills).
@@ -1143,13 +1205,14 @@ void gemm_i8_persistent(GemmParams p) {
     else
       store_quadrant32_passes<EPI, OUT, FLAGS, false, NB>(p, acc, wsc, bsc, as, lbl, mw, nw, lane, stage_w,
                                                           out_off);
-    // The staging slot's next unit (2g + 6) is issued during the next
-    // stage; a wave's DMA into a slot writes the same 8 KB it used for
-    // staging, so its own staging reads returning is all that unit waits for.
+    // The staging slot's next unit (2g + 6; STAGE_RING: the B tile of stage
+    // g + 3) is issued during the next stage; a wave's DMA into a slot
+    // writes the same 8 KB it used for staging, so its own staging reads
+    // returning is all that unit waits for.
     wait_lgkm();
     // The next tile's first fragments (its stage 0 landed before the last
-    // barrier, in the slots cur_a and the one after).
-    static_for<0, NB - 1>([&](auto k) { read_group(cur_a, next_slot(cur_a), 0, decltype(k)::value, fa0, fb0); });
+    // barrier).
+    static_for<0, NB - 1>([&](auto k) { read_group(a_of(cur_a), b_of(cur_a), 0, decltype(k)::value, fa0, fb0); });
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 }

@@ -550,6 +550,19 @@ def test_swiglu_quantize(gpu, rows, width):
     assert_bits_equal(np_of(res['q']), wq, f'codes {rows}x{width}')
 
 
+@pytest.mark.parametrize('rows,width,ld', [(300, 2048, 4608), (300, 4096, 16384), (7, 8192, 16896)])
+def test_swiglu_quantize_row_stride(gpu, rows, width, ld):
+    """Rows read from a wider buffer (row stride ld > 2W), as the FFN
+    prologue reads a column slice of a larger FC1 output."""
+    g = torch.Generator().manual_seed(rows * 3 + width)
+    big = randn16(g, (rows, ld), 2.0)
+    res = kernels.swiglu_quantize(big.to(gpu)[:, 256:256 + 2 * width], want_group_max=True)
+    wq, ws, wg = o.fc2_prologue(np_of(big[:, 256:256 + 2 * width].contiguous()))
+    assert_bits_equal(np_of(res['group_max']), wg, f'group max {rows}x{width} ld {ld}')
+    assert_bits_equal(np_of(res['scale']).reshape(-1), ws, 'scale')
+    assert_bits_equal(np_of(res['q']), wq, f'codes {rows}x{width} ld {ld}')
+
+
 def test_swiglu_external_max_fp32_input_and_phases(gpu):
     g = torch.Generator().manual_seed(77)
     x = randn16(g, (9, 2 * 1024), 2.0, torch.float32)
