@@ -324,6 +324,28 @@ def test_gemm_more_tiles_than_cus(gpu, k):
     assert_bits_equal(np_of(got), o.int_mm(np_of(a), np_of(b)), f'gemm {m}x{n}x{k}')
 
 
+@pytest.mark.parametrize('m,n,k', [(100, 70000, 128), (100, 70000, 384), (65, 66000, 640)])
+def test_gemm_128_row_tiles_more_than_cus(gpu, m, n, k):
+    # M <= 128 rows takes 128 x 256 tiles; past 65536 columns there are more
+    # tiles than CUs (274 and 258), so a workgroup runs several tiles and the
+    # three-stage operand ring crosses tile boundaries after 1, 3 or 5 K
+    # steps, with the epilogue staging through a ring slot in between.
+    print(f'128-row tiles {m}x{n}x{k}', flush=True)
+    g = torch.Generator().manual_seed(m + k)
+    a = randi8(g, (m, k))
+    b = randi8(g, (n, k))
+    rs = torch.rand((m, 1), generator=g) * 0.01 + 1e-4
+    ws = (torch.rand((n, 1), generator=g) * 1e-3 + 1e-6) / 512
+    res = randn16(g, (m, n), 1 / 512)
+    acc = o.int_mm(np_of(a), np_of(b))
+    ag, bg = a.to(gpu), b.to(gpu)
+    assert_bits_equal(np_of(kernels.gemm(ag, bg)), acc, 'int32')
+    got = kernels.gemm(ag, bg, epilogue=kernels.EPI_ROW, row_scale=rs.to(gpu), col_scale=ws.to(gpu),
+                       residual=res.to(gpu), out_dtype=torch.float16)
+    want = o.residual_add(np_of(res), o.dequantize_row(acc, np_of(rs), np_of(ws), 'f16'))
+    assert_bits_equal(np_of(got), want, 'row + residual')
+
+
 @pytest.mark.parametrize('epi,out_dtype,bias_dtype,residual', [
     ('column', torch.float16, torch.float16, False), ('row', torch.float16, None, True),
     ('row', torch.float32, torch.float32, False), ('column', torch.bfloat16, None, False),
