@@ -88,7 +88,7 @@ def test_noalloc_gemm_runs_unsplit_what_it_cannot_hold(gpu):
 
 
 def test_noalloc_split_gemm_replays_in_a_graph(gpu):
-    m, n, k = 512, 4096, 14336       # 128 x 256 tiles, K split four ways, finished in the kernel
+    m, n, k = 512, 4096, 14336       # 128 x 256 tiles, K split four ways, partials added by a second kernel
     assert 0 < kernels.gemm_workspace_bytes(m, n, k, gpu) <= _abi.GEMM_SCRATCH_BYTES
     g = torch.Generator().manual_seed(10)
     q = randi8(g, (m, k)).to(gpu)
